@@ -1,0 +1,203 @@
+// Dequant-matvec kernels for small token counts (decode): y[t, n] = sum_k W[n, k] x[t, k].
+//
+// Launch shape: 256 threads (4 wave64s) per workgroup, ROWS_PER_WG output rows per
+// workgroup, up to TCH tokens per launch column (grid.y walks token chunks). The
+// activations of the chunk are staged once into LDS as float32; each wave owns whole
+// rows and its 64 lanes stride over the row's 32-value units (GGUF) or 16-byte groups
+// (MXFP4), so a wave's loads of one row are contiguous. Lanes reduce with a wave sum.
+#include "rowdot.h"
+
+namespace tsa {
+namespace {
+
+constexpr int ROWS_PER_WG = 8;
+constexpr int MAX_X_LDS_BYTES = 64 * 1024;
+
+template <int TCH>
+__device__ __forceinline__ int stage_x(float* xs, const void* x, int x_dtype, int64_t t0, int64_t T, int64_t K) {
+    const int tn = (int)((T - t0) < TCH ? (T - t0) : TCH);
+    for (int64_t i = threadIdx.x; i < (int64_t)TCH * K; i += blockDim.x) {
+        const int64_t t = i / K;
+        xs[i] = t < tn ? load_act(x, x_dtype, (t0 + t) * K + (i - t * K)) : 0.0f;
+    }
+    __syncthreads();
+    return tn;
+}
+
+template <int TYPE, int A, int TCH>
+__global__ void __launch_bounds__(256) gguf_matvec_kernel(const uint8_t* __restrict__ w, const void* __restrict__ x,
+                                                          int x_dtype, int64_t T, int64_t K, void* __restrict__ y,
+                                                          int y_dtype, int64_t N) {
+    using Tr = GgufTraits<TYPE>;
+    extern __shared__ float xs[];
+    const int64_t t0 = (int64_t)blockIdx.y * TCH;
+    const int tn = stage_x<TCH>(xs, x, x_dtype, t0, T, K);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t upr = K / 32;
+    for (int r = wave; r < ROWS_PER_WG; r += 4) {
+        const int64_t n = (int64_t)blockIdx.x * ROWS_PER_WG + r;
+        if (n >= N) break;
+        float acc[TCH];
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) acc[t] = 0.0f;
+        for (int64_t j = lane; j < upr; j += 64) {
+            const int64_t U = n * upr + j;
+            float v[32];
+            decode_unit<TYPE, A>(w + (U / Tr::UPB) * Tr::TS, (int)(U % Tr::UPB), v);
+#pragma unroll
+            for (int t = 0; t < TCH; ++t) {
+                const float4* xv = reinterpret_cast<const float4*>(xs + t * K + 32 * j);
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 q = xv[i];
+                    a += v[4 * i] * q.x + v[4 * i + 1] * q.y + v[4 * i + 2] * q.z + v[4 * i + 3] * q.w;
+                }
+                acc[t] += a;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) {
+            const float s = wave_sum(acc[t]);
+            if (lane == 0 && t < tn) store_out(y, y_dtype, (t0 + t) * N + n, s);
+        }
+    }
+}
+
+template <int A, int TCH>
+__global__ void __launch_bounds__(256) mxfp4_matvec_kernel(const uint8_t* __restrict__ blocks,
+                                                           const uint8_t* __restrict__ scales,
+                                                           const void* __restrict__ bias, int bias_dtype,
+                                                           const void* __restrict__ x, int x_dtype, int64_t T,
+                                                           void* __restrict__ y, int y_dtype, int64_t N, int64_t K) {
+    extern __shared__ float xs[];
+    const int64_t t0 = (int64_t)blockIdx.y * TCH;
+    const int tn = stage_x<TCH>(xs, x, x_dtype, t0, T, K);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t G = K / 32;
+    for (int r = wave; r < ROWS_PER_WG; r += 4) {
+        const int64_t n = (int64_t)blockIdx.x * ROWS_PER_WG + r;
+        if (n >= N) break;
+        float acc[TCH];
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) acc[t] = 0.0f;
+        for (int64_t g = lane; g < G; g += 64) {
+            const int64_t c = n * G + g;
+            uint32_t q[4];
+            if constexpr (A >= 16) {
+                const uint4 v = reinterpret_cast<const uint4*>(blocks)[c];
+                q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+            } else {
+                __builtin_memcpy(q, blocks + 16 * c, 16);
+            }
+            const float s = e8m0_to_f32(scales[c]);
+#pragma unroll
+            for (int t = 0; t < TCH; ++t) acc[t] += mx16_dot(q, xs + t * K + 32 * g) * s;
+        }
+        const float b = bias ? load_act(bias, bias_dtype, n) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) {
+            const float s = wave_sum(acc[t]);
+            if (lane == 0 && t < tn) store_out(y, y_dtype, (t0 + t) * N + n, s + b);
+        }
+    }
+}
+
+template <int TYPE, int A>
+hipError_t launch_gguf(const uint8_t* w, const void* x, int x_dtype, int64_t T, int64_t K, void* y, int y_dtype,
+                       int64_t N, int tch, hipStream_t st) {
+    const dim3 block(256), grid((unsigned)((N + ROWS_PER_WG - 1) / ROWS_PER_WG), (unsigned)((T + tch - 1) / tch));
+    const size_t lds = (size_t)tch * K * sizeof(float);
+    switch (tch) {
+        case 4: hipLaunchKernelGGL((gguf_matvec_kernel<TYPE, A, 4>), grid, block, lds, st, w, x, x_dtype, T, K, y, y_dtype, N); break;
+        case 2: hipLaunchKernelGGL((gguf_matvec_kernel<TYPE, A, 2>), grid, block, lds, st, w, x, x_dtype, T, K, y, y_dtype, N); break;
+        default: hipLaunchKernelGGL((gguf_matvec_kernel<TYPE, A, 1>), grid, block, lds, st, w, x, x_dtype, T, K, y, y_dtype, N); break;
+    }
+    return hipGetLastError();
+}
+
+template <int A>
+hipError_t launch_mx(const uint8_t* bl, const uint8_t* sc, const void* bias, int bias_dtype, const void* x, int x_dtype,
+                     int64_t T, void* y, int y_dtype, int64_t N, int64_t K, int tch, hipStream_t st) {
+    const dim3 block(256), grid((unsigned)((N + ROWS_PER_WG - 1) / ROWS_PER_WG), (unsigned)((T + tch - 1) / tch));
+    const size_t lds = (size_t)tch * K * sizeof(float);
+    switch (tch) {
+        case 4: hipLaunchKernelGGL((mxfp4_matvec_kernel<A, 4>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+        case 2: hipLaunchKernelGGL((mxfp4_matvec_kernel<A, 2>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+        default: hipLaunchKernelGGL((mxfp4_matvec_kernel<A, 1>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+    }
+    return hipGetLastError();
+}
+
+int pick_tch(int64_t T, int64_t K) {
+    int tch = T >= 4 ? 4 : (T >= 2 ? 2 : 1);
+    while (tch > 1 && (int64_t)tch * K * 4 > MAX_X_LDS_BYTES) tch >>= 1;
+    return tch;
+}
+
+}  // namespace
+}  // namespace tsa
+
+using namespace tsa;
+
+extern "C" int tsa_gguf_matvec(int ggml_type, const void* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T,
+                               int64_t K, void* y, int y_dtype, int64_t N, void* stream) {
+    clear_error();
+    int be, ts;
+    TSA_REQUIRE(gguf_geometry(ggml_type, &be, &ts), TSA_ERR_UNSUPPORTED_TYPE,
+                "Unsupported ggml_type: %d. Supported: Q8_0(8), Q4_K(12), Q5_K(13), Q6_K(14)", ggml_type);
+    TSA_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype), TSA_ERR_INVALID_ARG, "bad dtype (x %d, y %d)", x_dtype,
+                y_dtype);
+    TSA_REQUIRE(N >= 0 && K >= 0 && T >= 0, TSA_ERR_INVALID_ARG, "negative size");
+    TSA_REQUIRE(K % 32 == 0, TSA_ERR_SHAPE, "in_features (%lld) must be divisible by block_elements (32)", (long long)K);
+    TSA_REQUIRE((N * K) % be == 0, TSA_ERR_SHAPE,
+                "out_features*in_features (%lld) must be a whole number of blocks (%d values each)",
+                (long long)(N * K), be);
+    const int64_t expected = N * K / be * ts;
+    TSA_REQUIRE(w_bytes >= expected, TSA_ERR_WEIGHT_TOO_SMALL, "weight_data too small: got %lld bytes, expected %lld",
+                (long long)w_bytes, (long long)expected);
+    TSA_REQUIRE(K * 4 <= MAX_X_LDS_BYTES, TSA_ERR_SHAPE, "in_features (%lld) exceeds the supported maximum (%d)",
+                (long long)K, MAX_X_LDS_BYTES / 4);
+    if (N == 0 || T == 0) return TSA_OK;
+    TSA_REQUIRE(w && x && y, TSA_ERR_INVALID_ARG, "null pointer");
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const bool a16 = (reinterpret_cast<uintptr_t>(w) & 15) == 0, a2 = (reinterpret_cast<uintptr_t>(w) & 1) == 0;
+    const int tch = pick_tch(T, K);
+    hipStream_t st = as_stream(stream);
+    hipError_t e;
+    switch (ggml_type) {
+        case 8: e = a2 ? launch_gguf<8, 2>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st)
+                       : launch_gguf<8, 1>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st); break;
+        case 12: e = a16 ? launch_gguf<12, 16>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st)
+                         : launch_gguf<12, 1>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st); break;
+        case 13: e = a16 ? launch_gguf<13, 16>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st)
+                         : launch_gguf<13, 1>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st); break;
+        default: e = a2 ? launch_gguf<14, 2>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st)
+                        : launch_gguf<14, 1>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st); break;
+    }
+    TSA_HIP_CHECK(e);
+    return TSA_OK;
+}
+
+extern "C" int tsa_mxfp4_matvec(const void* blocks, const void* scales, const void* bias, int bias_dtype,
+                                const void* x, int x_dtype, int64_t T, void* y, int y_dtype, int64_t N, int64_t K,
+                                void* stream) {
+    clear_error();
+    TSA_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype) && (!bias || valid_dtype(bias_dtype)),
+                TSA_ERR_INVALID_ARG, "bad dtype (x %d, y %d, bias %d)", x_dtype, y_dtype, bias_dtype);
+    TSA_REQUIRE(N >= 0 && K >= 0 && T >= 0, TSA_ERR_INVALID_ARG, "negative size");
+    TSA_REQUIRE(K % 32 == 0, TSA_ERR_SHAPE, "in_features (%lld) must be a multiple of 32", (long long)K);
+    TSA_REQUIRE(K * 4 <= MAX_X_LDS_BYTES, TSA_ERR_SHAPE, "in_features (%lld) exceeds the supported maximum (%d)",
+                (long long)K, MAX_X_LDS_BYTES / 4);
+    if (N == 0 || T == 0) return TSA_OK;
+    TSA_REQUIRE(blocks && scales && x && y, TSA_ERR_INVALID_ARG, "null pointer");
+    const uint8_t* bl = static_cast<const uint8_t*>(blocks);
+    const uint8_t* sc = static_cast<const uint8_t*>(scales);
+    const int tch = pick_tch(T, K);
+    hipStream_t st = as_stream(stream);
+    hipError_t e = (reinterpret_cast<uintptr_t>(blocks) & 15) == 0
+                       ? launch_mx<16>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st)
+                       : launch_mx<1>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
+    TSA_HIP_CHECK(e);
+    return TSA_OK;
+}

@@ -1,0 +1,317 @@
+// Fused top-k MoE decode over resident packed expert slots.
+//
+// Phase A (one launch for every (token, j) assignment and every block of the
+// intermediate dimension): gate/up rows of the selected expert -> activation
+// (GPT-OSS clamped SwiGLU or SiLU-gated) -> h[t, j, :] (float32, workspace).
+// Phase B (one launch over tokens x output rows): each workgroup owns a block of
+// output rows for one token and sums w[t, j] * (W_down[slot_j] h[t, j] + b_down)
+// over j in registers, so every output element has exactly one writer (no atomics,
+// deterministic order). Slots < 0 (or >= n_slots) contribute nothing.
+//
+// Semantics: tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases),
+// tinyserve/ggml_forward.py:88-115 (GGUF expert), tinyserve/csrc/expert_loop.cpp:83-121
+// (weighted top-k accumulation).
+#include "rowdot.h"
+
+namespace tsa {
+namespace {
+
+constexpr int H_PER_WG = 8;     // phase A: intermediate outputs per workgroup (2 per wave)
+constexpr int ROWS_B_PER_WG = 8;  // phase B: output rows per workgroup (2 per wave)
+
+__device__ __forceinline__ float activate(const tsa_expert_layout& L, float gate, float up) {
+    if (L.act == TSA_ACT_SWIGLU_OAI) {
+        const float g = fminf(gate, L.swiglu_limit);
+        const float u = fminf(fmaxf(up, -L.swiglu_limit), L.swiglu_limit);
+        return (u + 1.0f) * g * sigmoidf_(L.swiglu_alpha * g);
+    }
+    return gate * sigmoidf_(gate) * up;
+}
+
+__device__ __forceinline__ const uint8_t* slot_ptr(const uint8_t* pool, const tsa_expert_layout& L, int64_t slot) {
+    return pool + slot * L.slot_bytes;
+}
+
+__device__ __forceinline__ void stage(float* xs, const void* x, int dt, int64_t off, int64_t n) {
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) xs[i] = load_act(x, dt, off + i);
+}
+
+// ---------------------------------------------------------------- MXFP4
+template <int A>
+__global__ void __launch_bounds__(256) mx_phase_a(tsa_expert_layout L, const uint8_t* __restrict__ pool,
+                                                  int64_t n_slots, const int32_t* __restrict__ slots, int k,
+                                                  const void* __restrict__ x, int x_dtype, float* __restrict__ h) {
+    extern __shared__ float xs[];
+    const int64_t a = blockIdx.y;  // assignment t*k + j
+    const int64_t slot = slots[a];
+    if (slot < 0 || slot >= n_slots) return;
+    const int64_t H = L.hidden, I = L.inter, t = a / k;
+    stage(xs, x, x_dtype, t * H, H);
+    __syncthreads();
+    const uint8_t* base = slot_ptr(pool, L, slot);
+    const uint8_t* bl = base + L.gate_off;
+    const uint8_t* sc = base + L.gate_scales_off;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t G = H / 32;
+    for (int r = wave; r < H_PER_WG; r += 4) {
+        const int64_t i = (int64_t)blockIdx.x * H_PER_WG + r;
+        if (i >= I) break;
+        float pg = mx_row_partial<A>(bl, sc, 2 * i, G, xs, lane);
+        float pu = mx_row_partial<A>(bl, sc, 2 * i + 1, G, xs, lane);
+        pg = wave_sum(pg);
+        pu = wave_sum(pu);
+        if (lane == 0) {
+            if (L.gate_bias_off >= 0) {
+                pg += load_act(base + L.gate_bias_off, L.bias_dtype, 2 * i);
+                pu += load_act(base + L.gate_bias_off, L.bias_dtype, 2 * i + 1);
+            }
+            h[a * I + i] = activate(L, pg, pu);
+        }
+    }
+}
+
+template <int A>
+__global__ void __launch_bounds__(256) mx_phase_b(tsa_expert_layout L, const uint8_t* __restrict__ pool,
+                                                  int64_t n_slots, const int32_t* __restrict__ slots,
+                                                  const float* __restrict__ wts, int k, const float* __restrict__ h,
+                                                  void* __restrict__ y, int y_dtype) {
+    extern __shared__ float hs[];
+    const int64_t t = blockIdx.y, H = L.hidden, I = L.inter, G = I / 32;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float acc[ROWS_B_PER_WG / 4] = {};
+    for (int j = 0; j < k; ++j) {
+        const int64_t a = t * k + j, slot = slots[a];
+        if (slot < 0 || slot >= n_slots) continue;  // uniform across the workgroup
+        const float wj = wts[a];
+        __syncthreads();
+        stage(hs, h, TSA_F32, a * I, I);
+        __syncthreads();
+        const uint8_t* base = slot_ptr(pool, L, slot);
+#pragma unroll
+        for (int rr = 0; rr < ROWS_B_PER_WG / 4; ++rr) {
+            const int64_t n = (int64_t)blockIdx.x * ROWS_B_PER_WG + wave + 4 * rr;
+            if (n >= H) break;
+            float p = wave_sum(mx_row_partial<A>(base + L.down_off, base + L.down_scales_off, n, G, hs, lane));
+            if (L.down_bias_off >= 0) p += load_act(base + L.down_bias_off, L.bias_dtype, n);
+            acc[rr] += wj * p;
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < ROWS_B_PER_WG / 4; ++rr) {
+        const int64_t n = (int64_t)blockIdx.x * ROWS_B_PER_WG + wave + 4 * rr;
+        if (n < H && lane == 0) store_out(y, y_dtype, t * H + n, acc[rr]);
+    }
+}
+
+// ---------------------------------------------------------------- GGUF
+template <int TG, int AG>
+__global__ void __launch_bounds__(256) gguf_phase_a(tsa_expert_layout L, const uint8_t* __restrict__ pool,
+                                                    int64_t n_slots, const int32_t* __restrict__ slots, int k,
+                                                    const void* __restrict__ x, int x_dtype, float* __restrict__ h) {
+    extern __shared__ float xs[];
+    const int64_t a = blockIdx.y;
+    const int64_t slot = slots[a];
+    if (slot < 0 || slot >= n_slots) return;
+    const int64_t H = L.hidden, I = L.inter, t = a / k;
+    stage(xs, x, x_dtype, t * H, H);
+    __syncthreads();
+    const uint8_t* base = slot_ptr(pool, L, slot);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int r = wave; r < H_PER_WG; r += 4) {
+        const int64_t i = (int64_t)blockIdx.x * H_PER_WG + r;
+        if (i >= I) break;
+        const float pg = wave_sum(gguf_row_partial<TG, AG>(base + L.gate_off, i, H, xs, lane));
+        const float pu = wave_sum(gguf_row_partial<TG, AG>(base + L.up_off, i, H, xs, lane));
+        if (lane == 0) h[a * I + i] = activate(L, pg, pu);
+    }
+}
+
+template <int TD, int AD>
+__global__ void __launch_bounds__(256) gguf_phase_b(tsa_expert_layout L, const uint8_t* __restrict__ pool,
+                                                    int64_t n_slots, const int32_t* __restrict__ slots,
+                                                    const float* __restrict__ wts, int k, const float* __restrict__ h,
+                                                    void* __restrict__ y, int y_dtype) {
+    extern __shared__ float hs[];
+    const int64_t t = blockIdx.y, H = L.hidden, I = L.inter;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float acc[ROWS_B_PER_WG / 4] = {};
+    for (int j = 0; j < k; ++j) {
+        const int64_t a = t * k + j, slot = slots[a];
+        if (slot < 0 || slot >= n_slots) continue;
+        const float wj = wts[a];
+        __syncthreads();
+        stage(hs, h, TSA_F32, a * I, I);
+        __syncthreads();
+        const uint8_t* base = slot_ptr(pool, L, slot);
+#pragma unroll
+        for (int rr = 0; rr < ROWS_B_PER_WG / 4; ++rr) {
+            const int64_t n = (int64_t)blockIdx.x * ROWS_B_PER_WG + wave + 4 * rr;
+            if (n >= H) break;
+            acc[rr] += wj * wave_sum(gguf_row_partial<TD, AD>(base + L.down_off, n, I, hs, lane));
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < ROWS_B_PER_WG / 4; ++rr) {
+        const int64_t n = (int64_t)blockIdx.x * ROWS_B_PER_WG + wave + 4 * rr;
+        if (n < H && lane == 0) store_out(y, y_dtype, t * H + n, acc[rr]);
+    }
+}
+
+// ---------------------------------------------------------------- host side
+struct Launch {
+    dim3 ga, gb;
+    size_t lds_a, lds_b;
+};
+
+Launch shapes(const tsa_expert_layout& L, int64_t T, int k) {
+    Launch s;
+    s.ga = dim3((unsigned)((L.inter + H_PER_WG - 1) / H_PER_WG), (unsigned)(T * k));
+    s.gb = dim3((unsigned)((L.hidden + ROWS_B_PER_WG - 1) / ROWS_B_PER_WG), (unsigned)T);
+    s.lds_a = (size_t)L.hidden * 4;
+    s.lds_b = (size_t)L.inter * 4;
+    return s;
+}
+
+template <int TG, int AG>
+hipError_t launch_gguf_a(const Launch& s, const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
+                         const int32_t* slots, int k, const void* x, int xdt, float* h, hipStream_t st) {
+    hipLaunchKernelGGL((gguf_phase_a<TG, AG>), s.ga, dim3(256), s.lds_a, st, L, pool, n_slots, slots, k, x, xdt, h);
+    return hipGetLastError();
+}
+
+template <int TD, int AD>
+hipError_t launch_gguf_b(const Launch& s, const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
+                         const int32_t* slots, const float* w, int k, const float* h, void* y, int ydt, hipStream_t st) {
+    hipLaunchKernelGGL((gguf_phase_b<TD, AD>), s.gb, dim3(256), s.lds_b, st, L, pool, n_slots, slots, w, k, h, y, ydt);
+    return hipGetLastError();
+}
+
+int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) { return ((T * k * L.inter * 4) + 255) / 256 * 256; }
+
+}  // namespace
+
+int validate_layout(const tsa_expert_layout* L) {
+    TSA_REQUIRE(L != nullptr, TSA_ERR_INVALID_ARG, "layout is null");
+    TSA_REQUIRE(L->format == TSA_EXPERT_MXFP4 || L->format == TSA_EXPERT_GGUF, TSA_ERR_INVALID_ARG,
+                "layout.format %d is not MXFP4(1) or GGUF(2)", L->format);
+    TSA_REQUIRE(L->act == TSA_ACT_SILU || L->act == TSA_ACT_SWIGLU_OAI, TSA_ERR_INVALID_ARG, "layout.act %d unknown",
+                L->act);
+    TSA_REQUIRE(L->hidden > 0 && L->inter > 0 && L->slot_bytes > 0, TSA_ERR_SHAPE, "layout sizes must be positive");
+    TSA_REQUIRE(L->hidden % 32 == 0 && L->inter % 32 == 0, TSA_ERR_SHAPE,
+                "hidden (%lld) and intermediate (%lld) sizes must be multiples of 32", (long long)L->hidden,
+                (long long)L->inter);
+    TSA_REQUIRE(L->hidden * 4 <= 64 * 1024 && L->inter * 4 <= 64 * 1024, TSA_ERR_SHAPE,
+                "hidden/intermediate sizes above 16384 are not supported");
+    if (L->format == TSA_EXPERT_MXFP4) {
+        const int64_t H = L->hidden, I = L->inter;
+        const int64_t need[4][2] = {{L->gate_off, 2 * I * H / 2},
+                                    {L->gate_scales_off, 2 * I * H / 32},
+                                    {L->down_off, H * I / 2},
+                                    {L->down_scales_off, H * I / 32}};
+        for (auto& r : need)
+            TSA_REQUIRE(r[0] >= 0 && r[0] + r[1] <= L->slot_bytes, TSA_ERR_WEIGHT_TOO_SMALL,
+                        "tensor at offset %lld (%lld bytes) exceeds slot_bytes %lld", (long long)r[0],
+                        (long long)r[1], (long long)L->slot_bytes);
+        if (L->gate_bias_off >= 0 || L->down_bias_off >= 0) {
+            TSA_REQUIRE(valid_dtype(L->bias_dtype), TSA_ERR_INVALID_ARG, "bad bias dtype %d", L->bias_dtype);
+            const int bs = dtype_size(L->bias_dtype);
+            TSA_REQUIRE((L->gate_bias_off < 0 || L->gate_bias_off % bs == 0) &&
+                            (L->down_bias_off < 0 || L->down_bias_off % bs == 0) && L->slot_bytes % bs == 0,
+                        TSA_ERR_INVALID_ARG, "bias offsets and slot_bytes must be multiples of the bias element size");
+            TSA_REQUIRE(L->gate_bias_off < 0 || L->gate_bias_off + 2 * I * bs <= L->slot_bytes,
+                        TSA_ERR_WEIGHT_TOO_SMALL, "gate_up bias exceeds the slot");
+            TSA_REQUIRE(L->down_bias_off < 0 || L->down_bias_off + H * bs <= L->slot_bytes, TSA_ERR_WEIGHT_TOO_SMALL,
+                        "down bias exceeds the slot");
+        }
+    } else {
+        int be, ts;
+        const int types[3] = {L->gate_type, L->up_type, L->down_type};
+        const int64_t offs[3] = {L->gate_off, L->up_off, L->down_off};
+        for (int i = 0; i < 3; ++i) {
+            TSA_REQUIRE(gguf_geometry(types[i], &be, &ts), TSA_ERR_UNSUPPORTED_TYPE,
+                        "Unsupported ggml_type: %d. Supported: Q8_0(8), Q4_K(12), Q5_K(13), Q6_K(14)", types[i]);
+            TSA_REQUIRE((L->hidden * L->inter) % be == 0, TSA_ERR_SHAPE, "matrix is not a whole number of blocks");
+            const int64_t nbytes = L->hidden * L->inter / be * ts;
+            TSA_REQUIRE(offs[i] >= 0 && offs[i] + nbytes <= L->slot_bytes, TSA_ERR_WEIGHT_TOO_SMALL,
+                        "weight_data too small: projection %d needs bytes [%lld, %lld) of a %lld-byte slot", i,
+                        (long long)offs[i], (long long)(offs[i] + nbytes), (long long)L->slot_bytes);
+        }
+        TSA_REQUIRE(L->gate_type == L->up_type, TSA_ERR_UNSUPPORTED_TYPE,
+                    "the fused decode needs gate and up in one ggml type (got %d and %d)", L->gate_type, L->up_type);
+    }
+    return TSA_OK;
+}
+
+}  // namespace tsa
+
+using namespace tsa;
+
+extern "C" int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t* bytes) {
+    clear_error();
+    int rc = validate_layout(layout);
+    if (rc) return rc;
+    TSA_REQUIRE(T >= 0 && k >= 1 && bytes, TSA_ERR_INVALID_ARG, "bad T/k/bytes");
+    *bytes = ws_bytes(*layout, T, k);
+    return TSA_OK;
+}
+
+extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool, int64_t n_slots, const int32_t* slots,
+                              const float* weights, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = validate_layout(layout);
+    if (rc) return rc;
+    const tsa_expert_layout& L = *layout;
+    TSA_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype), TSA_ERR_INVALID_ARG, "bad dtype (x %d, y %d)", x_dtype,
+                y_dtype);
+    TSA_REQUIRE(T >= 0 && k >= 1 && k <= 64 && n_slots >= 0, TSA_ERR_INVALID_ARG, "bad T (%lld) / k (%d) / n_slots",
+                (long long)T, k);
+    if (T == 0) return TSA_OK;
+    TSA_REQUIRE(pool && slots && weights && x && y, TSA_ERR_INVALID_ARG, "null pointer");
+    TSA_REQUIRE(workspace && workspace_bytes >= ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
+                "workspace too small: got %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)ws_bytes(L, T, k));
+    const Launch s = shapes(L, T, k);
+    hipStream_t st = as_stream(stream);
+    const uint8_t* pl = static_cast<const uint8_t*>(pool);
+    float* h = static_cast<float*>(workspace);
+    const bool a16 = ((reinterpret_cast<uintptr_t>(pool) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 15) == 0;
+    hipError_t e = hipSuccess;
+    if (L.format == TSA_EXPERT_MXFP4) {
+        if (a16) {
+            hipLaunchKernelGGL((mx_phase_a<16>), s.ga, dim3(256), s.lds_a, st, L, pl, n_slots, slots, k, x, x_dtype, h);
+            hipLaunchKernelGGL((mx_phase_b<16>), s.gb, dim3(256), s.lds_b, st, L, pl, n_slots, slots, weights, k, h, y,
+                               y_dtype);
+        } else {
+            hipLaunchKernelGGL((mx_phase_a<1>), s.ga, dim3(256), s.lds_a, st, L, pl, n_slots, slots, k, x, x_dtype, h);
+            hipLaunchKernelGGL((mx_phase_b<1>), s.gb, dim3(256), s.lds_b, st, L, pl, n_slots, slots, weights, k, h, y,
+                               y_dtype);
+        }
+        TSA_LAUNCH_CHECK();
+        return TSA_OK;
+    }
+    const bool a2 = ((reinterpret_cast<uintptr_t>(pool) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
+    switch (L.gate_type) {
+        case 8: e = a2 ? launch_gguf_a<8, 2>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
+                       : launch_gguf_a<8, 1>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st); break;
+        case 12: e = a16 ? launch_gguf_a<12, 16>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
+                         : launch_gguf_a<12, 1>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st); break;
+        case 13: e = a16 ? launch_gguf_a<13, 16>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
+                         : launch_gguf_a<13, 1>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st); break;
+        default: e = a2 ? launch_gguf_a<14, 2>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
+                        : launch_gguf_a<14, 1>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st); break;
+    }
+    TSA_HIP_CHECK(e);
+    switch (L.down_type) {
+        case 8: e = a2 ? launch_gguf_b<8, 2>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st)
+                       : launch_gguf_b<8, 1>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st); break;
+        case 12: e = a16 ? launch_gguf_b<12, 16>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st)
+                         : launch_gguf_b<12, 1>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st); break;
+        case 13: e = a16 ? launch_gguf_b<13, 16>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st)
+                         : launch_gguf_b<13, 1>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st); break;
+        default: e = a2 ? launch_gguf_b<14, 2>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st)
+                        : launch_gguf_b<14, 1>(s, L, pl, n_slots, slots, weights, k, h, y, y_dtype, st); break;
+    }
+    TSA_HIP_CHECK(e);
+    return TSA_OK;
+}
