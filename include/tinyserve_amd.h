@@ -117,7 +117,9 @@ int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, in
 /* Fused top-k expert FFN over resident packed slots:
  *   y[t] = sum_j weights[t, j] * FFN(pool + slots[t, j] * slot_bytes, x[t]),
  * skipping slots < 0 (they contribute zero). slots [T, k] int32 and weights [T, k] f32
- * stay on the device (no host sync). y is overwritten.
+ * stay on the device (no host sync). y is overwritten. The workspace
+ * (tsa_moe_decode_workspace_size bytes) must be zero-filled once before its first use;
+ * calls leave it reusable. Calls that share a workspace must be ordered (one stream).
  * Replaces fast_expert_forward (tinyserve/csrc/expert_loop.cpp:41-123) and the per-expert
  * loops of ExpertPipeline._execute_layer_experts_native / _forward_cache_hits
  * (tinyserve/expert_pipeline.py:241-285,416-496) over GGMLExpertForward
@@ -127,6 +129,18 @@ int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool, int64_t n_
                    const int32_t* slots, const float* weights, int64_t T, int k,
                    const void* x, int x_dtype, void* y, int y_dtype,
                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Router + fused top-k expert FFN in one call: routes logits [T, E] (mode as in
+ * tsa_route_topk), maps expert ids to slots through expert_slot [E] (-1: not resident,
+ * contributes zero) and computes y as tsa_moe_decode does. idx_out [T, k] / w_out [T, k]
+ * (optional, may be NULL) receive the routing. For MXFP4 experts with T <= 4 this is a
+ * single kernel launch with no host sync.
+ * Replaces the route closure + execute_layer_experts pair of the MoE hook
+ * (tinyserve/_model_hooks.py:524-564, tinyserve/expert_pipeline.py:140-164). */
+int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                          const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype, int mode,
+                          int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                          int32_t* idx_out, float* w_out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Expert-major grouping of the (token, j) assignments idx [T, k] (int32 expert ids in
  * [0, E), ids < 0 ignored): counts [E], offsets [E+1] (exclusive scan), perm [T*k]

@@ -98,6 +98,90 @@ def test_moe_decode_negative_slots_and_permutation():
     np.testing.assert_allclose(to_f32(y1), to_f32(y2), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("H,E,k,T,routed", [(512, 6, 4, 1, False), (512, 8, 4, 4, True), (1024, 5, 2, 2, True),
+                                             (2048, 4, 4, 1, False), (512, 20, 6, 3, False)])
+def test_fused_decode_intermediate_and_output(H, E, k, T, routed):
+    """The single-launch kernel (H == I, bf16 x, T <= 4): the published intermediate h
+    (workspace, phase A) and the output (phase B) against the oracle."""
+    rng, lay, experts, pool = _mx_setup(H, H, E, seed=H + E + k + T)
+    L = mxfp4_expert_layout(lay)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    idx, w = oex.route_topk_then_softmax(logits, k)
+    ws = ops.moe_decode_workspace(L, T, k, "cuda")
+    if routed:
+        y, gidx, gw = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                            torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k, workspace=ws,
+                                            return_routing=True)
+        assert np.array_equal(gidx.cpu().numpy(), idx)
+        np.testing.assert_allclose(gw.cpu().numpy(), w, rtol=1e-5)
+    else:
+        y = ops.moe_decode(L, pool, torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
+                           bf16_dev(x_bits), workspace=ws)
+    torch.cuda.synchronize()
+    xf = synth.bf16_to_f32(x_bits)
+    h_gpu = ws[256 : 256 + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
+    for t in range(T):
+        for j in range(k):
+            e = experts[idx[t, j]]
+            wgu, _ = oex.mxfp4_expert_weights(e)
+            h_ref = oex.gptoss_swiglu(xf[t : t + 1] @ wgu.T + e["gate_up_bias"]).reshape(-1)
+            assert_close_bf16(h_gpu[t, j], h_ref, f"h[{t},{j}]")
+    assert_close_bf16(y, _mx_ref(experts, xf, idx, w), "fused output")
+    assert ws[:12].view(torch.int32).cpu().tolist() == [0, 0, 0]
+
+
+def test_moe_decode_mxfp4_two_launch_path_T6():
+    """T > 4 tokens take the two-launch kernels; same semantics."""
+    rng, lay, experts, pool = _mx_setup(256, 128, 6, seed=31)
+    L = mxfp4_expert_layout(lay)
+    T, k = 6, 3
+    x_bits = synth.bf16_normal(rng, (T, 256))
+    idx, w = oex.route_topk_then_softmax(rng.normal(size=(T, 6)).astype(np.float32), k)
+    y = ops.moe_decode(L, pool, torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
+                       bf16_dev(x_bits))
+    assert_close_bf16(y, _mx_ref(experts, synth.bf16_to_f32(x_bits), idx, w), "two-launch decode")
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_decode_routed_matches_oracle_and_repeats(T):
+    """Routing fused into the decode launch; 12 back-to-back launches on one workspace
+    (the grid-barrier counters must come back to zero) with different inputs each time."""
+    rng, lay, experts, pool = _mx_setup(512, 256, 8, seed=5 + T)
+    L = mxfp4_expert_layout(lay)
+    expert_slot = torch.arange(8, dtype=torch.int32, device="cuda")
+    ws = ops.moe_decode_workspace(L, T, 4, "cuda")
+    outs, refs = [], []
+    for it in range(12):
+        logits = rng.normal(size=(T, 8)).astype(np.float32)
+        x_bits = synth.bf16_normal(rng, (T, 512))
+        y, idx, w = ops.moe_decode_routed(L, pool, expert_slot, torch.from_numpy(logits).cuda(), bf16_dev(x_bits), 4,
+                                          workspace=ws, return_routing=True)
+        ridx, rw = oex.route_topk_then_softmax(logits, 4)
+        assert np.array_equal(idx.cpu().numpy(), ridx)
+        np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5)
+        outs.append(y)
+        refs.append(_mx_ref(experts, synth.bf16_to_f32(x_bits), ridx, rw))
+    torch.cuda.synchronize()
+    for y, ref in zip(outs, refs):
+        assert_close_bf16(y, ref, "routed decode")
+    bar = ws[:12].view(torch.int32).cpu().numpy()
+    assert bar.tolist() == [0, 0, 0], f"barrier counters/error flag not clean: {bar}"
+
+
+def test_moe_decode_routed_missing_expert_slot():
+    """expert_slot = -1 (not resident) contributes zero, as a negative slot does."""
+    rng, lay, experts, pool = _mx_setup(256, 128, 4, seed=8)
+    L = mxfp4_expert_layout(lay)
+    logits = np.array([[3.0, 2.0, 1.0, 0.0]], dtype=np.float32)
+    x_bits = synth.bf16_normal(rng, (1, 256))
+    es = torch.tensor([0, -1, 2, 3], dtype=torch.int32, device="cuda")
+    y = ops.moe_decode_routed(L, pool, es, torch.from_numpy(logits).cuda(), bf16_dev(x_bits), 2, out_dtype=torch.float32)
+    ridx, rw = oex.route_topk_then_softmax(logits, 2)
+    ref = np.float32(rw[0, 0]) * oex.mxfp4_expert_forward(synth.bf16_to_f32(x_bits), experts[0])
+    assert_close_bf16(y, ref, "missing slot")
+
+
 def _gguf_ref(experts, x, idx, w):
     return oex.moe_combine(x, idx, w, lambda e, xx: oex.gguf_expert_forward(xx, experts[e]))
 

@@ -186,9 +186,25 @@ hipError_t launch_gguf_b(const Launch& s, const tsa_expert_layout& L, const uint
     return hipGetLastError();
 }
 
-int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) { return ((T * k * L.inter * 4) + 255) / 256 * 256; }
-
 }  // namespace
+
+int64_t mx_fused_ws_bytes(const tsa_expert_layout& L, int64_t T, int k);
+int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
+                    const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
+                    int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
+                    int y_dtype, uint8_t* ws, int64_t ws_bytes, hipStream_t st);
+
+// Workspace: [0, 256) barrier counters (zero before first use; the fused kernel leaves
+// them zero), then the larger of the two-launch path's float h [T, k, I] and the fused
+// path's fp8 h terms, then int32 slots / ids and float weights [T, k] for routed calls.
+static int64_t h_region(const tsa_expert_layout& L, int64_t T, int k) {
+    const int64_t v1 = (T * k * L.inter * 4 + 255) / 256 * 256;
+    const int64_t fu = mx_fused_ws_bytes(L, T, k);
+    return v1 > fu ? v1 : fu;
+}
+static int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
+    return 256 + h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
+}
 
 int validate_layout(const tsa_expert_layout* L) {
     TSA_REQUIRE(L != nullptr, TSA_ERR_INVALID_ARG, "layout is null");
@@ -246,6 +262,19 @@ int validate_layout(const tsa_expert_layout* L) {
 
 using namespace tsa;
 
+static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
+                             const float* weights, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                             uint8_t* ws, hipStream_t st);
+
+__global__ void __launch_bounds__(256) tsa_map_slots_kernel(const int32_t* __restrict__ idx, int64_t n,
+                                                             const int32_t* __restrict__ expert_slot, int64_t E,
+                                                             int32_t* __restrict__ slots) {
+    const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    const int e = idx[a];
+    slots[a] = (e >= 0 && e < E) ? expert_slot[e] : -1;
+}
+
 extern "C" int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t* bytes) {
     clear_error();
     int rc = validate_layout(layout);
@@ -271,11 +300,21 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
     TSA_REQUIRE(workspace && workspace_bytes >= ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
                 "workspace too small: got %lld bytes, need %lld", (long long)workspace_bytes,
                 (long long)ws_bytes(L, T, k));
-    const Launch s = shapes(L, T, k);
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
-    float* h = static_cast<float*>(workspace);
-    const bool a16 = ((reinterpret_cast<uintptr_t>(pool) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 15) == 0;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    rc = mx_fused_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
+                         y, y_dtype, ws, workspace_bytes, st);
+    if (rc <= 0) return rc;
+    return two_launch_decode(L, pl, n_slots, slots, weights, T, k, x, x_dtype, y, y_dtype, ws, st);
+}
+
+static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
+                             const float* weights, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                             uint8_t* ws, hipStream_t st) {
+    const Launch s = shapes(L, T, k);
+    float* h = reinterpret_cast<float*>(ws + 256);
+    const bool a16 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 15) == 0;
     hipError_t e = hipSuccess;
     if (L.format == TSA_EXPERT_MXFP4) {
         if (a16) {
@@ -290,7 +329,7 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
         TSA_LAUNCH_CHECK();
         return TSA_OK;
     }
-    const bool a2 = ((reinterpret_cast<uintptr_t>(pool) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
+    const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
     switch (L.gate_type) {
         case 8: e = a2 ? launch_gguf_a<8, 2>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
                        : launch_gguf_a<8, 1>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st); break;
@@ -314,4 +353,43 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
     }
     TSA_HIP_CHECK(e);
     return TSA_OK;
+}
+
+extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                                     const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype,
+                                     int mode, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                                     int32_t* idx_out, float* w_out, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+    clear_error();
+    int rc = validate_layout(layout);
+    if (rc) return rc;
+    const tsa_expert_layout& L = *layout;
+    TSA_REQUIRE(valid_dtype(x_dtype) && valid_dtype(y_dtype) && valid_dtype(logits_dtype), TSA_ERR_INVALID_ARG,
+                "bad dtype (x %d, y %d, logits %d)", x_dtype, y_dtype, logits_dtype);
+    TSA_REQUIRE(mode >= 0 && mode <= 2, TSA_ERR_INVALID_ARG, "bad routing mode %d", mode);
+    TSA_REQUIRE(E >= 1 && E <= 1024 && k >= 1 && k <= 64 && k <= E && T >= 0, TSA_ERR_SHAPE,
+                "bad routing shape (E %lld, k %d, T %lld)", (long long)E, k, (long long)T);
+    if (T == 0) return TSA_OK;
+    TSA_REQUIRE(pool && expert_slot && logits && x && y, TSA_ERR_INVALID_ARG, "null pointer");
+    const int64_t need = ws_bytes(L, T, k);
+    TSA_REQUIRE(workspace && workspace_bytes >= need, TSA_ERR_WORKSPACE, "workspace too small: got %lld bytes, need %lld",
+                (long long)workspace_bytes, (long long)need);
+    hipStream_t st = as_stream(stream);
+    const uint8_t* pl = static_cast<const uint8_t*>(pool);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    rc = mx_fused_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
+                         T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+    if (rc <= 0) return rc;
+    // separate routing, slot mapping and the two-launch decode
+    const int64_t tk = (T * k * 4 + 255) / 256 * 256;
+    uint8_t* extra = ws + 256 + h_region(L, T, k);
+    int32_t* slots = reinterpret_cast<int32_t*>(extra);
+    int32_t* idx = idx_out ? idx_out : reinterpret_cast<int32_t*>(extra + tk);
+    float* w = w_out ? w_out : reinterpret_cast<float*>(extra + 2 * tk);
+    rc = tsa_route_topk(logits, logits_dtype, T, E, k, mode, idx, w, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(tsa_map_slots_kernel, dim3((unsigned)((T * k + 255) / 256)), dim3(256), 0, st, idx, T * k,
+                       expert_slot, E, slots);
+    TSA_LAUNCH_CHECK();
+    return two_launch_decode(L, pl, n_slots, slots, w, T, k, x, x_dtype, y, y_dtype, ws, st);
 }

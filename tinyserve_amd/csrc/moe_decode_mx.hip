@@ -1,0 +1,506 @@
+// Fused single-launch MXFP4 MoE decode (gfx950): routing + gate_up + clamped SwiGLU +
+// down + weighted top-k sum in one persistent launch.
+//
+// Work is a task list, phase A first:
+//   phase A task = (token t, expert j, 64 gate_up rows): each of the 4 waves owns 16
+//     consecutive rows (16 x 1440 B contiguous for K = 2880) and streams them with fully
+//     contiguous 16-byte-per-lane buffer loads: lane l of load s holds 16-byte group
+//     chunk c = 64 s + l of the tile, i.e. row c / G, group c % G. Each chunk (32 e2m1
+//     values) is expanded to bf16 pairs with v_cvt_scalef32_pk_bf16_fp4 (exact) and
+//     dotted with the activation's bf16 pairs from LDS by v_dot2c_f32_bf16 (fp32
+//     accumulate), then scaled by its e8m0 group scale and accumulated into the lane's
+//     partial of that row. DPP wave reductions give the 16 row sums; row pairs (gate,
+//     up) go through the clamped SwiGLU and the 8 h values are published with
+//     agent-coherent stores followed by a counter increment.
+//   phase B task = (token t, 16 output rows): wave j computes expert j's 16 down rows
+//     the same way, with h (rounded to bf16, like the reference's bf16 activations)
+//     staged in LDS; the waves' weighted rows are summed in a fixed order in LDS, so each
+//     output has one writer and the result is deterministic.
+//
+// Synchronisation: a workgroup waits (relaxed polls, bounded) only before its first
+// phase B task and only after issuing that task's weight loads, so the wait overlaps
+// HBM traffic. The grid never exceeds the co-resident workgroup count and every
+// workgroup finishes its phase A tasks before it waits, so the wait always ends; the
+// spin limit is a backstop that sets an error flag. The last workgroup to leave resets
+// the counters for the next launch.
+//
+// Routing (optional) runs in every workgroup's prologue on one wave with DPP reductions:
+// descending logit, ties to the lower expert id.
+//
+// Semantics: tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases, clamped
+// SwiGLU), :456-473 (routing), tinyserve/csrc/expert_loop.cpp:83-121 (weighted sum).
+#include "tsa_common.h"
+#include "formats.h"
+
+namespace tsa {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int MAXT = 4;   // tokens per fused launch
+constexpr int MAXK = 16;  // experts per token
+constexpr int WAVES = 4;
+constexpr int ROWS = 16;  // rows per wave tile
+constexpr int MISC_LDS = 2048;  // slot/weight/selection tables, per-wave row sums, flag
+constexpr int SPIN_LIMIT = 1 << 22;  // ~2 s of s_sleep(8); never reached in a healthy run
+
+// ---------------------------------------------------------------- DPP wave reductions
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float dpp_f(float v, float old) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ int dpp_i(int v, int old) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+// Lane l accumulates v[l-1], v[l-2], v[l-3] of the ORIGINAL values (row_shr 1,2,3), then
+// the partials of lanes l-4 (banks 1-3) and l-8 (banks 2-3), so lane 15 of each 16-lane
+// row holds the row sum; row_bcast 15 / 31 fold the rows into lane 63, which is read back
+// as a wave-uniform value. (Max/min use the same pattern; idempotence lets them fold the
+// running value at every step.)
+__device__ __forceinline__ float wave_sum_u(float v) {
+    const float o = v;
+    v += dpp_f<0x111, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x112, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x113, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x114, 0xF, 0xE>(v, 0.0f);
+    v += dpp_f<0x118, 0xF, 0xC>(v, 0.0f);
+    v += dpp_f<0x142, 0xA, 0xF>(v, 0.0f);
+    v += dpp_f<0x143, 0xC, 0xF>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max_u(float v) {
+    const float ni = -INFINITY;
+    v = fmaxf(v, dpp_f<0x111, 0xF, 0xF>(v, ni));
+    v = fmaxf(v, dpp_f<0x112, 0xF, 0xF>(v, ni));
+    v = fmaxf(v, dpp_f<0x113, 0xF, 0xF>(v, ni));
+    v = fmaxf(v, dpp_f<0x114, 0xF, 0xE>(v, ni));
+    v = fmaxf(v, dpp_f<0x118, 0xF, 0xC>(v, ni));
+    v = fmaxf(v, dpp_f<0x142, 0xA, 0xF>(v, ni));
+    v = fmaxf(v, dpp_f<0x143, 0xC, 0xF>(v, ni));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ int wave_min_u(int v) {
+    const int big = 0x7FFFFFFF;
+    v = min(v, dpp_i<0x111, 0xF, 0xF>(v, big));
+    v = min(v, dpp_i<0x112, 0xF, 0xF>(v, big));
+    v = min(v, dpp_i<0x113, 0xF, 0xF>(v, big));
+    v = min(v, dpp_i<0x114, 0xF, 0xE>(v, big));
+    v = min(v, dpp_i<0x118, 0xF, 0xC>(v, big));
+    v = min(v, dpp_i<0x142, 0xA, 0xF>(v, big));
+    v = min(v, dpp_i<0x143, 0xC, 0xF>(v, big));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+struct MxParams {
+    tsa_expert_layout L;
+    const uint8_t* pool;
+    int64_t n_slots;
+    const int32_t* slots;        // [T, k] (unrouted) or null
+    const float* wts;            // [T, k] (unrouted) or null
+    const void* logits;          // [T, E] (routed) or null
+    const int32_t* expert_slot;  // [E] (routed)
+    int32_t* idx_out;            // [T, k] (routed, optional)
+    float* w_out;                // [T, k] (routed, optional)
+    int logits_dtype, route_mode, E;
+    int T, k;
+    const uint16_t* x;  // bf16 [T, H]
+    void* y;
+    int y_dtype;
+    float* h;       // [T, k, I] published intermediate
+    unsigned* bar;  // [0] phase A waves published, [1] workgroups finished, [2] error flag
+    int nA, nB, grid;
+};
+
+__device__ __forceinline__ unsigned ld_relaxed(unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Byte offset in LDS of 16-byte chunk q (0..3) of 32-value group g of a bf16 vector:
+// chunks rotate by g/2 so that 16 lanes reading consecutive groups hit 8 distinct bank
+// quads (two 128-byte cycles, the minimum for 256 bytes).
+__device__ __forceinline__ int xchunk(int g, int q) { return 64 * g + 16 * ((q + (g >> 1)) & 3); }
+
+// One wave routes token t (E <= 256): selected ids into s_sel, weights into s_w.
+__device__ void route_token(const MxParams& p, int t, int lane, int* s_sel, float* s_w) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < p.E ? load_act(p.logits, p.logits_dtype, (int64_t)t * p.E + e) : -INFINITY;
+    }
+    unsigned taken = 0;
+    float myval = -INFINITY;  // lane r < k: the r-th selected logit
+    for (int r = 0; r < p.k; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // j ascending keeps the lowest id on ties within a lane
+            const int e = lane + 64 * j;
+            if (e < p.E && !((taken >> j) & 1u) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
+        }
+        const float m = wave_max_u(bv);
+        const int e = wave_min_u(bv == m ? bi : 0x7FFFFFFF);
+        if ((e & 63) == lane) taken |= 1u << (e >> 6);
+        if (lane == r) myval = m;
+        if (lane == 0) s_sel[t * p.k + r] = e;
+    }
+    float w;
+    if (p.route_mode == TSA_ROUTE_TOPK_SOFTMAX) {
+        const float top = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(myval)));  // lane 0 = max
+        const float ex = lane < p.k ? expf(myval - top) : 0.0f;
+        w = ex / wave_sum_u(ex);
+    } else {
+        const float vmax = wave_max_u(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j < p.E) s += expf(v[j] - vmax);
+        const float zsum = wave_sum_u(s);
+        const float pr = lane < p.k ? expf(myval - vmax) / zsum : 0.0f;
+        w = p.route_mode == TSA_ROUTE_SOFTMAX_TOPK_RENORM ? pr / wave_sum_u(pr) : pr;
+    }
+    if (lane < p.k) s_w[t * p.k + lane] = w;
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct XFrag {
+    bf16x8 v[4];
+};
+
+// The 32 bf16 activations of group g (LDS, swizzled).
+__device__ __forceinline__ XFrag load_x(const uint8_t* xs, int g) {
+    XFrag f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) f.v[d] = *reinterpret_cast<const bf16x8*>(xs + xchunk(g, d));
+    return f;
+}
+
+// Dot of one 16-byte MXFP4 chunk (32 e2m1 values) with 32 bf16 activations, unscaled.
+// The activation pairs are taken as bf16 shuffles of the 8-wide LDS read: going through
+// 32-bit dwords (bitcast of an element of a <4 x i32>) miscompiles with this toolchain -
+// all four v_dot2c operands of a read collapse onto one register (found with an
+// on-device probe; this form keeps them distinct and is exact).
+__device__ __forceinline__ float chunk_dot(const u32x4& q, const XFrag& x) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t w = q[d];
+        const bf16x8 xv = x.v[d];
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0),
+                                              __builtin_shufflevector(xv, xv, 0, 1), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1),
+                                              __builtin_shufflevector(xv, xv, 2, 3), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2),
+                                              __builtin_shufflevector(xv, xv, 4, 5), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3),
+                                              __builtin_shufflevector(xv, xv, 6, 7), acc, false);
+    }
+    return acc;
+}
+
+// A wave's 16-row tile: S contiguous loads of 64 x 16 B; its 16*G scale bytes (also
+// contiguous) go through LDS, loaded first so that waiting for them does not wait for
+// the tile.
+template <int G>
+struct Tile {
+    static constexpr int S = (ROWS * G + 63) / 64;
+    u32x4 q[S];
+};
+
+// Buffer resources start at the tile, so chunks past the matrix end read zero (no fault).
+template <int G>
+__device__ __forceinline__ void tile_load(Tile<G>& tl, uint8_t* rs, const uint8_t* blocks, const uint8_t* scales,
+                                          int64_t nrows, int64_t row0, int lane) {
+    static_assert(ROWS * G <= 128 * 16, "two 16-byte scale loads per lane");
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(blocks + row0 * G * 16), (short)0, (int)((nrows - row0) * G * 16), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(scales + row0 * G), (short)0, (int)((nrows - row0) * G), 0x00020000);
+    const u32x4 s0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, 16 * lane, 0, 0));
+    const u32x4 s1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, 16 * (64 + lane), 0, 0));
+#pragma unroll
+    for (int s = 0; s < Tile<G>::S; ++s)
+        tl.q[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, 16 * (64 * s + lane), 0, 2));
+    if (16 * lane < ROWS * G) *reinterpret_cast<u32x4*>(rs + 16 * lane) = s0;
+    if (16 * (64 + lane) < ROWS * G) *reinterpret_cast<u32x4*>(rs + 16 * (64 + lane)) = s1;
+}
+
+// Row sums of the tile against the bf16 vector xs: lane r < 16 returns row r's sum.
+// A row is wave-reduced right after the step holding its last chunk, so only the rows
+// still in progress keep partial registers. Chunks past row 15 are dropped.
+template <int G>
+__device__ __forceinline__ float tile_rows(const Tile<G>& tl, const uint8_t* rs, const uint8_t* xs, int lane) {
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    float mine = 0.0f;
+#pragma unroll
+    for (int s = 0; s < Tile<G>::S; ++s) {
+        const int c = 64 * s + lane;
+        const int r = c / G;
+        const XFrag x = load_x(xs, c - r * G);
+        const uint32_t sc = rs[c < ROWS * G ? c : 0];
+        const float v = chunk_dot(tl.q[s], x) * e8m0_to_f32(sc);
+        const int rlo = (64 * s) / G, rhi = (64 * s + 63) / G;
+#pragma unroll
+        for (int rr = rlo; rr <= rhi; ++rr) {
+            if (rr >= ROWS) break;
+            acc[rr] += (r == rr) ? v : 0.0f;
+            if (G * (rr + 1) - 1 <= 64 * s + 63) {  // last chunk of row rr is in this step
+                const float sr = wave_sum_u(acc[rr]);
+                mine = lane == rr ? sr : mine;
+            }
+        }
+    }
+    return mine;
+}
+
+// A copy of v the compiler cannot see through: lane-derived addressing is then recomputed
+// inside each task instead of being hoisted out of the task loop and kept live (which
+// would cost ~4 VGPRs per load step).
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ float swiglu_oai(const tsa_expert_layout& L, float gate, float up) {
+    const float g = fminf(gate, L.swiglu_limit);
+    const float u = fminf(fmaxf(up, -L.swiglu_limit), L.swiglu_limit);
+    return (u + 1.0f) * g * sigmoidf_(L.swiglu_alpha * g);
+}
+
+// Stage n bf16 values (n % 32 == 0, 16-aligned source) into LDS with the chunk swizzle.
+__device__ __forceinline__ void stage_bf16(uint8_t* xs, const uint16_t* src, int n, int tid, int nthreads) {
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+    for (int c = tid; c < n / 8; c += nthreads) *reinterpret_cast<u32x4*>(xs + xchunk(c >> 2, c & 3)) = s4[c];
+}
+
+template <int G>
+__global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter;  // H == I == 32 G
+    const int T = p.T, k = p.k;
+    int* s_slot = reinterpret_cast<int*>(smem);                      // [MAXT*MAXK]
+    float* s_w = reinterpret_cast<float*>(smem + 4 * MAXT * MAXK);   // [MAXT*MAXK]
+    int* s_sel = reinterpret_cast<int*>(smem + 8 * MAXT * MAXK);     // [MAXT*MAXK]
+    float* s_y = reinterpret_cast<float*>(smem + 12 * MAXT * MAXK);  // [WAVES][16]
+    int* s_flag = reinterpret_cast<int*>(smem + 12 * MAXT * MAXK + 4 * WAVES * ROWS);
+    uint8_t* rsc = smem + MISC_LDS + wave * ROWS * G;  // this wave's tile scales
+    uint8_t* vec = smem + MISC_LDS + WAVES * ROWS * G;  // phase A: x [T][H] bf16; phase B: h [WAVES][I] bf16
+
+    // ---- prologue: activations into LDS (phase A workgroups), routing / slot table
+    if ((int)blockIdx.x < p.nA)
+        for (int t = 0; t < T; ++t) stage_bf16(vec + t * H * 2, p.x + (int64_t)t * H, H, tid, blockDim.x);
+    if (p.logits) {
+        if (wave == 0)
+            for (int t = 0; t < T; ++t) route_token(p, t, lane, s_sel, s_w);
+        __syncthreads();
+        for (int i = tid; i < T * k; i += blockDim.x) {
+            const int e = s_sel[i];
+            s_slot[i] = p.expert_slot[e];
+            if (blockIdx.x == 0 && p.idx_out) {
+                p.idx_out[i] = e;
+                p.w_out[i] = s_w[i];
+            }
+        }
+    } else {
+        for (int i = tid; i < T * k; i += blockDim.x) {
+            s_slot[i] = p.slots[i];
+            s_w[i] = p.wts[i];
+        }
+    }
+    if (tid == 0) s_flag[0] = 0;
+    __syncthreads();
+
+    // ---- phase A: gate_up rows -> SwiGLU -> publish h
+    int task = blockIdx.x;
+    const int tiles = I / 32;  // 64-row tiles per expert, 32 h values each
+    for (; task < p.nA; task += p.grid) {
+        const int t = task / (k * tiles), j = (task / tiles) % k, kb = task % tiles;
+        const int64_t slot = s_slot[t * k + j];
+        const bool live = slot >= 0 && slot < p.n_slots;
+        const int64_t row0 = (int64_t)kb * 64 + ROWS * wave;
+        float hv = 0.0f;
+        if (live) {
+            const uint8_t* base = p.pool + slot * L.slot_bytes;
+            float bias = 0.0f;
+            if (L.gate_bias_off >= 0 && lane < ROWS) bias = load_act(base + L.gate_bias_off, L.bias_dtype, row0 + lane);
+            Tile<G> tl;
+            tile_load<G>(tl, rsc, base + L.gate_off, base + L.gate_scales_off, 2 * (int64_t)I, row0, lane);
+            const float rs = tile_rows<G>(tl, rsc, vec + t * H * 2, opaque(lane)) + bias;  // lane r < 16: row r
+            const float up = __shfl_down(rs, 1, 64);                          // lane 2i: (gate, up) of h row0/2 + i
+            hv = swiglu_oai(L, rs, up);
+        }
+        if (lane < ROWS && (lane & 1) == 0)
+            __hip_atomic_store(p.h + (int64_t)(t * k + j) * I + row0 / 2 + lane / 2, hv, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // the h stores are complete before the count moves
+        if (lane == 0) __hip_atomic_fetch_add(&p.bar[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- phase B: down rows of every selected expert, weighted sum in a fixed order
+    bool waited = false, aborted = false;
+    const int RB = H / ROWS;
+    const int rounds = (k + WAVES - 1) / WAVES;
+    uint8_t* hs = vec + wave * I * 2;
+    const unsigned need = (unsigned)p.nA * WAVES;
+    for (; task < p.nA + p.nB && !aborted; task += p.grid) {
+        const int b = task - p.nA;
+        const int t = b / RB;
+        const int64_t n0 = (int64_t)(b % RB) * ROWS;
+        float yv = 0.0f;  // lane r < 16: this wave's weighted row n0 + r
+        for (int rd = 0; rd < rounds; ++rd) {
+            const int j = rd * WAVES + wave;
+            const int64_t slot = j < k ? s_slot[t * k + j] : -1;
+            const bool live = slot >= 0 && slot < p.n_slots;
+            const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
+            Tile<G> tl;
+            float bias = 0.0f;
+            if (live) {
+                if (L.down_bias_off >= 0 && lane < ROWS) bias = load_act(base + L.down_bias_off, L.bias_dtype, n0 + lane);
+                tile_load<G>(tl, rsc, base + L.down_off, base + L.down_scales_off, (int64_t)H, n0, lane);
+            }
+            if (!waited) {  // the first phase B task's weights are in flight already
+                if (tid == 0) {
+                    int spins = 0;
+                    while (ld_relaxed(&p.bar[0]) < need) {
+                        __builtin_amdgcn_s_sleep(8);
+                        if (++spins > SPIN_LIMIT) {
+                            __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            s_flag[0] = 1;
+                            break;
+                        }
+                    }
+                }
+                __syncthreads();
+                waited = true;
+                aborted = s_flag[0] != 0;
+            }
+            if (aborted) break;
+            if (live) {
+                // h of (t, j): agent-coherent loads, rounded to bf16 into this wave's LDS area
+                const float* hsrc = p.h + (int64_t)(t * k + j) * I;
+                for (int c = lane; c < I / 8; c += 64) {
+                    uint32_t pk[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float a0 = __hip_atomic_load(hsrc + 8 * c + 2 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const float a1 =
+                            __hip_atomic_load(hsrc + 8 * c + 2 * e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        pk[e] = (uint32_t)f32_to_bf16_bits(a0) | ((uint32_t)f32_to_bf16_bits(a1) << 16);
+                    }
+                    *reinterpret_cast<u32x4*>(hs + xchunk(c >> 2, c & 3)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                const float rs = tile_rows<G>(tl, rsc, hs, opaque(lane)) + bias;
+                yv += s_w[t * k + j] * rs;
+            }
+        }
+        if (aborted) break;
+        if (lane < ROWS) s_y[wave * ROWS + lane] = yv;
+        __syncthreads();
+        if (wave == 0 && lane < ROWS) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) sum += s_y[w * ROWS + lane];
+            store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + lane, sum);
+        }
+        __syncthreads();
+    }
+    // ---- leave: the last workgroup out resets the counters for the next launch
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned done = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == (unsigned)p.grid - 1) {
+            __hip_atomic_store(&p.bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int G>
+const void* kernel_ptr() {
+    return reinterpret_cast<const void*>(&mx_decode_kernel<G>);
+}
+
+const void* kernel_for_g(int G) {
+    switch (G) {
+        case 16: return kernel_ptr<16>();
+        case 32: return kernel_ptr<32>();
+        case 64: return kernel_ptr<64>();
+        case 90: return kernel_ptr<90>();
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+int64_t mx_fused_ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
+    return (T * k * L.inter * 4 + 255) / 256 * 256;
+}
+
+// Enqueue the fused kernel: TSA_OK, 1 if the shape/layout/dtype is outside what it handles
+// (the caller then uses the two-launch kernels), or an error status.
+int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
+                    const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
+                    int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
+                    int y_dtype, uint8_t* ws, int64_t ws_bytes, hipStream_t st) {
+    if (L.format != TSA_EXPERT_MXFP4 || L.act != TSA_ACT_SWIGLU_OAI || x_dtype != TSA_BF16) return 1;
+    if (T < 1 || T > MAXT || k < 1 || k > MAXK || L.hidden != L.inter) return 1;
+    const int G = (int)(L.hidden / 32);
+    const void* kfn = kernel_for_g(G);
+    if (!kfn) return 1;
+    if (logits && E > 256) return 1;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(x) | (uintptr_t)L.slot_bytes |
+                         (uintptr_t)L.gate_off | (uintptr_t)L.down_off;
+    if (al & 15) return 1;
+    TSA_REQUIRE(ws_bytes >= 256 + mx_fused_ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
+                "workspace too small for the fused decode");
+    const size_t lds = MISC_LDS + (size_t)WAVES * ROWS * G + (size_t)((T > WAVES ? T : WAVES) * L.hidden * 2);
+
+    MxParams p{};
+    p.L = L;
+    p.pool = pool;
+    p.n_slots = n_slots;
+    p.slots = slots;
+    p.wts = wts;
+    p.logits = logits;
+    p.logits_dtype = logits_dtype;
+    p.route_mode = mode;
+    p.expert_slot = expert_slot;
+    p.E = (int)E;
+    p.idx_out = idx_out;
+    p.w_out = w_out;
+    p.T = (int)T;
+    p.k = k;
+    p.x = static_cast<const uint16_t*>(x);
+    p.y = y;
+    p.y_dtype = y_dtype;
+    p.bar = reinterpret_cast<unsigned*>(ws);
+    p.h = reinterpret_cast<float*>(ws + 256);
+    p.nA = (int)(T * k * (L.inter / 32));
+    p.nB = (int)(T * (L.hidden / ROWS));
+
+    int per_cu = 0;
+    TSA_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 256, lds));
+    const int cus = num_cus();
+    TSA_REQUIRE(per_cu > 0 && cus > 0, TSA_ERR_HIP, "fused decode kernel cannot be resident (lds %zu)", lds);
+    const int resident = per_cu * cus;
+    p.grid = p.nA + p.nB < resident ? p.nA + p.nB : resident;
+    void* args[] = {&p};
+    TSA_HIP_CHECK(hipLaunchKernel(kfn, dim3(p.grid), dim3(256), args, lds, st));
+    return TSA_OK;
+}
+
+}  // namespace tsa

@@ -129,9 +129,10 @@ def _n_slots(pool: torch.Tensor, layout: _lib.ExpertLayout) -> int:
 
 
 def moe_decode_workspace(layout: _lib.ExpertLayout, T: int, k: int, device) -> torch.Tensor:
+    """Zero-filled decode workspace (its barrier counters must start at zero; calls keep them so)."""
     n = ctypes.c_int64()
     _lib.check(_lib.load().tsa_moe_decode_workspace_size(ctypes.byref(layout), int(T), int(k), ctypes.byref(n)))
-    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+    return torch.zeros(max(n.value, 1), dtype=torch.uint8, device=device)
 
 
 def moe_decode(layout: _lib.ExpertLayout, pool: torch.Tensor, slots: torch.Tensor, weights: torch.Tensor,
@@ -155,6 +156,32 @@ def moe_decode(layout: _lib.ExpertLayout, pool: torch.Tensor, slots: torch.Tenso
                                           out.data_ptr(), _lib.tsa_dtype(out.dtype), workspace.data_ptr(),
                                           workspace.numel(), _stream(x)))
     return out
+
+
+def moe_decode_routed(layout: _lib.ExpertLayout, pool: torch.Tensor, expert_slot: torch.Tensor, logits: torch.Tensor,
+                      x: torch.Tensor, top_k: int, mode: str = "topk_then_softmax", out: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                      return_routing: bool = False):
+    """Router top-k + fused expert FFN in one call (a single launch for MXFP4, T <= 4)."""
+    _lib.require_device(pool, expert_slot, logits, x, what="tensor")
+    H = layout.hidden
+    x2 = x.reshape(-1, H).contiguous()
+    T = x2.shape[0]
+    lg = logits.reshape(T, -1).contiguous()
+    E = lg.shape[1]
+    expert_slot = expert_slot.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((T, H), dtype=out_dtype or x.dtype, device=x.device)
+    if workspace is None:
+        workspace = moe_decode_workspace(layout, T, top_k, x.device)
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device) if return_routing else None
+    w = torch.empty((T, top_k), dtype=torch.float32, device=x.device) if return_routing else None
+    _lib.check(_lib.load().tsa_moe_decode_routed(
+        ctypes.byref(layout), pool.data_ptr(), _n_slots(pool, layout), expert_slot.data_ptr(), E, lg.data_ptr(),
+        _lib.tsa_dtype(lg.dtype), ROUTE_MODES[mode], T, int(top_k), x2.data_ptr(), _lib.tsa_dtype(x2.dtype),
+        out.data_ptr(), _lib.tsa_dtype(out.dtype), _lib.ptr(idx), _lib.ptr(w), workspace.data_ptr(), workspace.numel(),
+        _stream(x)))
+    return (out, idx, w) if return_routing else out
 
 
 def group_by_expert(idx: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
