@@ -9,6 +9,17 @@ import torch
 COS_MIN = 0.9999
 REL_MAX = 1e-2
 
+# MoE decode workspace: a 16640-byte counter header (launch-wide words, then one
+# completion counter per (token, expert) pair every 256 bytes), then float h [T, k, I].
+WS_HDR = 16640
+
+
+def ws_header_clean(ws: torch.Tensor) -> None:
+    """Every counter and the error flag of a decode workspace header are back to zero."""
+    hdr = ws[:WS_HDR].view(torch.int32).cpu().numpy()
+    bad = np.nonzero(hdr)[0]
+    assert bad.size == 0, f"workspace header not clean: words {bad[:8].tolist()} = {hdr[bad[:8]].tolist()}"
+
 
 def to_f32(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy()

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import expert as oex
-from tests.helpers import assert_close_bf16, bf16_dev, to_f32
+from tests.helpers import WS_HDR, assert_close_bf16, bf16_dev, to_f32, ws_header_clean
 from tinyserve_amd import ops, synth
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout
 
@@ -120,7 +120,7 @@ def test_fused_decode_intermediate_and_output(H, E, k, T, routed):
                            bf16_dev(x_bits), workspace=ws)
     torch.cuda.synchronize()
     xf = synth.bf16_to_f32(x_bits)
-    h_gpu = ws[256 : 256 + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
+    h_gpu = ws[WS_HDR : WS_HDR + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
     for t in range(T):
         for j in range(k):
             e = experts[idx[t, j]]
@@ -128,7 +128,7 @@ def test_fused_decode_intermediate_and_output(H, E, k, T, routed):
             h_ref = oex.gptoss_swiglu(xf[t : t + 1] @ wgu.T + e["gate_up_bias"]).reshape(-1)
             assert_close_bf16(h_gpu[t, j], h_ref, f"h[{t},{j}]")
     assert_close_bf16(y, _mx_ref(experts, xf, idx, w), "fused output")
-    assert ws[:12].view(torch.int32).cpu().tolist() == [0, 0, 0]
+    ws_header_clean(ws)
 
 
 def test_moe_decode_mxfp4_two_launch_path_T6():
@@ -165,8 +165,7 @@ def test_moe_decode_routed_matches_oracle_and_repeats(T):
     torch.cuda.synchronize()
     for y, ref in zip(outs, refs):
         assert_close_bf16(y, ref, "routed decode")
-    bar = ws[:12].view(torch.int32).cpu().numpy()
-    assert bar.tolist() == [0, 0, 0], f"barrier counters/error flag not clean: {bar}"
+    ws_header_clean(ws)
 
 
 def test_moe_decode_routed_missing_expert_slot():

@@ -194,16 +194,16 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
                     int y_dtype, uint8_t* ws, int64_t ws_bytes, hipStream_t st);
 
-// Workspace: [0, 256) barrier counters (zero before first use; the fused kernel leaves
-// them zero), then the larger of the two-launch path's float h [T, k, I] and the fused
-// path's fp8 h terms, then int32 slots / ids and float weights [T, k] for routed calls.
+// Workspace: the WS_HDR-byte counter header (zero before first use; the fused kernel
+// leaves it zero), then float h [T, k, I] (shared by both paths), then int32 slots / ids
+// and float weights [T, k] for routed calls.
 static int64_t h_region(const tsa_expert_layout& L, int64_t T, int k) {
     const int64_t v1 = (T * k * L.inter * 4 + 255) / 256 * 256;
     const int64_t fu = mx_fused_ws_bytes(L, T, k);
     return v1 > fu ? v1 : fu;
 }
 static int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
-    return 256 + h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
+    return WS_HDR + h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
 }
 
 int validate_layout(const tsa_expert_layout* L) {
@@ -313,7 +313,7 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
                              const float* weights, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
                              uint8_t* ws, hipStream_t st) {
     const Launch s = shapes(L, T, k);
-    float* h = reinterpret_cast<float*>(ws + 256);
+    float* h = reinterpret_cast<float*>(ws + WS_HDR);
     const bool a16 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 15) == 0;
     hipError_t e = hipSuccess;
     if (L.format == TSA_EXPERT_MXFP4) {
@@ -382,7 +382,7 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
     if (rc <= 0) return rc;
     // separate routing, slot mapping and the two-launch decode
     const int64_t tk = (T * k * 4 + 255) / 256 * 256;
-    uint8_t* extra = ws + 256 + h_region(L, T, k);
+    uint8_t* extra = ws + WS_HDR + h_region(L, T, k);
     int32_t* slots = reinterpret_cast<int32_t*>(extra);
     int32_t* idx = idx_out ? idx_out : reinterpret_cast<int32_t*>(extra + tk);
     float* w = w_out ? w_out : reinterpret_cast<float*>(extra + 2 * tk);

@@ -11,21 +11,26 @@
 //     accumulate), then scaled by its e8m0 group scale and accumulated into the lane's
 //     partial of that row. DPP wave reductions give the 16 row sums; row pairs (gate,
 //     up) go through the clamped SwiGLU and the 8 h values are published with
-//     agent-coherent stores followed by a counter increment.
+//     agent-coherent stores; once all 4 waves' stores are complete the workgroup adds 1
+//     to the completion counter of its (token, expert) pair.
 //   phase B task = (token t, 16 output rows): wave j computes expert j's 16 down rows
 //     the same way, with h (rounded to bf16, like the reference's bf16 activations)
 //     staged in LDS; the waves' weighted rows are summed in a fixed order in LDS, so each
 //     output has one writer and the result is deterministic.
 //
-// Synchronisation: a workgroup waits (relaxed polls, bounded) only before its first
-// phase B task and only after issuing that task's weight loads, so the wait overlaps
-// HBM traffic. The grid never exceeds the co-resident workgroup count and every
-// workgroup finishes its phase A tasks before it waits, so the wait always ends; the
-// spin limit is a backstop that sets an error flag. The last workgroup to leave resets
-// the counters for the next launch.
+// Synchronisation: before a wave first reads h of pair (t, j) it polls that pair's
+// counter (relaxed, bounded) until all I/32 phase A tasks of the pair have counted, and
+// it issues the task's weight loads before polling, so the wait overlaps HBM traffic.
+// Each pair's counter sits in its own 256-byte block and takes one atomic per phase A
+// workgroup task: same-address agent-scope atomics serialise, so one counter per wave
+// (1440 adds for GPT-OSS-20B shapes) costs ~15 us where this costs ~1. The grid never
+// exceeds the co-resident workgroup count and every workgroup finishes its phase A
+// tasks before it polls, so every wait ends; the spin limit is a backstop that sets an
+// error flag. The last phase B workgroup to leave resets the counters for the next launch
+// (workgroups without phase B work never read them).
 //
-// Routing (optional) runs in every workgroup's prologue on one wave with DPP reductions:
-// descending logit, ties to the lower expert id.
+// Routing (optional) runs in every workgroup's prologue on wave 0 with DPP reductions
+// (descending logit, ties to the lower expert id) while the other waves stage x.
 //
 // Semantics: tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases, clamped
 // SwiGLU), :456-473 (routing), tinyserve/csrc/expert_loop.cpp:83-121 (weighted sum).
@@ -43,7 +48,8 @@ constexpr int MAXK = 16;  // experts per token
 constexpr int WAVES = 4;
 constexpr int ROWS = 16;  // rows per wave tile
 constexpr int MISC_LDS = 2048;  // slot/weight/selection tables, per-wave row sums, flag
-constexpr int SPIN_LIMIT = 1 << 22;  // ~2 s of s_sleep(8); never reached in a healthy run
+constexpr int SPIN_LIMIT = 1 << 23;  // ~2 s of s_sleep(4); never reached in a healthy run
+static_assert(MAXT * MAXK <= WS_MAX_PAIRS, "one header counter per (token, expert) pair");
 
 // ---------------------------------------------------------------- DPP wave reductions
 template <int CTRL, int ROW_MASK, int BANK_MASK>
@@ -113,7 +119,7 @@ struct MxParams {
     void* y;
     int y_dtype;
     float* h;       // [T, k, I] published intermediate
-    unsigned* bar;  // [0] phase A waves published, [1] workgroups finished, [2] error flag
+    unsigned* bar;  // workspace header: [1] phase B workgroups finished, [2] error flag, pair counters
     int nA, nB, grid;
 };
 
@@ -121,21 +127,56 @@ __device__ __forceinline__ unsigned ld_relaxed(unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Completion counter of pair i = t*k + j (header layout in tsa_common.h).
+__device__ __forceinline__ unsigned* pair_ctr(const MxParams& p, int i) {
+    return p.bar + (WS_CTR_OFF + i * WS_CTR_STRIDE) / 4;
+}
+
 // Byte offset in LDS of 16-byte chunk q (0..3) of 32-value group g of a bf16 vector:
 // chunks rotate by g/2 so that 16 lanes reading consecutive groups hit 8 distinct bank
 // quads (two 128-byte cycles, the minimum for 256 bytes).
 __device__ __forceinline__ int xchunk(int g, int q) { return 64 * g + 16 * ((q + (g >> 1)) & 3); }
 
-// One wave routes token t (E <= 256): selected ids into s_sel, weights into s_w.
-__device__ void route_token(const MxParams& p, int t, int lane, int* s_sel, float* s_w) {
-    float v[4];
+// v[j] = element base + min(lane + 64 j, n - 1) of a float/bf16/fp16 array: four
+// unconditional loads issued together (a per-element dtype branch would serialise them).
+__device__ __forceinline__ void load4(const void* src, int dtype, int64_t base, int n, int lane, float v[4]) {
+    int idx[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j;
-        v[j] = e < p.E ? load_act(p.logits, p.logits_dtype, (int64_t)t * p.E + e) : -INFINITY;
+    for (int j = 0; j < 4; ++j) idx[j] = min(lane + 64 * j, n - 1);
+    if (dtype == TSA_F32) {
+        const float* f = static_cast<const float*>(src) + base;
+        const float a = f[idx[0]], b = f[idx[1]], c = f[idx[2]], d = f[idx[3]];
+        v[0] = a; v[1] = b; v[2] = c; v[3] = d;
+    } else {
+        const uint16_t* h = static_cast<const uint16_t*>(src) + base;
+        const uint32_t a = h[idx[0]], b = h[idx[1]], c = h[idx[2]], d = h[idx[3]];
+        const bool bf = dtype == TSA_BF16;
+        v[0] = bf ? bf16_bits_to_f32(a) : f16_bits_to_f32(a);
+        v[1] = bf ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+        v[2] = bf ? bf16_bits_to_f32(c) : f16_bits_to_f32(c);
+        v[3] = bf ? bf16_bits_to_f32(d) : f16_bits_to_f32(d);
     }
+}
+
+// A bias element, without a dtype branch around the load (the bits are converted after).
+__device__ __forceinline__ float load_bias(const uint8_t* src, int dtype, int64_t i) {
+    if (dtype == TSA_F32) return reinterpret_cast<const float*>(src)[i];
+    const uint32_t b = reinterpret_cast<const uint16_t*>(src)[i];
+    return dtype == TSA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// One wave routes token t (E <= 256): slots of the selected experts into s_slot (es[j] =
+// expert_slot[lane + 64 j], loaded by the caller), weights into s_w; lane r < k returns
+// the r-th selected expert id.
+__device__ int route_token(const MxParams& p, int t, int lane, const int es[4], int* s_slot, float* s_w) {
+    float v[4];
+    load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j >= p.E) v[j] = -INFINITY;
     unsigned taken = 0;
     float myval = -INFINITY;  // lane r < k: the r-th selected logit
+    int mysel = -1;           // lane r < k: the r-th selected id
     for (int r = 0; r < p.k; ++r) {
         float bv = -INFINITY;
         int bi = 0x7FFFFFFF;
@@ -146,9 +187,12 @@ __device__ void route_token(const MxParams& p, int t, int lane, int* s_sel, floa
         }
         const float m = wave_max_u(bv);
         const int e = wave_min_u(bv == m ? bi : 0x7FFFFFFF);
-        if ((e & 63) == lane) taken |= 1u << (e >> 6);
-        if (lane == r) myval = m;
-        if (lane == 0) s_sel[t * p.k + r] = e;
+        const int je = e >> 6;
+        if ((e & 63) == lane) {
+            taken |= 1u << je;
+            s_slot[t * p.k + r] = je == 0 ? es[0] : je == 1 ? es[1] : je == 2 ? es[2] : es[3];
+        }
+        if (lane == r) { myval = m; mysel = e; }
     }
     float w;
     if (p.route_mode == TSA_ROUTE_TOPK_SOFTMAX) {
@@ -166,6 +210,7 @@ __device__ void route_token(const MxParams& p, int t, int lane, int* s_sel, floa
         w = p.route_mode == TSA_ROUTE_SOFTMAX_TOPK_RENORM ? pr / wave_sum_u(pr) : pr;
     }
     if (lane < p.k) s_w[t * p.k + lane] = w;
+    return mysel;
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -278,8 +323,42 @@ __device__ __forceinline__ float swiglu_oai(const tsa_expert_layout& L, float ga
 
 // Stage n bf16 values (n % 32 == 0, 16-aligned source) into LDS with the chunk swizzle.
 __device__ __forceinline__ void stage_bf16(uint8_t* xs, const uint16_t* src, int n, int tid, int nthreads) {
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
-    for (int c = tid; c < n / 8; c += nthreads) *reinterpret_cast<u32x4*>(xs + xchunk(c >> 2, c & 3)) = s4[c];
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), (short)0, n * 2, 0x00020000);
+    for (int c0 = 0; c0 < n / 8; c0 += 2 * nthreads) {  // two 16-byte loads in flight per thread
+        const int ca = c0 + tid, cb = c0 + nthreads + tid;
+        const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * ca, 0, 0));
+        const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * cb, 0, 0));
+        if (ca < n / 8) *reinterpret_cast<u32x4*>(xs + xchunk(ca >> 2, ca & 3)) = a;
+        if (cb < n / 8) *reinterpret_cast<u32x4*>(xs + xchunk(cb >> 2, cb & 3)) = b;
+    }
+}
+
+// I floats (published h) -> bf16 into LDS with the chunk swizzle. Piece p holds floats
+// 4p..4p+3 = group p/8, chunk (p%8)/2, bytes 8*(p%2) of that chunk.
+__device__ __forceinline__ void stage_h(uint8_t* hs, const float* src, int I, int lane) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, I * 4, 0x00020000);
+    constexpr int B = 6;  // pieces per lane per batch, loads in flight together
+    const int pieces = I / 4;
+    for (int base = 0; base < pieces; base += 64 * B) {
+        u32x4 v[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b)  // sc1: coherent with the other XCDs' published stores
+            v[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (base + 64 * b + lane), 0, 16));
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int pc = base + 64 * b + lane;
+            if (pc < pieces) {
+                const uint32_t lo = (uint32_t)f32_to_bf16_bits(__uint_as_float(v[b][0])) |
+                                    ((uint32_t)f32_to_bf16_bits(__uint_as_float(v[b][1])) << 16);
+                const uint32_t hi = (uint32_t)f32_to_bf16_bits(__uint_as_float(v[b][2])) |
+                                    ((uint32_t)f32_to_bf16_bits(__uint_as_float(v[b][3])) << 16);
+                const int g = pc >> 3, q = (pc & 7) >> 1;
+                *reinterpret_cast<uint2*>(hs + xchunk(g, q) + 8 * (pc & 1)) = make_uint2(lo, hi);
+            }
+        }
+    }
 }
 
 template <int G>
@@ -291,32 +370,36 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
     const int T = p.T, k = p.k;
     int* s_slot = reinterpret_cast<int*>(smem);                      // [MAXT*MAXK]
     float* s_w = reinterpret_cast<float*>(smem + 4 * MAXT * MAXK);   // [MAXT*MAXK]
-    int* s_sel = reinterpret_cast<int*>(smem + 8 * MAXT * MAXK);     // [MAXT*MAXK]
     float* s_y = reinterpret_cast<float*>(smem + 12 * MAXT * MAXK);  // [WAVES][16]
     int* s_flag = reinterpret_cast<int*>(smem + 12 * MAXT * MAXK + 4 * WAVES * ROWS);
     uint8_t* rsc = smem + MISC_LDS + wave * ROWS * G;  // this wave's tile scales
     uint8_t* vec = smem + MISC_LDS + WAVES * ROWS * G;  // phase A: x [T][H] bf16; phase B: h [WAVES][I] bf16
 
-    // ---- prologue: activations into LDS (phase A workgroups), routing / slot table
-    if ((int)blockIdx.x < p.nA)
-        for (int t = 0; t < T; ++t) stage_bf16(vec + t * H * 2, p.x + (int64_t)t * H, H, tid, blockDim.x);
+    // ---- prologue: routing / slot table on wave 0 while the other waves stage the
+    // activations into LDS (phase A workgroups only)
+    const bool stage = (int)blockIdx.x < p.nA;
     if (p.logits) {
-        if (wave == 0)
-            for (int t = 0; t < T; ++t) route_token(p, t, lane, s_sel, s_w);
-        __syncthreads();
-        for (int i = tid; i < T * k; i += blockDim.x) {
-            const int e = s_sel[i];
-            s_slot[i] = p.expert_slot[e];
-            if (blockIdx.x == 0 && p.idx_out) {
-                p.idx_out[i] = e;
-                p.w_out[i] = s_w[i];
+        if (wave == 0) {
+            int es[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+            for (int t = 0; t < T; ++t) {
+                const int sel = route_token(p, t, lane, es, s_slot, s_w);
+                if (blockIdx.x == 0 && p.idx_out && lane < k) {
+                    p.idx_out[t * k + lane] = sel;
+                    p.w_out[t * k + lane] = s_w[t * k + lane];
+                }
             }
+        } else if (stage) {
+            for (int t = 0; t < T; ++t) stage_bf16(vec + t * H * 2, p.x + (int64_t)t * H, H, tid - 64, blockDim.x - 64);
         }
     } else {
         for (int i = tid; i < T * k; i += blockDim.x) {
             s_slot[i] = p.slots[i];
             s_w[i] = p.wts[i];
         }
+        if (stage)
+            for (int t = 0; t < T; ++t) stage_bf16(vec + t * H * 2, p.x + (int64_t)t * H, H, tid, blockDim.x);
     }
     if (tid == 0) s_flag[0] = 0;
     __syncthreads();
@@ -333,7 +416,7 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
         if (live) {
             const uint8_t* base = p.pool + slot * L.slot_bytes;
             float bias = 0.0f;
-            if (L.gate_bias_off >= 0 && lane < ROWS) bias = load_act(base + L.gate_bias_off, L.bias_dtype, row0 + lane);
+            if (L.gate_bias_off >= 0) bias = load_bias(base + L.gate_bias_off, L.bias_dtype, row0 + (lane & (ROWS - 1)));
             Tile<G> tl;
             tile_load<G>(tl, rsc, base + L.gate_off, base + L.gate_scales_off, 2 * (int64_t)I, row0, lane);
             const float rs = tile_rows<G>(tl, rsc, vec + t * H * 2, opaque(lane)) + bias;  // lane r < 16: row r
@@ -343,17 +426,20 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
         if (lane < ROWS && (lane & 1) == 0)
             __hip_atomic_store(p.h + (int64_t)(t * k + j) * I + row0 / 2 + lane / 2, hv, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);  // the h stores are complete before the count moves
-        if (lane == 0) __hip_atomic_fetch_add(&p.bar[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's h stores are complete ...
+        __syncthreads();                // ... and so are the other waves' before the count moves
+        if (tid == 0) __hip_atomic_fetch_add(pair_ctr(p, t * k + j), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- phase B: down rows of every selected expert, weighted sum in a fixed order
-    bool waited = false, aborted = false;
+    bool did_b = false;
+    uint64_t ready = 0;  // pairs t*k+j whose h this wave has seen complete (wave-uniform)
     const int RB = H / ROWS;
     const int rounds = (k + WAVES - 1) / WAVES;
     uint8_t* hs = vec + wave * I * 2;
-    const unsigned need = (unsigned)p.nA * WAVES;
-    for (; task < p.nA + p.nB && !aborted; task += p.grid) {
+    const unsigned need = (unsigned)(I / 32);  // phase A tasks per pair
+    for (; task < p.nA + p.nB; task += p.grid) {
+        did_b = true;
         const int b = task - p.nA;
         const int t = b / RB;
         const int64_t n0 = (int64_t)(b % RB) * ROWS;
@@ -366,40 +452,27 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
             Tile<G> tl;
             float bias = 0.0f;
             if (live) {
-                if (L.down_bias_off >= 0 && lane < ROWS) bias = load_act(base + L.down_bias_off, L.bias_dtype, n0 + lane);
+                if (L.down_bias_off >= 0) bias = load_bias(base + L.down_bias_off, L.bias_dtype, n0 + (lane & (ROWS - 1)));
                 tile_load<G>(tl, rsc, base + L.down_off, base + L.down_scales_off, (int64_t)H, n0, lane);
             }
-            if (!waited) {  // the first phase B task's weights are in flight already
-                if (tid == 0) {
+            if (live) {
+                const int pair = t * k + j;
+                if (!((ready >> pair) & 1)) {  // the task's weights are in flight already
+                    unsigned* c = pair_ctr(p, pair);
                     int spins = 0;
-                    while (ld_relaxed(&p.bar[0]) < need) {
-                        __builtin_amdgcn_s_sleep(8);
+                    while (ld_relaxed(c) < need) {
+                        __builtin_amdgcn_s_sleep(4);
                         if (++spins > SPIN_LIMIT) {
                             __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             s_flag[0] = 1;
                             break;
                         }
                     }
+                    ready |= 1ull << pair;
                 }
-                __syncthreads();
-                waited = true;
-                aborted = s_flag[0] != 0;
-            }
-            if (aborted) break;
-            if (live) {
-                // h of (t, j): agent-coherent loads, rounded to bf16 into this wave's LDS area
-                const float* hsrc = p.h + (int64_t)(t * k + j) * I;
-                for (int c = lane; c < I / 8; c += 64) {
-                    uint32_t pk[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float a0 = __hip_atomic_load(hsrc + 8 * c + 2 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        const float a1 =
-                            __hip_atomic_load(hsrc + 8 * c + 2 * e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        pk[e] = (uint32_t)f32_to_bf16_bits(a0) | ((uint32_t)f32_to_bf16_bits(a1) << 16);
-                    }
-                    *reinterpret_cast<u32x4*>(hs + xchunk(c >> 2, c & 3)) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-                }
+                // h of (t, j) -> bf16 in this wave's LDS area. 16-byte buffer loads with the
+                // sc1 (agent-coherent) cache policy, all issued before the first use.
+                stage_h(hs, p.h + (int64_t)(t * k + j) * I, I, lane);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -407,7 +480,6 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
                 yv += s_w[t * k + j] * rs;
             }
         }
-        if (aborted) break;
         if (lane < ROWS) s_y[wave * ROWS + lane] = yv;
         __syncthreads();
         if (wave == 0 && lane < ROWS) {
@@ -416,14 +488,19 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
             for (int w = 0; w < WAVES; ++w) sum += s_y[w * ROWS + lane];
             store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + lane, sum);
         }
+        const bool aborted = s_flag[0] != 0;  // written before the barrier above
         __syncthreads();
+        if (aborted) break;
     }
-    // ---- leave: the last workgroup out resets the counters for the next launch
-    __syncthreads();
-    if (tid == 0) {
+    // ---- leave: the last phase B workgroup out resets the counters for the next launch.
+    // Every phase A count has landed by then (each pair was seen complete), and the
+    // workgroups without phase B work never read the counters.
+    if (did_b && tid == 0) {
+        const unsigned nbw = (unsigned)(p.nB < p.grid ? p.nB : p.grid);
         const unsigned done = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done == (unsigned)p.grid - 1) {
-            __hip_atomic_store(&p.bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == nbw - 1) {
+            for (int i = 0; i < T * k; ++i)
+                __hip_atomic_store(pair_ctr(p, i), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
@@ -465,7 +542,7 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
     const uintptr_t al = reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(x) | (uintptr_t)L.slot_bytes |
                          (uintptr_t)L.gate_off | (uintptr_t)L.down_off;
     if (al & 15) return 1;
-    TSA_REQUIRE(ws_bytes >= 256 + mx_fused_ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
+    TSA_REQUIRE(ws_bytes >= WS_HDR + mx_fused_ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
                 "workspace too small for the fused decode");
     const size_t lds = MISC_LDS + (size_t)WAVES * ROWS * G + (size_t)((T > WAVES ? T : WAVES) * L.hidden * 2);
 
@@ -488,7 +565,7 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
     p.y = y;
     p.y_dtype = y_dtype;
     p.bar = reinterpret_cast<unsigned*>(ws);
-    p.h = reinterpret_cast<float*>(ws + 256);
+    p.h = reinterpret_cast<float*>(ws + WS_HDR);
     p.nA = (int)(T * k * (L.inter / 32));
     p.nB = (int)(T * (L.hidden / ROWS));
 
