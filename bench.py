@@ -43,24 +43,29 @@ def _bf16(bits: np.ndarray, dev) -> torch.Tensor:
 class MoEWorkload:
     """Resident layers of experts + per-step router logits and activations."""
 
-    def __init__(self, wl: int, n_layers: int, n_steps: int, dev: torch.device):
+    def __init__(self, wl: int, n_layers: int, n_steps: int, dev: torch.device, tiled: bool = True):
         self.wl = wl
         base = synth.workload(wl)
         self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
         self.route = base["route"]
         lay = base["layout"]
+        self.slot_bytes = lay.total_bytes  # the checkpoint-order expert: the algorithmic bytes
+        pool0 = base["pool"]
+        self.tiled = tiled and wl == 3
         if wl == 3:
-            self.L = mxfp4_expert_layout(lay)
+            if self.tiled:  # the resident pool in the 16-row MFMA tile order (same weights)
+                lay = synth.mxfp4_tiled_layout(self.H, self.I)
+                pool0 = np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in base["experts"]])
+            self.L = mxfp4_expert_layout(lay, tiled=self.tiled)
         else:
             self.L = gguf_expert_layout(lay, {"gate": 13, "up": 13, "down": 14},
                                         {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
-        self.slot_bytes = lay.total_bytes
         g = torch.Generator(device=dev)
         g.manual_seed(20261201 + wl)
         # layer 0 = the seeded numpy workload (parity-checked by the tests); others random on the GPU
-        self.pools = [torch.from_numpy(base["pool"]).to(dev)]
+        self.pools = [torch.from_numpy(pool0).to(dev)]
         for _ in range(1, n_layers):
-            p = torch.randint(0, 256, base["pool"].shape, dtype=torch.uint8, device=dev, generator=g)
+            p = torch.randint(0, 256, pool0.shape, dtype=torch.uint8, device=dev, generator=g)
             self._fix_scales(p, lay, g)
             self.pools.append(p)
         self.logits = torch.randn((n_steps, self.E), device=dev, generator=g)
@@ -156,6 +161,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--checkpoint-order", action="store_true",
+                    help="workload 3: keep the experts in the checkpoint order (the slower row-major kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
@@ -164,7 +171,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     K, W = args.steps, args.warmup
     n_layers = args.layers
-    wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev)
+    wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev, tiled=not args.checkpoint_order)
     torch.cuda.synchronize()
 
     # warmup (eager), also validates every call
@@ -220,6 +227,7 @@ def main() -> int:
             if args.workload == 3 else "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)",
             "bytes_per_step": nbytes,
             "layers_rotated": n_layers,
+            "pool_layout": "mxfp4 16-row mfma tiles" if wl.tiled else "checkpoint order",
             "graph": not args.no_graph,
         },
         "roofline": {

@@ -52,6 +52,8 @@ typedef enum tsa_expert_format { TSA_EXPERT_MXFP4 = 1, TSA_EXPERT_GGUF = 2 } tsa
  *    even = gate, odd = up), gate_up scales [2I, H/32] u8 at gate_scales_off,
  *    down blocks [H, I/32, 16] at down_off, down scales [H, I/32] at down_scales_off,
  *    optional biases [2I] / [H] of bias_dtype at gate_bias_off / down_bias_off (-1 = none).
+ *    mx_tiled = 1: both matrices are instead stored in the 16-row MFMA tile order that
+ *    tsa_mxfp4_tile produces (the fast decode path); 0: the checkpoint order above.
  *  GGUF: gate [I x H] of gate_type at gate_off, up [I x H] of up_type at up_off,
  *    down [H x I] of down_type at down_off (GGUF has no biases; set them to -1).
  *  act: TSA_ACT_SWIGLU_OAI = (up+1)*g*sigmoid(alpha*g), g = min(gate, limit),
@@ -67,6 +69,8 @@ typedef struct tsa_expert_layout {
     int64_t gate_scales_off, down_scales_off;
     int64_t gate_bias_off, down_bias_off;
     float swiglu_limit, swiglu_alpha;
+    int32_t mx_tiled;
+    int32_t reserved;
 } tsa_expert_layout;
 
 /* ---- library info / errors (no reference counterpart) ---- */
@@ -96,6 +100,23 @@ int tsa_gguf_matvec(int ggml_type, const void* w, int64_t w_bytes,
  * Replaces dequant_mxfp4_no_transpose / dequant_mxfp4 (tinyserve/mxfp4.py:20-53). */
 int tsa_mxfp4_dequant(const void* blocks, const void* scales, int64_t N, int64_t K,
                       void* out, int out_dtype, int transpose, void* stream);
+
+/* Sizes of an MXFP4 matrix [N, K] (N % 16 == 0, K % 32 == 0) in the 16-row MFMA tile
+ * order: blocks_bytes = N*K/2 (same as the checkpoint order), scales_bytes = N/16 *
+ * 256 * ceil(ceil(K/128)/4) (per-lane scale words, zero-padded).
+ * No reference counterpart: the tile order is this library's device layout. */
+int tsa_mxfp4_tile_sizes(int64_t N, int64_t K, int64_t* blocks_bytes, int64_t* scales_bytes);
+
+/* Repack an MXFP4 matrix from the checkpoint order (blocks [N, K/32, 16], scales
+ * [N, K/32]) into the 16-row MFMA tile order: tile r = rows 16r..16r+15 is 8*K
+ * contiguous bytes whose 1 KB piece m holds, at 16*(16*q + i), the 16-byte block 4m+q
+ * of row 16r+i (a wave's 16-byte-per-lane load of piece m is one MFMA operand); the
+ * scale of that block is byte m%4 of the 32-bit word (m/4, lane 16q+i) of the tile's
+ * scale area. Out-of-place; the caller owns both outputs. Used when experts are
+ * copied into the resident pool (the reference copies the checkpoint bytes as they are:
+ * ExpertStore.copy_to_buffer_slot / copy_to_buffer, tinyserve/expert_store.py:532-560). */
+int tsa_mxfp4_tile(const void* blocks, const void* scales, int64_t N, int64_t K,
+                   void* tiled_blocks, void* tiled_scales, void* stream);
 
 /* y[t, n] = sum_k deq(W)[n, k] * x[t, k] + bias[n] (bias may be NULL).
  * Replaces dot_scaled_vecmat (tinyserve/triton_dot_scaled.py:68-122) /

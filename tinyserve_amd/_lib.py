@@ -54,6 +54,8 @@ class ExpertLayout(ctypes.Structure):
         ("down_bias_off", ctypes.c_int64),
         ("swiglu_limit", ctypes.c_float),
         ("swiglu_alpha", ctypes.c_float),
+        ("mx_tiled", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -68,6 +70,8 @@ SIGNATURES = {
     "tsa_gguf_dequant": (_I32, [_I32, _P, _I64, _I64, _P, _I32, _P]),
     "tsa_gguf_matvec": (_I32, [_I32, _P, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _P]),
     "tsa_mxfp4_dequant": (_I32, [_P, _P, _I64, _I64, _P, _I32, _I32, _P]),
+    "tsa_mxfp4_tile_sizes": (_I32, [_I64, _I64, _P, _P]),
+    "tsa_mxfp4_tile": (_I32, [_P, _P, _I64, _I64, _P, _P, _P]),
     "tsa_mxfp4_matvec": (_I32, [_P, _P, _P, _I32, _P, _I32, _I64, _P, _I32, _I64, _I64, _P]),
     "tsa_route_topk": (_I32, [_P, _I32, _I64, _I64, _I32, _I32, _P, _P, _P]),
     "tsa_moe_decode_workspace_size": (_I32, [_LP, _I64, _I32, ctypes.POINTER(_I64)]),

@@ -193,6 +193,12 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
                     int y_dtype, uint8_t* ws, int64_t ws_bytes, hipStream_t st);
+int64_t mx_tile_scale_bytes(int64_t K);
+const char* mxt_unsupported(const tsa_expert_layout& L);
+int mxt_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
+                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
+                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype,
+                     uint8_t* ws, int64_t ws_bytes, hipStream_t st);
 
 // Workspace: the WS_HDR-byte counter header (zero before first use; the fused kernel
 // leaves it zero), then float h [T, k, I] (shared by both paths), then int32 slots / ids
@@ -218,12 +224,19 @@ int validate_layout(const tsa_expert_layout* L) {
                 (long long)L->inter);
     TSA_REQUIRE(L->hidden * 4 <= 64 * 1024 && L->inter * 4 <= 64 * 1024, TSA_ERR_SHAPE,
                 "hidden/intermediate sizes above 16384 are not supported");
+    TSA_REQUIRE(L->mx_tiled == 0 || (L->mx_tiled == 1 && L->format == TSA_EXPERT_MXFP4), TSA_ERR_INVALID_ARG,
+                "layout.mx_tiled must be 0, or 1 for MXFP4 experts (got %d)", L->mx_tiled);
+    if (L->mx_tiled) {
+        const char* why = mxt_unsupported(*L);
+        TSA_REQUIRE(!*why, TSA_ERR_SHAPE, "%s", why);
+    }
     if (L->format == TSA_EXPERT_MXFP4) {
         const int64_t H = L->hidden, I = L->inter;
+        const bool tl = L->mx_tiled != 0;
         const int64_t need[4][2] = {{L->gate_off, 2 * I * H / 2},
-                                    {L->gate_scales_off, 2 * I * H / 32},
+                                    {L->gate_scales_off, tl ? 2 * I / 16 * mx_tile_scale_bytes(H) : 2 * I * H / 32},
                                     {L->down_off, H * I / 2},
-                                    {L->down_scales_off, H * I / 32}};
+                                    {L->down_scales_off, tl ? H / 16 * mx_tile_scale_bytes(I) : H * I / 32}};
         for (auto& r : need)
             TSA_REQUIRE(r[0] >= 0 && r[0] + r[1] <= L->slot_bytes, TSA_ERR_WEIGHT_TOO_SMALL,
                         "tensor at offset %lld (%lld bytes) exceeds slot_bytes %lld", (long long)r[0],
@@ -275,6 +288,29 @@ __global__ void __launch_bounds__(256) tsa_map_slots_kernel(const int32_t* __res
     slots[a] = (e >= 0 && e < E) ? expert_slot[e] : -1;
 }
 
+// Tiled MXFP4 layouts: the fused MFMA kernel over chunks of up to 4 tokens (one launch
+// each, stream-ordered on the shared workspace, whose counters every launch resets).
+static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
+                        const float* weights, const void* logits, int logits_dtype, int mode,
+                        const int32_t* expert_slot, int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k,
+                        const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws, int64_t ws_bytes,
+                        hipStream_t st) {
+    TSA_REQUIRE(x_dtype == TSA_BF16, TSA_ERR_INVALID_ARG, "tiled MXFP4 experts take bf16 activations (got dtype %d)",
+                x_dtype);
+    TSA_REQUIRE(k <= 16, TSA_ERR_SHAPE, "tiled MXFP4 decode supports top-k <= 16 (got %d)", k);
+    const int64_t H = L.hidden, ys = dtype_size(y_dtype);
+    for (int64_t t0 = 0; t0 < T; t0 += 4) {
+        const int64_t tc = T - t0 < 4 ? T - t0 : 4;
+        const void* lg = logits ? static_cast<const uint8_t*>(logits) + t0 * E * dtype_size(logits_dtype) : nullptr;
+        int rc = mxt_fused_decode(L, pl, n_slots, slots ? slots + t0 * k : nullptr, weights ? weights + t0 * k : nullptr,
+                                  lg, logits_dtype, mode, expert_slot, E, idx_out ? idx_out + t0 * k : nullptr,
+                                  w_out ? w_out + t0 * k : nullptr, tc, k, static_cast<const uint16_t*>(x) + t0 * H,
+                                  static_cast<uint8_t*>(y) + t0 * H * ys, y_dtype, ws, ws_bytes, st);
+        if (rc) return rc;
+    }
+    return TSA_OK;
+}
+
 extern "C" int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t* bytes) {
     clear_error();
     int rc = validate_layout(layout);
@@ -303,6 +339,9 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (L.mx_tiled)
+        return tiled_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x,
+                            x_dtype, y, y_dtype, ws, workspace_bytes, st);
     rc = mx_fused_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
                          y, y_dtype, ws, workspace_bytes, st);
     if (rc <= 0) return rc;
@@ -377,9 +416,14 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
-    rc = mx_fused_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
-                         T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
-    if (rc <= 0) return rc;
+    if (L.mx_tiled && E <= 256)
+        return tiled_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
+                            w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+    if (!L.mx_tiled) {
+        rc = mx_fused_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
+                             w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+        if (rc <= 0) return rc;
+    }
     // separate routing, slot mapping and the two-launch decode
     const int64_t tk = (T * k * 4 + 255) / 256 * 256;
     uint8_t* extra = ws + WS_HDR + h_region(L, T, k);
@@ -391,5 +435,8 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
     hipLaunchKernelGGL(tsa_map_slots_kernel, dim3((unsigned)((T * k + 255) / 256)), dim3(256), 0, st, idx, T * k,
                        expert_slot, E, slots);
     TSA_LAUNCH_CHECK();
+    if (L.mx_tiled)
+        return tiled_decode(L, pl, n_slots, slots, w, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype, y,
+                            y_dtype, ws, workspace_bytes, st);
     return two_launch_decode(L, pl, n_slots, slots, w, T, k, x, x_dtype, y, y_dtype, ws, st);
 }

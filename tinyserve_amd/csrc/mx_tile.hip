@@ -1,0 +1,71 @@
+// MXFP4 16-row MFMA tile order (device layout of the fast decode path).
+//
+// A wave multiplies 16 weight rows at a time with v_mfma_f32_16x16x32_bf16, whose A
+// operand gives lane 16q+i row i and 8 consecutive K values of K-slice q. Each lane
+// expands one 16-byte MXFP4 block (32 values) into four such operands, so one MFMA group
+// m covers blocks 4m..4m+3 of 16 rows: exactly 1 KB. Storing each group's 1 KB in lane
+// order makes every operand fetch one fully contiguous 16-byte-per-lane load, which
+// streams from HBM like a memcpy (a row-major fetch of the same operands touches 16 rows
+// per load and runs at ~60% of that rate on MI355X).
+//
+//   tile r (rows 16r..16r+15) = 256*G bytes, G = K/32 blocks per row;
+//   block b of row 16r+i at tile offset 1024*(b/4) + 16*(16*(b%4) + i)
+//   (a short last group just ends early, so the tile is dense);
+//   its e8m0 scale at tile-scale offset 256*(b/16) + 4*(16*(b%4) + i) + (b/4)%4, the
+//   tile-scale area being 256 * ceil(ceil(G/4)/4) bytes, zero where no block exists.
+#include "tsa_common.h"
+
+namespace tsa {
+
+int64_t mx_tile_groups(int64_t K) { return (K / 32 + 3) / 4; }              // MFMA groups per row tile
+int64_t mx_tile_scale_bytes(int64_t K) { return 256 * ((mx_tile_groups(K) + 3) / 4); }  // per row tile
+
+namespace {
+
+// One thread per (row, block): moves 16 bytes and one scale byte.
+__global__ void __launch_bounds__(256) mx_tile_kernel(const uint8_t* __restrict__ blocks,
+                                                      const uint8_t* __restrict__ scales, int64_t N, int64_t G,
+                                                      int64_t stile, uint8_t* __restrict__ tb,
+                                                      uint8_t* __restrict__ ts) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= N * G) return;
+    const int64_t n = c / G, b = c % G;
+    const int64_t r = n / 16, i = n % 16;
+    const int64_t lanepos = 16 * (b % 4) + i;
+    const uint4 v = *reinterpret_cast<const uint4*>(blocks + 16 * c);
+    *reinterpret_cast<uint4*>(tb + r * 256 * G + 1024 * (b / 4) + 16 * lanepos) = v;
+    ts[r * stile + 256 * (b / 16) + 4 * lanepos + (b / 4) % 4] = scales[c];
+}
+
+}  // namespace
+}  // namespace tsa
+
+using namespace tsa;
+
+extern "C" int tsa_mxfp4_tile_sizes(int64_t N, int64_t K, int64_t* blocks_bytes, int64_t* scales_bytes) {
+    clear_error();
+    TSA_REQUIRE(blocks_bytes && scales_bytes, TSA_ERR_INVALID_ARG, "null output pointer");
+    TSA_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0, TSA_ERR_SHAPE,
+                "tiled MXFP4 needs N %% 16 == 0 and K %% 32 == 0 (N %lld, K %lld)", (long long)N, (long long)K);
+    *blocks_bytes = N * K / 2;
+    *scales_bytes = N / 16 * mx_tile_scale_bytes(K);
+    return TSA_OK;
+}
+
+extern "C" int tsa_mxfp4_tile(const void* blocks, const void* scales, int64_t N, int64_t K, void* tiled_blocks,
+                              void* tiled_scales, void* stream) {
+    int64_t bb = 0, sb = 0;
+    int rc = tsa_mxfp4_tile_sizes(N, K, &bb, &sb);
+    if (rc) return rc;
+    TSA_REQUIRE(blocks && scales && tiled_blocks && tiled_scales, TSA_ERR_INVALID_ARG, "null pointer");
+    TSA_REQUIRE(((reinterpret_cast<uintptr_t>(blocks) | reinterpret_cast<uintptr_t>(tiled_blocks)) & 15) == 0,
+                TSA_ERR_INVALID_ARG, "blocks and tiled_blocks must be 16-byte aligned");
+    hipStream_t st = as_stream(stream);
+    TSA_HIP_CHECK(hipMemsetAsync(tiled_scales, 0, (size_t)sb, st));
+    const int64_t G = K / 32, n = N * G;
+    hipLaunchKernelGGL(mx_tile_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const uint8_t*>(blocks), static_cast<const uint8_t*>(scales), N, G,
+                       mx_tile_scale_bytes(K), static_cast<uint8_t*>(tiled_blocks), static_cast<uint8_t*>(tiled_scales));
+    TSA_LAUNCH_CHECK();
+    return TSA_OK;
+}

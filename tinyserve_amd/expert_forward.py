@@ -39,9 +39,10 @@ def _is_silu(act_fn) -> bool:
 
 
 def mxfp4_expert_layout(layout: TensorLayout, act_fn=None, slot_bytes: int | None = None,
-                        swiglu_limit: float = _SWIGLU_LIMIT, swiglu_alpha: float = _QUICK_GELU_COEFF
-                        ) -> _lib.ExpertLayout:
-    """tsa_expert_layout of a GPT-OSS MXFP4 slot (gate_up_proj[_scales/_bias], down_proj[...])."""
+                        swiglu_limit: float = _SWIGLU_LIMIT, swiglu_alpha: float = _QUICK_GELU_COEFF,
+                        tiled: bool = False) -> _lib.ExpertLayout:
+    """tsa_expert_layout of a GPT-OSS MXFP4 slot (gate_up_proj[_scales/_bias], down_proj[...]);
+    ``tiled`` marks matrices stored in the 16-row MFMA tile order (synth.mxfp4_tiled_layout)."""
     specs = layout.specs
     gu_shape = tuple(specs["gate_up_proj"][0])
     dn_shape = tuple(specs["down_proj"][0])
@@ -70,6 +71,7 @@ def mxfp4_expert_layout(layout: TensorLayout, act_fn=None, slot_bytes: int | Non
     bias_dt = specs.get("gate_up_proj_bias", specs.get("down_proj_bias", (None, torch.bfloat16)))[1]
     L.bias_dtype = _BIAS_DTYPES[bias_dt]
     L.swiglu_limit, L.swiglu_alpha = float(swiglu_limit), float(swiglu_alpha)
+    L.mx_tiled = int(bool(tiled))
     return L
 
 

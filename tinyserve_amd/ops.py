@@ -78,6 +78,33 @@ def mxfp4_dequant(blocks: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype
     return out.view(shape)
 
 
+def mxfp4_tile_sizes(N: int, K: int) -> tuple[int, int]:
+    """(blocks_bytes, scales_bytes) of an [N, K] MXFP4 matrix in the 16-row MFMA tile order."""
+    bb, sb = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(_lib.load().tsa_mxfp4_tile_sizes(N, K, ctypes.byref(bb), ctypes.byref(sb)))
+    return bb.value, sb.value
+
+
+def mxfp4_tile(blocks: torch.Tensor, scales: torch.Tensor, out_blocks: torch.Tensor | None = None,
+               out_scales: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Repack MXFP4 blocks [N, G, 16] + scales [N, G] (checkpoint order) into the 16-row
+    MFMA tile order the fast decode reads (uint8 tensors of mxfp4_tile_sizes bytes)."""
+    _lib.require_device(blocks, scales, what="blocks/scales")
+    N = blocks.shape[0]
+    K = blocks[0].numel() * 2
+    bb, sb = mxfp4_tile_sizes(N, K)
+    blocks, scales = blocks.contiguous(), scales.contiguous()
+    if out_blocks is None:
+        out_blocks = torch.empty(bb, dtype=torch.uint8, device=blocks.device)
+    if out_scales is None:
+        out_scales = torch.empty(sb, dtype=torch.uint8, device=blocks.device)
+    if out_blocks.numel() * out_blocks.element_size() < bb or out_scales.numel() * out_scales.element_size() < sb:
+        raise ValueError(f"outputs too small: need {bb} and {sb} bytes")
+    _lib.check(_lib.load().tsa_mxfp4_tile(blocks.data_ptr(), scales.data_ptr(), N, K, out_blocks.data_ptr(),
+                                          out_scales.data_ptr(), _stream(blocks)))
+    return out_blocks, out_scales
+
+
 def mxfp4_matvec(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None,
                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """y[T, N] = x[T, K] @ deq(W)^T + bias with W in MXFP4 ([N, G, 16] or [N, 16G] blocks)."""

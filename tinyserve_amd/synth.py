@@ -120,6 +120,35 @@ def pack_mxfp4_expert(e: dict, layout: TensorLayout) -> np.ndarray:
     return slot
 
 
+def mxfp4_tiled_layout(hidden: int, inter: int, bias: bool = True) -> TensorLayout:
+    """The same tensors with both matrices in the 16-row MFMA tile order
+    (tinyserve_amd.mx_tiles): blocks keep their shape and size, scales become
+    [rows/16, tile_scale_bytes] per-tile areas."""
+    from .mx_tiles import tile_scale_bytes
+
+    specs = {
+        "gate_up_proj": ((2 * inter, hidden // 32, 16), torch.uint8),
+        "gate_up_proj_scales": ((2 * inter // 16, tile_scale_bytes(hidden)), torch.uint8),
+    }
+    if bias:
+        specs["gate_up_proj_bias"] = ((2 * inter,), torch.bfloat16)
+    specs["down_proj"] = ((hidden, inter // 32, 16), torch.uint8)
+    specs["down_proj_scales"] = ((hidden // 16, tile_scale_bytes(inter)), torch.uint8)
+    if bias:
+        specs["down_proj_bias"] = ((hidden,), torch.bfloat16)
+    return TensorLayout(specs)
+
+
+def pack_mxfp4_expert_tiled(e: dict, layout: TensorLayout) -> np.ndarray:
+    """Pack an expert (make_mxfp4_expert dict) into a mxfp4_tiled_layout slot."""
+    from .mx_tiles import tile_mxfp4
+
+    gb, gs = tile_mxfp4(e["gate_up_blocks"], e["gate_up_scales"])
+    db, ds = tile_mxfp4(e["down_blocks"], e["down_scales"])
+    return pack_mxfp4_expert({**e, "gate_up_blocks": gb, "gate_up_scales": gs, "down_blocks": db, "down_scales": ds},
+                             layout)
+
+
 # ----------------------------------------------------------------------------- GGUF experts
 def gguf_layout(hidden: int, inter: int, gate_type: int, up_type: int, down_type: int) -> TensorLayout:
     """gate || up || down raw bytes (tinyserve/mmap_store.py:86-91)."""
