@@ -34,6 +34,64 @@ from tinyserve_amd import _lib, ops, synth  # noqa: E402
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+COPY_ELEMS = 64 << 20  # calibration copy: 64 Mi float32 read + written (256 MiB each way)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_calibration(dev) -> None:
+    """A plain elementwise copy of known size (reads and writes 4 * COPY_ELEMS bytes),
+    launched three times so that a rocprofv3 --pmc pass can scale FETCH_SIZE/WRITE_SIZE."""
+    a = torch.ones(COPY_ELEMS, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    del a, b
+
+
+def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, counter value per dispatch) from a rocprofv3 --output-format csv run."""
+    import csv
+    import glob
+
+    rows = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name") == counter:
+                    rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+    return rows
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str, kernel_key: str, workload: int, command: str) -> dict:
+    """Calibrated HBM bytes per launch of the kernel whose name contains kernel_key."""
+    out = {"workload": workload, "kernel": kernel_key, "command": command}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(d, counter)
+        copy = [v for k, v in rows if "MulFunctor" in k]  # torch.mul's elementwise kernel
+        kern = [v for k, v in rows if kernel_key in k]
+        if not copy or not kern:
+            raise SystemExit(f"{counter}: no calibration copy ({len(copy)}) or {kernel_key} ({len(kern)}) dispatches in {d}")
+        copy_kib = max(copy)  # the 256 MiB copy is the largest elementwise dispatch
+        factor = copy_kib * 1024.0 / (4.0 * COPY_ELEMS)
+        out[counter] = {"kib_per_dispatch": float(np.mean(kern)), "dispatches": len(kern),
+                        "copy_kib": copy_kib, "copy_factor": factor,
+                        "bytes_per_launch": float(np.mean(kern)) * 1024.0 / factor}
+    out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    return out
+
+
+def load_traffic(workload: int, kernel_key: str):
+    try:
+        import json as _json
+
+        with open(TRAFFIC_FILE) as fh:
+            t = _json.load(fh)
+        if t.get("workload") == workload and t.get("kernel") == kernel_key:
+            return t
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def _bf16(bits: np.ndarray, dev) -> torch.Tensor:
@@ -163,7 +221,21 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--checkpoint-order", action="store_true",
                     help="workload 3: keep the experts in the checkpoint order (the slower row-major kernel)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="launch a 256 MiB copy first (for rocprofv3 --pmc traffic calibration)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc csv runs (no GPU work)")
+    ap.add_argument("--pmc-command", default="", help="the profiled command, recorded with --summarize-pmc")
     args = ap.parse_args()
+    kernel_key = "mxt_decode_kernel" if args.workload == 3 and not args.checkpoint_order else (
+        "mx_decode_kernel" if args.workload == 3 else "gguf_phase")
+    if args.summarize_pmc:
+        t = summarize_pmc(*args.summarize_pmc, kernel_key, args.workload, args.pmc_command)
+        os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+        with open(TRAFFIC_FILE, "w") as fh:
+            json.dump(t, fh, indent=1)
+        print(json.dumps(t))
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
         return 2
@@ -171,6 +243,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     K, W = args.steps, args.warmup
     n_layers = args.layers
+    if args.copy_calibration:
+        copy_calibration(dev)
     wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev, tiled=not args.checkpoint_order)
     torch.cuda.synchronize()
 
@@ -242,6 +316,13 @@ def main() -> int:
                     "included)",
         },
     }
+    tr = load_traffic(args.workload, kernel_key)
+    if tr:
+        line["roofline"]["traffic"] = round(tr["traffic_bytes_per_launch"])
+        line["roofline"]["traffic_note"] = (
+            f"HBM bytes per launch of {kernel_key} from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the "
+            f"counter's reading for a {4 * COPY_ELEMS >> 20} MiB copy (factors {tr['FETCH_SIZE']['copy_factor']:.3f}, "
+            f"{tr['WRITE_SIZE']['copy_factor']:.3f}); algorithmic bytes {nbytes}")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(line))
