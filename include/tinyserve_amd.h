@@ -111,8 +111,8 @@ int tsa_mxfp4_tile_sizes(int64_t N, int64_t K, int64_t* blocks_bytes, int64_t* s
  * [N, K/32]) into the 16-row MFMA tile order: tile r = rows 16r..16r+15 is 8*K
  * contiguous bytes whose 1 KB piece m holds, at 16*(16*q + i), the 16-byte block 4m+q
  * of row 16r+i (a wave's 16-byte-per-lane load of piece m is one MFMA operand); the
- * scale of that block is byte m%4 of the 32-bit word (m/4, lane 16q+i) of the tile's
- * scale area. Out-of-place; the caller owns both outputs. Used when experts are
+ * scale of that block is byte m%4 of 32-bit word m/4 of lane 16q+i, each lane's words
+ * stored in lane-major chunks of up to 4 words (see mx_tile.hip). Out-of-place; the caller owns both outputs. Used when experts are
  * copied into the resident pool (the reference copies the checkpoint bytes as they are:
  * ExpertStore.copy_to_buffer_slot / copy_to_buffer, tinyserve/expert_store.py:532-560). */
 int tsa_mxfp4_tile(const void* blocks, const void* scales, int64_t N, int64_t K,

@@ -20,12 +20,13 @@
 //     waves' weighted rows are summed in a fixed order in LDS, so each output has one
 //     writer and the result is deterministic.
 //
-// Synchronisation (same scheme as the checkpoint-order kernel in moe_decode_mx.hip):
-// before a wave first reads h of pair (t, j) it polls that pair's counter, after issuing
-// the task's weight loads so that the wait overlaps HBM traffic; the grid never exceeds
-// the co-resident workgroup count and phase A work precedes every poll, so every wait
-// ends; the spin limit is a backstop that raises the workspace error flag. The last
-// phase B workgroup out resets the counters.
+// Synchronisation: per-(token, expert) completion counters as in moe_decode_mx.hip, but
+// only wave 0 of a phase B workgroup polls (the token's k counters, spaced by s_sleep),
+// after every wave has issued its down-tile loads, and the others wait at a barrier:
+// hundreds of waves polling the same few lines with agent-scope loads measurably slowed
+// the weight stream. The grid never exceeds the co-resident workgroup count and phase A
+// work precedes every poll, so every wait ends; the spin limit is a backstop that raises
+// the workspace error flag. The last phase B workgroup out resets the counters.
 //
 // Semantics: tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases, clamped
 // SwiGLU), :456-473 (routing), tinyserve/csrc/expert_loop.cpp:83-121 (weighted sum).
@@ -93,6 +94,10 @@ struct Tile {
     uint32_t sc[MS];
 };
 
+// The scale words (W per lane, W = stile_bytes / 256 <= MS) come in lane-major chunks of
+// up to 4 words: one 16-byte load per chunk, bounded to the tile's scale area. A load
+// wider than a lane's part of a chunk picks up the next lane's words; words >= W are
+// zeroed, so they can only meet the zero blocks of groups past the row end.
 template <int MM>
 __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, int64_t tile_bytes,
                                           const uint8_t* scales, int64_t stile_bytes, int lane) {
@@ -100,8 +105,14 @@ __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, i
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(blocks), (short)0, (int)tile_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(scales), (short)0, (int)stile_bytes, 0x00020000);
+    const int W = (int)(stile_bytes >> 8);
 #pragma unroll
-    for (int u = 0; u < Tile<MM>::MS; ++u) tl.sc[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 256 * u + 4 * lane, 0, 0);
+    for (int c = 0; c < (Tile<MM>::MS + 3) / 4; ++c) {
+        const int wc = W - 4 * c < 4 ? (W - 4 * c > 0 ? W - 4 * c : 0) : 4;  // this chunk's words per lane
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 * c + 4 * wc * lane, 0, 0));
+#pragma unroll
+        for (int d = 0; d < 4 && 4 * c + d < Tile<MM>::MS; ++d) tl.sc[4 * c + d] = 4 * c + d < W ? v[d] : 0u;
+    }
     __builtin_amdgcn_sched_barrier(0);
     // Every piece is issued, in order, before any is used: left alone the scheduler sinks
     // loads into the MFMA loop to save registers (a third of the tile in flight) or
@@ -113,24 +124,33 @@ __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, i
     }
 }
 
-// Rows 4q..4q+3 of W_tile * v (lane 16q+i, any i), v a zero-padded bf16 vector [128 MM]
-// in LDS. Four accumulators keep consecutive MFMAs independent.
+// Rows 4q..4q+3 of W_tile * v (lanes 16q+i; the result is in lane 16q), v a zero-padded
+// bf16 vector [128 MM] in LDS. Only B column 0 is needed, so only lanes 0, 16, 32, 48 read
+// their 8 activations (exec-masked): the other lanes keep stale values, which only reach
+// result columns 1..15. (A full-wave broadcast read returns 1 KB into VGPRs per 16-byte
+// useful read and slowed the concurrent weight stream.) Two accumulators alternate so
+// that consecutive MFMAs are independent.
 template <int MM>
 __device__ __forceinline__ v4f tile_mfma(const Tile<MM>& tl, const uint8_t* vec, int lane) {
-    v4f acc[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    v4f acc[2];
+    acc[0] = acc[1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const uint8_t* vb = vec + 64 * (lane >> 4);  // K-slice q of piece m: values 128 m + 32 q ..
+    const bool col0 = (lane & 15) == 0;
+    bf16x8 b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[u] = bf16x8{};
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
         const float s = e8m0_to_f32((tl.sc[m >> 2] >> (8 * (m & 3))) & 255u);
+        if (col0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(vb + 256 * m + 16 * u);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(expand(tl.q[m][u], s), b, acc[u], 0, 0, 0);
+            for (int u = 0; u < 4; ++u) b[u] = *reinterpret_cast<const bf16x8*>(vb + 256 * m + 16 * u);
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            acc[u & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(expand(tl.q[m][u], s), b[u], acc[u & 1], 0, 0, 0);
     }
-    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    return acc[0] + acc[1];
 }
 
 // Bias rows r0..r0+3 of an n-row bias vector: the raw 16 bytes at row r0 (a bounded
@@ -248,7 +268,7 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
 
     // ---- phase B: down tiles of every selected expert, weighted sum in a fixed order
     bool did_b = false;
-    uint64_t ready = 0;  // pairs t*k+j whose h this wave has seen complete (wave-uniform)
+    unsigned tok_ready = 0;  // tokens whose k pairs this workgroup has seen complete (workgroup-uniform)
     const int RB = H / 16;
     const int rounds = (k + WAVES - 1) / WAVES;
     uint8_t* hs = vec + wave * KP * 2;
@@ -263,29 +283,41 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
             const int j = rd * WAVES + wave;
             const int64_t slot = j < k ? uniform(s_slot[t * k + j]) : -1;
             const bool live = slot >= 0 && slot < p.n_slots;
+            const bool hb = L.down_bias_off >= 0;
+            const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
+            const int64_t tile = n0 / 16;
+            u32x4 braw = u32x4{0u, 0u, 0u, 0u};
+            Tile<MM> tl;
             if (live) {
-                const uint8_t* base = p.pool + slot * L.slot_bytes;
-                const int64_t tile = n0 / 16;
-                const bool hb = L.down_bias_off >= 0;
-                u32x4 braw = u32x4{0u, 0u, 0u, 0u};
                 if (hb) braw = bias_raw(base + L.down_bias_off, L.bias_dtype, (int64_t)H, n0 + 4 * q);
-                Tile<MM> tl;
                 tile_load<MM>(tl, base + L.down_off + tile * p.dn_tile, p.dn_tile,
                               base + L.down_scales_off + tile * p.dn_stile, p.dn_stile, lane);
-                const int pair = t * k + j;
-                if (!((ready >> pair) & 1)) {  // the task's weights are in flight already
-                    unsigned* c = pair_ctr(p.bar, pair);
-                    int spins = 0;
-                    while (ld_relaxed(c) < need) {
-                        __builtin_amdgcn_s_sleep(4);
-                        if (++spins > SPIN_LIMIT) {
-                            __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            s_flag[0] = 1;
-                            break;
+            }
+            if (rd == 0 && !((tok_ready >> t) & 1)) {
+                // The round's weights are in flight; wave 0 alone waits for the token's k pairs
+                // (one poller per workgroup: polls of hot counter lines compete with the
+                // weight stream, so they are few and spaced), the others wait at the barrier.
+                if (wave == 0) {
+                    for (int jj = 0; jj < k; ++jj) {
+                        const int sj = uniform(s_slot[t * k + jj]);
+                        if (sj < 0 || sj >= p.n_slots) continue;  // a dead pair's h is never read
+                        unsigned* c = pair_ctr(p.bar, t * k + jj);
+                        int spins = 0;
+                        while (ld_relaxed(c) < need) {
+                            __builtin_amdgcn_s_sleep(8);
+                            if (++spins > SPIN_LIMIT) {
+                                __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                s_flag[0] = 1;
+                                break;
+                            }
                         }
                     }
-                    ready |= 1ull << pair;
                 }
+                __syncthreads();
+                tok_ready |= 1u << t;
+            }
+            if (live) {
+                const int pair = t * k + j;
                 // h of (t, j) -> this wave's LDS area (sc1: coherent with other XCDs' stores)
                 stage_vec<16>(hs, p.h + (int64_t)pair * I, I, KP, lane, 64);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");

@@ -11,22 +11,25 @@
 //   tile r (rows 16r..16r+15) = 256*G bytes, G = K/32 blocks per row;
 //   block b of row 16r+i at tile offset 1024*(b/4) + 16*(16*(b%4) + i)
 //   (a short last group just ends early, so the tile is dense);
-//   its e8m0 scale at tile-scale offset 256*(b/16) + 4*(16*(b%4) + i) + (b/4)%4, the
-//   tile-scale area being 256 * ceil(ceil(G/4)/4) bytes, zero where no block exists.
+//   its e8m0 scale is byte m%4 (m = b/4) of 32-bit word w = m/4 of lane l = 16*(b%4) + i;
+//   a lane's W = ceil(ceil(G/4)/4) words are stored in chunks of 4: chunk c = w/4 holds
+//   words 4c..4c+3 of every lane, lane-major, each lane's part width min(4, W - 4c) words,
+//   so a wave fetches all its scales with one 16-byte (and one shorter) load per lane.
+//   The tile-scale area is 256 * W bytes, zero where no block exists.
 #include "tsa_common.h"
 
 namespace tsa {
 
 int64_t mx_tile_groups(int64_t K) { return (K / 32 + 3) / 4; }              // MFMA groups per row tile
-int64_t mx_tile_scale_bytes(int64_t K) { return 256 * ((mx_tile_groups(K) + 3) / 4); }  // per row tile
+int64_t mx_tile_scale_words(int64_t K) { return (mx_tile_groups(K) + 3) / 4; }  // per lane
+int64_t mx_tile_scale_bytes(int64_t K) { return 256 * mx_tile_scale_words(K); }  // per row tile
 
 namespace {
 
 // One thread per (row, block): moves 16 bytes and one scale byte.
 __global__ void __launch_bounds__(256) mx_tile_kernel(const uint8_t* __restrict__ blocks,
                                                       const uint8_t* __restrict__ scales, int64_t N, int64_t G,
-                                                      int64_t stile, uint8_t* __restrict__ tb,
-                                                      uint8_t* __restrict__ ts) {
+                                                      int64_t W, uint8_t* __restrict__ tb, uint8_t* __restrict__ ts) {
     const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= N * G) return;
     const int64_t n = c / G, b = c % G;
@@ -34,7 +37,8 @@ __global__ void __launch_bounds__(256) mx_tile_kernel(const uint8_t* __restrict_
     const int64_t lanepos = 16 * (b % 4) + i;
     const uint4 v = *reinterpret_cast<const uint4*>(blocks + 16 * c);
     *reinterpret_cast<uint4*>(tb + r * 256 * G + 1024 * (b / 4) + 16 * lanepos) = v;
-    ts[r * stile + 256 * (b / 16) + 4 * lanepos + (b / 4) % 4] = scales[c];
+    const int64_t w = b / 16, ch = w / 4, width = W - 4 * ch < 4 ? W - 4 * ch : 4;
+    ts[r * 256 * W + 1024 * ch + 4 * width * lanepos + 4 * (w % 4) + (b / 4) % 4] = scales[c];
 }
 
 }  // namespace
@@ -65,7 +69,7 @@ extern "C" int tsa_mxfp4_tile(const void* blocks, const void* scales, int64_t N,
     const int64_t G = K / 32, n = N * G;
     hipLaunchKernelGGL(mx_tile_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        static_cast<const uint8_t*>(blocks), static_cast<const uint8_t*>(scales), N, G,
-                       mx_tile_scale_bytes(K), static_cast<uint8_t*>(tiled_blocks), static_cast<uint8_t*>(tiled_scales));
+                       mx_tile_scale_words(K), static_cast<uint8_t*>(tiled_blocks), static_cast<uint8_t*>(tiled_scales));
     TSA_LAUNCH_CHECK();
     return TSA_OK;
 }

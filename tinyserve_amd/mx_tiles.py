@@ -15,9 +15,14 @@ def tile_groups(K: int) -> int:
     return (K // 32 + 3) // 4
 
 
+def tile_scale_words(K: int) -> int:
+    """32-bit scale words per lane of a 16-row tile (byte m % 4 of word m // 4 = group m)."""
+    return (tile_groups(K) + 3) // 4
+
+
 def tile_scale_bytes(K: int) -> int:
-    """Scale bytes per 16-row tile (per-lane 32-bit words, zero-padded)."""
-    return 256 * ((tile_groups(K) + 3) // 4)
+    """Scale bytes per 16-row tile (64 lanes' words, zero-padded)."""
+    return 256 * tile_scale_words(K)
 
 
 def tile_sizes(N: int, K: int) -> tuple[int, int]:
@@ -35,7 +40,11 @@ def tile_offsets(N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
     r, i = n // 16, n % 16
     lane = 16 * (b % 4) + i
     boff = r * 256 * G + 1024 * (b // 4) + 16 * lane
-    soff = r * tile_scale_bytes(K) + 256 * (b // 16) + 4 * lane + (b // 4) % 4
+    W = tile_scale_words(K)
+    w = b // 16  # the lane's word holding group m = b // 4 (byte m % 4); words go in chunks of 4
+    ch = w // 4
+    width = np.minimum(4, W - 4 * ch)
+    soff = r * 256 * W + 1024 * ch + 4 * width * lane + 4 * (w % 4) + (b // 4) % 4
     return boff, soff
 
 
