@@ -13,7 +13,13 @@ capture stream, bracketed by torch.cuda.synchronize(). value = algorithmic bytes
 step / time per step (GB/s); algorithmic bytes = the 4 selected experts' weights,
 scales and biases + activations in/out + logits.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {3,4,2,1}]
+--workload 5 measures batched prefill instead: 2048 tokens x hidden 2880 through the same
+layer shape with Zipf-skewed top-4 routing, grouped by expert and run on the grouped
+MXFP4 MFMA GEMMs (one step = one whole prefill of the layer: routing, grouping, gate_up +
+SwiGLU, down, weighted combine); value = algorithmic FLOPs / time (TFLOP/s), against the
+dense bf16 MFMA peak.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {3,4,5}]
 """
 from __future__ import annotations
 
@@ -34,6 +40,7 @@ from tinyserve_amd import _lib, ops, synth  # noqa: E402
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (the prefill GEMMs run bf16 MFMA)
 COPY_ELEMS = 64 << 20  # calibration copy: 64 Mi float32 read + written (256 MiB each way)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -177,6 +184,120 @@ class MoEWorkload:
             _lib.BF16, self.idx[s].data_ptr(), self.w[s].data_ptr(), self.ws.data_ptr(), self.ws.numel(), st))
 
 
+class PrefillWorkload:
+    """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
+    2048-token prefill; one step = one layer's whole batched MoE."""
+
+    def __init__(self, n_layers: int, dev: torch.device):
+        base = synth.workload(5)
+        self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
+        lay = synth.mxfp4_tiled_layout(self.H, self.I)
+        self.L = mxfp4_expert_layout(lay, tiled=True)
+        pool0 = np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in base["experts"]])
+        g = torch.Generator(device=dev)
+        g.manual_seed(20261205)
+        self.pools = [torch.from_numpy(pool0).to(dev)]
+        for _ in range(1, n_layers):  # further layers: random nibbles, scales and biases in range
+            p = torch.randint(0, 256, pool0.shape, dtype=torch.uint8, device=dev, generator=g)
+            MoEWorkload._fix_scales(p, lay, g)
+            self.pools.append(p)
+        self.logits = torch.from_numpy(base["logits"]).to(dev)
+        self.x = _bf16(base["x_bits"], dev)
+        self.T = self.x.shape[0]
+        self.y = torch.empty_like(self.x)
+        self.idx = torch.empty((self.T, self.k), dtype=torch.int32, device=dev)
+        self.w = torch.empty((self.T, self.k), dtype=torch.float32, device=dev)
+        self.expert_slot = torch.arange(self.E, dtype=torch.int32, device=dev)
+        self.ws = ops.moe_prefill_workspace(self.L, self.T, self.k, self.E, dev)
+        self.n_layers = n_layers
+
+    def flops_per_step(self) -> int:
+        """2 x (gate_up 2I x H + down H x I) multiply-adds per (token, expert) assignment."""
+        return 2 * self.T * self.k * (2 * self.I * self.H + self.H * self.I)
+
+    def step(self, s: int) -> None:
+        lib = _lib.load()
+        st = torch.cuda.current_stream().cuda_stream
+        pool = self.pools[s % self.n_layers]
+        _lib.check(lib.tsa_route_topk(self.logits.data_ptr(), _lib.F32, self.T, self.E, self.k,
+                                      ops.ROUTE_MODES["topk_then_softmax"], self.idx.data_ptr(), self.w.data_ptr(), st))
+        _lib.check(lib.tsa_moe_prefill(
+            ctypes.byref(self.L), pool.data_ptr(), pool.shape[0], self.expert_slot.data_ptr(), self.E,
+            self.idx.data_ptr(), self.w.data_ptr(), self.T, self.k, self.x.data_ptr(), _lib.BF16, self.y.data_ptr(),
+            _lib.BF16, self.ws.data_ptr(), self.ws.numel(), st))
+
+
+def cpu_baseline_prefill(budget_s: float = 15.0) -> dict:
+    """The oracle's grouped prefill (per expert: numpy dequant of its weights, fp32 BLAS
+    matmuls over its tokens, weighted scatter) on a bounded sample of the workload's
+    tokens, as TFLOP/s."""
+    from threadpoolctl import threadpool_info
+
+    from oracle import expert as oex
+
+    wl = synth.workload(5)
+    idx, w = oex.route_topk_then_softmax(wl["logits"], wl["top_k"])
+    H, I = wl["hidden"], wl["inter"]
+    n_tok = 128
+    x = synth.bf16_to_f32(wl["x_bits"][:n_tok])
+    fwd = lambda e, xx: oex.mxfp4_expert_forward(xx, wl["experts"][e])  # noqa: E731
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        oex.moe_combine_grouped(x, idx[:n_tok], w[:n_tok], fwd)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    flops = 2 * n_tok * wl["top_k"] * 3 * H * I
+    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"{len(times)} grouped prefills of the first {n_tok} of the workload's tokens (median "
+                      f"{med * 1e3:.0f} ms; numpy dequant of each routed expert + fp32 BLAS matmuls)"}
+
+
+def run_prefill(args, dev) -> int:
+    wl = PrefillWorkload(args.layers_prefill, dev)
+    K, W = args.steps, args.warmup
+    for s in range(W):
+        wl.step(s)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for s in range(K):
+            wl.step(s)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / K
+    tflops = wl.flops_per_step() / (ms_step * 1e-3) / 1e12
+    line = {
+        "metric": "MoE batched-prefill grouped MXFP4 expert GEMM TFLOP/s",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_step, 4),
+        "tokens_per_s": round(wl.T / (ms_step * 1e-3)),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 weights expanded exactly to bf16, bf16 activations, bf16 MFMA, fp32 accumulate",
+        "data": f"synthetic: seeded workload-5 layer + {args.layers_prefill - 1} random layers rotated per step",
+        "config": {"workload": "gpt-oss-20b-shaped mxfp4 moe layer prefill (2048 tokens, hidden 2880, 32 experts, "
+                               "zipf top-4)", "flops_per_step": wl.flops_per_step(), "tokens": wl.T},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "note": "whole step (routing, grouping, both GEMMs, combine) per HIP-event time"},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_prefill()
+    print(json.dumps(line))
+    return 0
+
+
 def cpu_baseline(wl_id: int, budget_s: float = 12.0) -> dict:
     """The oracle (numpy restatement of the reference CPU path: full dequant of the
     selected experts, then fp32 matmuls) timed on this host, one token of one layer."""
@@ -215,7 +336,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
-    ap.add_argument("--workload", type=int, default=3, choices=[3, 4])
+    ap.add_argument("--workload", type=int, default=3, choices=[3, 4, 5])
+    ap.add_argument("--layers-prefill", type=int, default=3, help="workload 5: distinct layers rotated per step")
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -241,6 +363,12 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == 5:
+        if "--steps" not in sys.argv:
+            args.steps = 20
+        if "--warmup" not in sys.argv:
+            args.warmup = 3
+        return run_prefill(args, dev)
     K, W = args.steps, args.warmup
     n_layers = args.layers
     if args.copy_calibration:

@@ -4,77 +4,104 @@
 
 namespace tsa {
 int validate_layout(const tsa_expert_layout* L);
+bool pf_mxt_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k);
+int64_t pf_mxt_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int64_t E);
+int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot,
+                   int64_t E, const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y,
+                   int y_dtype, uint8_t* ws, hipStream_t stream);
 
 namespace {
 
-constexpr int GROUP_THREADS = 1024;
+constexpr int GROUP_THREADS = 512;
 constexpr int GROUP_WAVES = GROUP_THREADS / 64;
 constexpr int MAX_GROUP_E = 1024;
 
-// Single-workgroup stable counting sort of assignment ids by expert.
-// Pass 1 counts; pass 2 walks the assignments in rounds of 1024 (in order), ranks
-// each one among equal experts of lower index inside its wave (ballot), then across
-// the waves of the round (per-wave distinct-expert counts in LDS), then across rounds
-// (running offsets), so the result is token-major within every expert.
+// Lanes of the wave holding the same expert as this lane (e >= 0; lanes with e < 0 are in
+// no group), found with one ballot per bit of the expert id instead of a loop over the
+// distinct experts.
+__device__ __forceinline__ unsigned long long peers(int e, int nbits) {
+    unsigned long long m = __ballot(e >= 0);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const unsigned long long v = __ballot(bit);
+        m &= bit ? v : ~v;
+    }
+    return m;
+}
+
+// Single-workgroup stable counting sort of assignment ids by expert. Wave w owns one
+// contiguous chunk of the assignments (a multiple of 64 long) and walks it in batches of
+// 64. Pass 1 counts per (wave, expert) in LDS: the lowest lane of each group of equal
+// experts in a batch adds the group's size (a wave owns its row of counters, so no
+// atomics). An exclusive scan over the waves, per expert, then gives each wave its first
+// rank inside the expert, and a scan over the experts the offsets. Pass 2 walks the same
+// batches in the same order and places each assignment at offset + the wave's running
+// rank + its rank among the group's lanes, so every expert's run keeps assignment order
+// (token-major), as the reference's grouping does.
 __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __restrict__ idx, int64_t n, int E,
                                                               int32_t* __restrict__ counts,
                                                               int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ perm) {
-    __shared__ int cnt[MAX_GROUP_E];
-    __shared__ int run[MAX_GROUP_E];
-    __shared__ int wave_cnt[GROUP_WAVES][64];
-    __shared__ int wave_eid[GROUP_WAVES][64];
-    __shared__ int wave_nuniq[GROUP_WAVES];
+    __shared__ int wcnt[GROUP_WAVES][MAX_GROUP_E];
+    __shared__ int eoff[MAX_GROUP_E];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += GROUP_THREADS) cnt[e] = 0;
+    const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int i = tid; i < GROUP_WAVES * MAX_GROUP_E; i += GROUP_THREADS) (&wcnt[0][0])[i] = 0;
     __syncthreads();
-    for (int64_t a = tid; a < n; a += GROUP_THREADS) {
-        const int e = idx[a];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {  // exclusive scan; E <= 1024 so a serial scan is negligible
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            offsets[e] = acc;
-            counts[e] = cnt[e];
-            run[e] = acc;
-            acc += cnt[e];
-        }
-        offsets[E] = acc;
-    }
-    __syncthreads();
-    for (int64_t base = 0; base < n; base += GROUP_THREADS) {
-        const int64_t a = base + tid;
-        int e = a < n ? idx[a] : -1;
+    const int64_t chunk = ((n + GROUP_WAVES - 1) / GROUP_WAVES + 63) / 64 * 64;
+    const int64_t a0 = wave * chunk, a1 = a0 + chunk < n ? a0 + chunk : n;
+    for (int64_t b = a0; b < a1; b += 64) {
+        const int64_t a = b + lane;
+        int e = a < a1 ? idx[a] : -1;
         if (e >= E) e = -1;
-        unsigned long long remaining = __ballot(e >= 0);
-        int my_rank = 0, nuniq = 0;
-        while (remaining) {
-            const int leader = __ffsll((unsigned long long)remaining) - 1;
-            const int le = __shfl(e, leader, 64);
-            const unsigned long long m = __ballot(e == le) & remaining;
-            if (e == le) my_rank = __popcll(m & ((1ull << lane) - 1ull));
-            if (lane == 0) {
-                wave_eid[wave][nuniq] = le;
-                wave_cnt[wave][nuniq] = __popcll(m);
+        const unsigned long long m = peers(e, nbits);
+        if (e >= 0 && !(m & below)) wcnt[wave][e] += __popcll(m);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += GROUP_THREADS) {
+        int run = 0;
+        for (int w = 0; w < GROUP_WAVES; ++w) {
+            const int c = wcnt[w][e];
+            wcnt[w][e] = run;
+            run += c;
+        }
+        eoff[e] = run;
+    }
+    __syncthreads();
+    if (wave == 0) {  // offsets: exclusive scan of the totals, 16 experts per lane at most
+        const int per = (E + 63) / 64;
+        int loc = 0;
+        for (int j = 0; j < per; ++j)
+            if (lane * per + j < E) loc += eoff[lane * per + j];
+        int inc = loc;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(inc, d, 64);
+            if (lane >= d) inc += v;
+        }
+        int run = inc - loc;
+        for (int j = 0; j < per; ++j) {
+            const int e = lane * per + j;
+            if (e < E) {
+                const int c = eoff[e];
+                counts[e] = c;
+                offsets[e] = run;
+                eoff[e] = run;
+                run += c;
             }
-            remaining &= ~m;
-            ++nuniq;
         }
-        if (lane == 0) wave_nuniq[wave] = nuniq;
-        __syncthreads();
+        if (lane == 63) offsets[E] = inc;
+    }
+    __syncthreads();
+    for (int64_t b = a0; b < a1; b += 64) {
+        const int64_t a = b + lane;
+        int e = a < a1 ? idx[a] : -1;
+        if (e >= E) e = -1;
+        const unsigned long long m = peers(e, nbits);
         if (e >= 0) {
-            int before = 0;  // same expert in earlier waves of this round
-            for (int w = 0; w < wave; ++w)
-                for (int u = 0; u < wave_nuniq[w]; ++u)
-                    if (wave_eid[w][u] == e) before += wave_cnt[w][u];
-            perm[run[e] + before + my_rank] = (int32_t)a;
+            perm[eoff[e] + wcnt[wave][e] + __popcll(m & below)] = (int32_t)a;
+            if (!(m & below)) wcnt[wave][e] += __popcll(m);  // after every lane of the group read it
         }
-        __syncthreads();
-        if (lane == 0)
-            for (int u = 0; u < nuniq; ++u) atomicAdd(&run[wave_eid[wave][u]], wave_cnt[wave][u]);
-        __syncthreads();
     }
 }
 
@@ -88,6 +115,14 @@ __global__ void __launch_bounds__(256) map_slots_kernel(const int32_t* __restric
 }
 
 }  // namespace
+
+int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                        hipStream_t stream) {
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, stream, idx, n, E, counts, offsets, perm);
+    TSA_LAUNCH_CHECK();
+    return TSA_OK;
+}
+
 }  // namespace tsa
 
 using namespace tsa;
@@ -100,16 +135,23 @@ extern "C" int tsa_group_by_expert(const int32_t* idx, int64_t T, int k, int64_t
                 MAX_GROUP_E);
     TSA_REQUIRE(T * k < (int64_t)1 << 31, TSA_ERR_SHAPE, "too many assignments");
     TSA_REQUIRE(idx && counts && offsets && (perm || T == 0), TSA_ERR_INVALID_ARG, "null pointer");
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, as_stream(stream), idx, T * k, (int)E, counts,
-                       offsets, perm);
-    TSA_LAUNCH_CHECK();
-    return TSA_OK;
+    return launch_group_kernel(idx, T * k, (int)E, counts, offsets, perm, as_stream(stream));
 }
 
-static int64_t prefill_ws(const tsa_expert_layout& L, int64_t T, int k) {
+// Workspace of the token-chunked decode path: the assignments' slots, then a decode workspace.
+static int64_t chunked_ws(const tsa_expert_layout& L, int64_t T, int k) {
     int64_t dec = 0;
     tsa_moe_decode_workspace_size(&L, T, k, &dec);
     return ((T * k * 4 + 255) / 256) * 256 + dec;
+}
+
+// MXFP4 tiled pools with bf16 activations take the grouped MFMA GEMMs; every other
+// layout runs the fused decode kernel over chunks of tokens.
+static int64_t prefill_ws(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
+    const int64_t c = chunked_ws(L, T, k);
+    if (L.format != TSA_EXPERT_MXFP4 || !L.mx_tiled) return c;
+    const int64_t g = pf_mxt_workspace_bytes(L, T, k, E);
+    return g > c ? g : c;
 }
 
 extern "C" int tsa_moe_prefill_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t E,
@@ -118,7 +160,7 @@ extern "C" int tsa_moe_prefill_workspace_size(const tsa_expert_layout* layout, i
     int rc = validate_layout(layout);
     if (rc) return rc;
     TSA_REQUIRE(T >= 0 && k >= 1 && E >= 1 && bytes, TSA_ERR_INVALID_ARG, "bad T/k/E/bytes");
-    *bytes = prefill_ws(*layout, T, k);
+    *bytes = prefill_ws(*layout, T, k, E);
     return TSA_OK;
 }
 
@@ -132,9 +174,16 @@ extern "C" int tsa_moe_prefill(const tsa_expert_layout* layout, const void* pool
     TSA_REQUIRE(T >= 0 && k >= 1 && E >= 1, TSA_ERR_INVALID_ARG, "bad T/k/E");
     if (T == 0) return TSA_OK;
     TSA_REQUIRE(expert_slot && idx && weights, TSA_ERR_INVALID_ARG, "null pointer");
-    const int64_t need = prefill_ws(*layout, T, k);
+    TSA_REQUIRE(E <= 1024, TSA_ERR_SHAPE, "E %lld exceeds 1024", (long long)E);
+    const int64_t need = prefill_ws(*layout, T, k, E);
     TSA_REQUIRE(workspace && workspace_bytes >= need, TSA_ERR_WORKSPACE, "workspace too small: got %lld bytes, need %lld",
                 (long long)workspace_bytes, (long long)need);
+    if (pf_mxt_supported(*layout, x_dtype, T, k)) {
+        TSA_REQUIRE(x && y, TSA_ERR_INVALID_ARG, "null pointer");
+        return pf_mxt_prefill(*layout, static_cast<const uint8_t*>(pool), n_slots, expert_slot, E, idx, weights, T, k,
+                              static_cast<const uint16_t*>(x), y, y_dtype, static_cast<uint8_t*>(workspace),
+                              as_stream(stream));
+    }
     int32_t* slots = static_cast<int32_t*>(workspace);
     const int64_t off = ((T * k * 4 + 255) / 256) * 256;
     hipLaunchKernelGGL(map_slots_kernel, dim3((unsigned)((T * k + 255) / 256)), dim3(256), 0, as_stream(stream), idx,

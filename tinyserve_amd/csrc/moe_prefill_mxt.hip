@@ -1,0 +1,504 @@
+// Batched (prefill) MoE over MXFP4 experts in the 16-row MFMA tile order: the grouped
+// expert GEMMs on the matrix cores.
+//
+// After the (token, expert) assignments are sorted expert-major (group_kernel), each
+// expert's rows form one contiguous run of the sorted order, cut into tiles of up to 128
+// rows (pf_table_kernel). Two persistent GEMM launches then cover every (row tile, weight
+// tile) pair:
+//   gate_up: h[i, :] = SwiGLU(x[token(i)] W_gu^T + b_gu), bf16, in sorted order;
+//   down:    yk[a, :] = h[i] W_dn^T + b_dn, bf16, by assignment id a = perm[i]
+// (bf16 like the reference's per-expert outputs), and a combine pass forms
+// y[t] = sum_j w[t, j] yk[t k + j] over j in order, so every output has one writer and the
+// result does not depend on scheduling.
+//
+// GEMM workgroup: 8 waves, a 256-weight-row x 128-token tile; wave (wn, wt) owns 64 rows
+// x 64 tokens = 2 x 2 blocks of v_mfma_f32_32x32x16_bf16 (that form issues at the bf16
+// peak with 4 independent chains per wave; 16x16x32 needs about 16). K advances in 128-wide
+// pieces. Weights are the A operand: the MXFP4 16-row tile order delivers a 16-row piece
+// as one contiguous 1 KB, which v_cvt_scalef32_pk_bf16_fp4 expands exactly (scale folded
+// in). Activations are the B operand. Both reach LDS by direct buffer-to-LDS loads issued
+// ahead of use (weights, which mostly come from HBM or the MALL, 4 pieces ahead in a 5-deep
+// ring; activations, which mostly hit L2, 1 piece ahead), with one wait + barrier per piece.
+// Workgroups are persistent, one per CU; the tile list is split into 8 contiguous ranges,
+// one per XCD (workgroup b runs on XCD b % 8), in row-tile-major order, so the workgroups
+// running together on an XCD share the row tile's activations in its L2.
+//
+// Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
+// weighted scatter), tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases,
+// clamped SwiGLU).
+#include <mutex>
+
+#include "fused_common.h"
+#include "mfma_tile.h"
+
+namespace tsa {
+
+int64_t mx_tile_scale_bytes(int64_t K);
+
+namespace {
+
+constexpr int PF_THREADS = 512;
+constexpr int PF_BM = 128;                        // sorted rows (tokens) per workgroup tile
+constexpr int PF_BN = 256;                        // weight rows per workgroup tile
+constexpr int PF_XST = 2;                         // activation stages (mostly L2 hits)
+constexpr int PF_WST = 5;                         // weight stages (from HBM / MALL: issued further ahead)
+constexpr int PF_XAHEAD = PF_XST - 1;
+constexpr int PF_WAHEAD = PF_WST - 1;
+static_assert(PF_WAHEAD > PF_XAHEAD && PF_WAHEAD < 5, "weights of piece i must be issued before its activations");
+constexpr int PF_XBYTES = PF_BM * 128 * 2;        // a piece of bf16 activations: 32 KB
+constexpr int PF_WBYTES = (PF_BN / 16) * 1024;    // a piece of MXFP4 weights: 16 KB
+constexpr int PF_SBYTES = (PF_BN / 16) * 256;     // one scale word per lane of every row tile: 4 KB
+constexpr int PF_WOFF = PF_XST * PF_XBYTES;
+constexpr int PF_SOFF = PF_WOFF + PF_WST * PF_WBYTES;
+constexpr int PF_LDS = PF_SOFF + 2 * PF_SBYTES;   // 152 KB
+
+struct PfEntry {
+    int slot, row0, rows, expert;
+};
+
+struct PfGemm {
+    tsa_expert_layout L;
+    const uint8_t* pool;
+    const int* n_entries;     // device: valid table entries
+    const PfEntry* table;
+    const uint16_t* src;      // gate_up: x [T, K] rows gathered through perm; down: h [n, K] sorted
+    int64_t src_rows;         // rows of src (bounds of its buffer resource)
+    const int32_t* perm;      // sorted position -> assignment id (token * k + j)
+    int k;
+    uint16_t* out;            // gate_up: h [n, N / 2]; down: yk [T k, N]
+    int N, K, NT, MP;         // weight rows, reduction length, tiles along N, pieces along K
+    int64_t w_off, s_off, b_off;        // slot offsets of the tiled blocks, tiled scales, bias (< 0: none)
+    int64_t tile_bytes, stile_bytes;    // per 16-row tile
+};
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Raw buffer descriptor (base, num_records bytes; loads past the end return zero).
+__device__ __forceinline__ v4i buf_desc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+}
+
+// 16 (or 4) bytes per lane from buffer offset voff straight into LDS at lds + 16 lane (or
+// 4 lane): one contiguous 1 KB (256 B) per wave. Issued as inline assembly so that the
+// compiler does not place its conservative vmcnt(0) before every later LDS read: the K loop
+// waits for exactly what it needs (pf_wait). Loads return in order, so the compiler's own
+// waits for its loads can only get stricter, never too weak.
+__device__ __forceinline__ void pf_dma(const v4i& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void pf_dma4(const v4i& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(lds)
+                 : "memory", "m0");
+}
+
+// This wave's loads except the newest n are complete (and its LDS work), then the
+// workgroup barrier: every wave's part of the piece is in LDS, and every wave is done
+// reading the stages that are refilled next.
+#define PF_WAIT_CASE(n) \
+    case n: asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+__device__ __forceinline__ void pf_wait(int n) {
+    switch (n) {  // n above 16 waits for 16 (stricter)
+        PF_WAIT_CASE(0) PF_WAIT_CASE(1) PF_WAIT_CASE(2) PF_WAIT_CASE(3) PF_WAIT_CASE(4) PF_WAIT_CASE(5)
+        PF_WAIT_CASE(6) PF_WAIT_CASE(7) PF_WAIT_CASE(8) PF_WAIT_CASE(9) PF_WAIT_CASE(10) PF_WAIT_CASE(11)
+        PF_WAIT_CASE(12) PF_WAIT_CASE(13) PF_WAIT_CASE(14) PF_WAIT_CASE(15)
+        default: asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    }
+}
+#undef PF_WAIT_CASE
+
+// One 128-wide piece of a wave's 64-row x 64-token block on v_mfma_f32_32x32x16_bf16
+// (2 x 2 blocks of 32 x 32). K order within the piece: step j (0..7) covers, for lanes
+// 32g..32g+31, dword 2g + j%2 of MXFP4 block j/2, so a weight lane (row r, group g) reads
+// the 8 contiguous bytes at 16 (16 (j/2) + r%16) + 8g of its 16-row tile, and the
+// activation fragment (subtile, j) is one contiguous 1 KB, laid out so by the DMA. NB of
+// the 2 token subtiles are live. Lanes whose block starts at or past K get a zero weight
+// operand (past the end of a row the bytes belong to the next tile, and the activations
+// there are stand-ins).
+template <int NB>
+__device__ __forceinline__ void pf_piece(v16f (&acc)[2][2], const uint8_t* xs, const uint8_t* ws, const uint8_t* ss,
+                                         int mp, int K, int wn, int wt, int lane) {
+    const int g = lane >> 5, rr = lane & 31;
+    uint2 A[2][4];
+    float s[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int rt = 4 * wn + 2 * rb + (rr >> 4);  // row tile in the workgroup tile
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int lt = 16 * q + (rr & 15);      // the 16-row tile's lane holding this row's block q
+            A[rb][q] = *reinterpret_cast<const uint2*>(ws + rt * 1024 + 16 * lt + 8 * g);
+            s[rb][q] = e8m0_to_f32(ss[rt * 256 + 4 * lt + (mp & 3)]);
+        }
+    }
+    if (128 * (mp + 1) > K) {  // the row's last, partial piece
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (128 * mp + 32 * q >= K) A[rb][q] = make_uint2(0u, 0u);
+    }
+    // activations: token row (64 wt + 32 b + lane % 32) of the piece, chunk 4 (j / 2) + 2g + j % 2
+    // stored at slot chunk ^ (token % 16)
+    const uint8_t* xrow = xs + (64 * wt + rr) * 256;
+    auto bfrag = [&](int b, int j) {
+        const int ch = 4 * (j >> 1) + 2 * g + (j & 1);
+        return *reinterpret_cast<const bf16x8*>(xrow + b * 32 * 256 + 16 * (ch ^ (rr & 15)));
+    };
+    bf16x8 B[2][NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) B[0][b] = bfrag(b, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (j < 7) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) B[(j + 1) & 1][b] = bfrag(b, j + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's MFMAs
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const uint32_t w = (j & 1) ? A[rb][j >> 1].y : A[rb][j >> 1].x;
+            const bf16x8 Af = expand(w, s[rb][j >> 1]);
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                acc[rb][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Af, B[j & 1][b], acc[rb][b], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The K loop of one tile, as a stream of steps s = -PF_WAHEAD .. MP - 1: step s waits for
+// and multiplies piece s (s >= 0), then issues the activations of piece s + PF_XAHEAD and
+// the weights of piece s + PF_WAHEAD, in that order. The weights of piece i therefore go
+// out in an earlier step than its activations, so once this wave's loads up to X(s) are
+// complete, W(s) and its scale word are too; the loads newer than X(s) are counted
+// exactly (never fewer than issued: a wait for fewer outstanding is only stricter). NB = 0:
+// the wave has no live block in this tile and only takes part in the loads and barriers.
+template <int NB, class IX, class IW, class WL>
+__device__ __forceinline__ void pf_kloop(v16f (&acc)[2][2], IX& issue_x, IW& issue_w, WL& w_loads, int MP, int K,
+                                         int wn, int wt, int lane) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    auto x_loads = [&](int i) { return i >= 0 && i < MP ? 4 : 0; };
+    for (int st = -PF_WAHEAD; st < MP; ++st) {
+        if (st >= 0) {
+            int newer = w_loads(st - PF_XAHEAD + PF_WAHEAD);
+#pragma unroll
+            for (int u = st - PF_XAHEAD + 1; u < st; ++u) newer += x_loads(u + PF_XAHEAD) + w_loads(u + PF_WAHEAD);
+            pf_wait(newer);
+        }
+        if (st + PF_XAHEAD >= 0 && st + PF_XAHEAD < MP) issue_x(st + PF_XAHEAD);
+        if (st + PF_WAHEAD < MP) issue_w(st + PF_WAHEAD);
+        if (NB > 0 && st >= 0) {
+            const uint8_t* xs = smem + (st % PF_XST) * PF_XBYTES;
+            const uint8_t* ws = smem + PF_WOFF + (st % PF_WST) * PF_WBYTES;
+            const uint8_t* ss = smem + PF_SOFF + ((st >> 2) & 1) * PF_SBYTES;
+            pf_piece<NB ? NB : 1>(acc, xs, ws, ss, st, K, wn, wt, lane);
+        }
+    }
+}
+
+template <bool GATE_UP>
+__global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const int wn = wave & 3, wt = wave >> 2;
+    const int g = lane >> 5, rr = lane & 31;
+    const int N = p.N, K = p.K, MP = p.MP;
+    const int total = uniform(*p.n_entries) * p.NT;
+    const int xcd = blockIdx.x & 7, R = gridDim.x >> 3;
+    const int lo = (int)((int64_t)total * xcd / 8), hi = (int)((int64_t)total * (xcd + 1) / 8);
+    const int W = (int)(p.stile_bytes >> 8);  // scale words per lane
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const v4i xr = buf_desc(p.src, (uint32_t)(p.src_rows * K * 2));
+
+    for (int t = lo + (int)(blockIdx.x >> 3); t < hi; t += R) {
+        const int m = t / p.NT, nt = t % p.NT;
+        const PfEntry e = p.table[m];
+        const int slot = uniform(e.slot), row0 = uniform(e.row0), rows = uniform(e.rows);
+        const uint8_t* base = p.pool + (int64_t)slot * p.L.slot_bytes;
+
+        // Activation DMA: each instruction copies 4 whole token rows of the piece (4 x 256 B,
+        // coalesced): lanes 16 i .. 16 i + 15 carry token 4 (4 w + c) + i (c = 0..3), lane slot
+        // s = lane % 16 the row's 16-byte chunk s ^ (token % 16). The swizzle keeps the B
+        // fragment reads (one chunk of 32 tokens per lane group) free of bank conflicts.
+        // Tokens past the tile's rows re-read token 0's row (their columns are dropped).
+        uint32_t xoff[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            int tok = 16 * wave + 4 * c + (lane >> 4);
+            if (tok >= rows) tok = 0;
+            const int64_t srow = GATE_UP ? p.perm[row0 + tok] / p.k : row0 + tok;
+            xoff[c] = (uint32_t)(srow * K * 2);
+        }
+        // Weight DMA: wave w fills row tiles 2w, 2w+1 of the workgroup's 16; one resource
+        // spans the workgroup's live tiles (tiles past N read zero).
+        const int rtw = nt * (PF_BN / 16);
+        int nrw = N / 16 - rtw;
+        nrw = nrw > PF_BN / 16 ? PF_BN / 16 : nrw;
+        const v4i wr = buf_desc(base + p.w_off + (int64_t)rtw * p.tile_bytes, (uint32_t)(nrw * p.tile_bytes));
+        const uint32_t tb = (uint32_t)p.tile_bytes;
+        // Scale DMA: with the weights of the first piece of every group of 4, word mp / 4 of
+        // the same row tiles (chunked lane-major: word w of a lane at 1024 (w / 4) + 4 width
+        // lane + 4 (w % 4), width = min(4, W - 4 (w / 4))) into ring slot (mp / 4) % 2.
+        const v4i sr = buf_desc(base + p.s_off + (int64_t)rtw * p.stile_bytes, (uint32_t)(nrw * p.stile_bytes));
+        const uint32_t sb = (uint32_t)p.stile_bytes;
+        auto issue_x = [&](int mp) {
+            const uint32_t st = lds0 + (uint32_t)((mp % PF_XST) * PF_XBYTES) + 16 * wave * 256;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int tok = 16 * wave + 4 * c + (lane >> 4);
+                int kk = 128 * mp + 8 * ((lane & 15) ^ (tok & 15));
+                if (kk >= K) kk = 0;  // stand-in inside the row; its weight operand is zeroed
+                pf_dma(xr, xoff[c] + 2 * kk, st + c * 1024);
+            }
+        };
+        auto issue_w = [&](int mp) {  // 2 loads, + 2 scale loads when mp % 4 == 0
+            const uint32_t st = lds0 + PF_WOFF + (uint32_t)((mp % PF_WST) * PF_WBYTES);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                pf_dma(wr, (2 * wave + jj) * tb + 1024 * mp + 16 * lane, st + (2 * wave + jj) * 1024);
+            if ((mp & 3) == 0) {
+                const int w = mp >> 2;
+                const int wc = W - 4 * (w >> 2) < 4 ? W - 4 * (w >> 2) : 4;
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj)
+                    pf_dma4(sr, (2 * wave + jj) * sb + 1024 * (w >> 2) + 4 * wc * lane + 4 * (w & 3),
+                            lds0 + PF_SOFF + (w & 1) * PF_SBYTES + (2 * wave + jj) * 256);
+            }
+        };
+        auto w_loads = [&](int mp) { return mp >= 0 && mp < MP ? 2 + ((mp & 3) == 0 ? 2 : 0) : 0; };
+
+        // This wave's block: row tiles rtw + 4wn .. +3 (two 32-row blocks), tokens 64 wt .. +63.
+        const int rt0 = rtw + 4 * wn;
+        const bool rows_live = rt0 < N / 16;
+        int nsub = (rows - 64 * wt + 31) >> 5;
+        nsub = nsub < 0 ? 0 : (nsub > 2 ? 2 : nsub);
+        const bool active = rows_live && nsub > 0;
+
+        v16f acc[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+        // One K loop per live-subtile count, so the accumulators keep one register home
+        // (a per-piece branch made the compiler copy them after every piece).
+        if (!active) pf_kloop<0>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        else if (nsub == 2) pf_kloop<2>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        else pf_kloop<1>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        __syncthreads();  // every wave is done with the last stages before the next tile refills them
+
+        if (!active) continue;
+        // Epilogue: acc[rb][b][4u + r] is row 32 rb + 8u + 4g + r of the wave's 64 (r = 0..3),
+        // token column 64 wt + 32 b + (lane % 32).
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const int rbase = 16 * rt0 + 32 * rb;
+            if (rbase >= N) break;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int r0 = rbase + 8 * u + 4 * g;
+                if (r0 >= N) continue;  // N % 32 == 16: the block's second row tile is past N
+                v4f bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (p.b_off >= 0) bias = bias_value(bias_raw(base + p.b_off, p.L.bias_dtype, N, r0), p.L.bias_dtype);
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int tk = 64 * wt + 32 * b + rr;
+                    if (b >= nsub || tk >= rows) continue;
+                    const v4f v = v4f{acc[rb][b][4 * u], acc[rb][b][4 * u + 1], acc[rb][b][4 * u + 2], acc[rb][b][4 * u + 3]} + bias;
+                    if (GATE_UP) {
+                        const float h0 = swiglu_oai(p.L, v[0], v[1]), h1 = swiglu_oai(p.L, v[2], v[3]);
+                        const uint32_t packed = (uint32_t)f32_to_bf16_bits(h0) | ((uint32_t)f32_to_bf16_bits(h1) << 16);
+                        *reinterpret_cast<uint32_t*>(p.out + (int64_t)(row0 + tk) * (N / 2) + r0 / 2) = packed;
+                    } else {
+                        const int64_t asg = p.perm[row0 + tk];
+                        const uint32_t w0 = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+                        const uint32_t w1 = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+                        *reinterpret_cast<uint2*>(p.out + asg * N + r0) = make_uint2(w0, w1);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Tile table: expert e with a resident slot and c_e sorted rows gets ceil(c_e / 128)
+// entries (slot, first sorted row, rows, e), experts in order. E <= 1024.
+__global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restrict__ counts,
+                                                        const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ expert_slot, int E,
+                                                        int64_t n_slots, int* __restrict__ n_entries,
+                                                        PfEntry* __restrict__ table) {
+    __shared__ int pre[1024];
+    const int e = threadIdx.x;
+    int slot = -1, c = 0, nt = 0;
+    if (e < E) {
+        slot = expert_slot[e];
+        c = counts[e];
+        nt = (slot >= 0 && slot < n_slots) ? (c + PF_BM - 1) / PF_BM : 0;
+    }
+    pre[e] = nt;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
+        const int v = e >= d ? pre[e - d] : 0;
+        __syncthreads();
+        pre[e] += v;
+        __syncthreads();
+    }
+    const int start = pre[e] - nt;
+    for (int j = 0; j < nt; ++j) {
+        const int r = c - PF_BM * j;
+        table[start + j] = PfEntry{slot, offsets[e] + PF_BM * j, r < PF_BM ? r : PF_BM, e};
+    }
+    if (e == 1023) *n_entries = pre[1023];
+}
+
+// y[t] = sum_j w[t, j] yk[t k + j] over the live assignments, j in order; 8 columns per thread.
+__global__ void __launch_bounds__(256) pf_combine_kernel(const uint16_t* __restrict__ yk,
+                                                         const int32_t* __restrict__ idx,
+                                                         const float* __restrict__ w,
+                                                         const int32_t* __restrict__ expert_slot, int64_t E,
+                                                         int64_t n_slots, int64_t T, int k, int H, void* y,
+                                                         int y_dtype) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int cpr = H / 8;
+    if (g >= T * cpr) return;
+    const int64_t t = g / cpr;
+    const int c = (int)(g % cpr);
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < k; ++j) {
+        const int e = idx[t * k + j];
+        if (e < 0 || e >= E) continue;
+        const int s = expert_slot[e];
+        if (s < 0 || s >= n_slots) continue;
+        const float wj = w[t * k + j];
+        const u32x4 v = *reinterpret_cast<const u32x4*>(yk + (t * k + j) * H + 8 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[2 * i] += wj * bf16_bits_to_f32(v[i] & 0xFFFFu);
+            acc[2 * i + 1] += wj * bf16_bits_to_f32(v[i] >> 16);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) store_out(y, y_dtype, t * H + 8 * c + i, acc[i]);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- host side
+
+// Whether the tiled MXFP4 grouped-GEMM path covers this call (else the caller uses the
+// fused decode kernel token chunk by token chunk).
+bool pf_mxt_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k) {
+    const int64_t n = T * k;
+    return L.format == TSA_EXPERT_MXFP4 && L.mx_tiled && x_dtype == TSA_BF16 && L.hidden % 16 == 0 &&
+           L.inter % 16 == 0 && T * L.hidden * 2 < ((int64_t)1 << 32) && n * L.inter * 2 < ((int64_t)1 << 32);
+}
+
+static int64_t al256(int64_t v) { return (v + 255) / 256 * 256; }
+
+struct PfWs {
+    int64_t counts, offsets, perm, nent, table, h, yk, total;
+};
+
+static PfWs pf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
+    const int64_t n = T * k;
+    PfWs w;
+    int64_t o = 0;
+    w.counts = o; o += al256(4 * E);
+    w.offsets = o; o += al256(4 * (E + 1));
+    w.perm = o; o += al256(4 * n);
+    w.nent = o; o += 256;
+    w.table = o; o += al256((int64_t)sizeof(PfEntry) * (n / PF_BM + E + 1));
+    w.h = o; o += al256(2 * n * L.inter);
+    w.yk = o; o += al256(2 * n * L.hidden);
+    w.total = o;
+    return w;
+}
+
+int64_t pf_mxt_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
+    return pf_ws_layout(L, T, k, E).total;
+}
+
+int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                        hipStream_t stream);
+
+int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot,
+                   int64_t E, const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y,
+                   int y_dtype, uint8_t* ws, hipStream_t stream) {
+    const PfWs w = pf_ws_layout(L, T, k, E);
+    int32_t* counts = reinterpret_cast<int32_t*>(ws + w.counts);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + w.offsets);
+    int32_t* perm = reinterpret_cast<int32_t*>(ws + w.perm);
+    int* nent = reinterpret_cast<int*>(ws + w.nent);
+    PfEntry* table = reinterpret_cast<PfEntry*>(ws + w.table);
+    uint16_t* h = reinterpret_cast<uint16_t*>(ws + w.h);
+    uint16_t* yk = reinterpret_cast<uint16_t*>(ws + w.yk);
+    const int H = (int)L.hidden, I = (int)L.inter;
+
+    int rc = launch_group_kernel(idx, T * k, (int)E, counts, offsets, perm, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(pf_table_kernel, dim3(1), dim3(1024), 0, stream, counts, offsets, expert_slot, (int)E, n_slots,
+                       nent, table);
+    TSA_LAUNCH_CHECK();
+
+    static std::once_flag lds_once;
+    static hipError_t lds_err = hipSuccess;
+    std::call_once(lds_once, [] {
+        lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gemm_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+        if (lds_err == hipSuccess)
+            lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gemm_kernel<false>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+    });
+    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", PF_LDS, hipGetErrorString(lds_err));
+    const int grid = (num_cus() / 8) * 8;
+    PfGemm g{};
+    g.L = L;
+    g.pool = pool;
+    g.n_entries = nent;
+    g.table = table;
+    g.perm = perm;
+    g.k = k;
+    // gate_up: [2I, H] -> h
+    g.src = x;
+    g.src_rows = T;
+    g.out = h;
+    g.N = 2 * I;
+    g.K = H;
+    g.NT = (2 * I + PF_BN - 1) / PF_BN;
+    g.MP = (H + 127) / 128;
+    g.w_off = L.gate_off;
+    g.s_off = L.gate_scales_off;
+    g.b_off = L.gate_bias_off;
+    g.tile_bytes = 16 * (int64_t)H / 2;
+    g.stile_bytes = mx_tile_scale_bytes(H);
+    hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    TSA_LAUNCH_CHECK();
+    // down: [H, I] -> yk
+    g.src = h;
+    g.src_rows = T * k;
+    g.out = yk;
+    g.N = H;
+    g.K = I;
+    g.NT = (H + PF_BN - 1) / PF_BN;
+    g.MP = (I + 127) / 128;
+    g.w_off = L.down_off;
+    g.s_off = L.down_scales_off;
+    g.b_off = L.down_bias_off;
+    g.tile_bytes = 16 * (int64_t)I / 2;
+    g.stile_bytes = mx_tile_scale_bytes(I);
+    hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    TSA_LAUNCH_CHECK();
+
+    const int64_t threads = T * (H / 8);
+    hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, yk, idx,
+                       weights, expert_slot, E, n_slots, T, k, H, y, y_dtype);
+    TSA_LAUNCH_CHECK();
+    return TSA_OK;
+}
+
+}  // namespace tsa
