@@ -9,9 +9,9 @@ import torch
 COS_MIN = 0.9999
 REL_MAX = 1e-2
 
-# MoE decode workspace: a 16640-byte counter header (launch-wide words, then one
-# completion counter per (token, expert) pair every 256 bytes), then float h [T, k, I].
-WS_HDR = 16640
+# MoE decode workspace: a 41216-byte header (launch-wide words, one completion counter per
+# (token, expert) pair every 256 bytes, then 96 completion flags per pair), then h [T, k, I].
+WS_HDR = 41216
 
 
 def ws_header_clean(ws: torch.Tensor) -> None:

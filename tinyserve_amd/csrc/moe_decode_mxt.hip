@@ -61,7 +61,8 @@ struct MxtParams {
     void* y;
     int y_dtype;
     uint16_t* h;    // bf16 [T, k, I] published intermediate
-    unsigned* bar;  // workspace header: [1] phase B workgroups finished, [2] error flag, pair counters
+    unsigned* bar;  // workspace header: [1] phase B workgroups finished, [2] error flag
+    unsigned* flags;  // [T k][WS_FLAG_WORDS]: gate_up task kb of pair (t, j) is published
     int nA, nB, grid;
     int64_t gu_tile, gu_stile, dn_tile, dn_stile;  // bytes per 16-row tile: blocks, scale words
 };
@@ -225,8 +226,9 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
             __hip_atomic_store(reinterpret_cast<uint32_t*>(p.h + (int64_t)(t * k + j) * I + row0 / 2 + 2 * q), packed,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's h stores are complete ...
-        __syncthreads();                // ... and so are the other waves' before the count moves
-        if (tid == 0) __hip_atomic_fetch_add(pair_ctr(p.bar, t * k + j), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();                // ... and so are the other waves' before the flag is set
+        if (tid == 0)
+            __hip_atomic_store(&p.flags[(t * k + j) * WS_FLAG_WORDS + kb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- phase B: down tiles of every selected expert, weighted sum in a fixed order
@@ -235,7 +237,6 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
     const int RB = H / 16;
     const int rounds = (k + WAVES - 1) / WAVES;
     uint8_t* hs = vec + wave * KP * 2;
-    const unsigned need = (unsigned)tiles;  // phase A tasks per pair
     for (; task < p.nA + p.nB; task += p.grid) {
         did_b = true;
         const int b = task - p.nA;
@@ -264,9 +265,12 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
                     for (int jj = 0; jj < k; ++jj) {
                         const int sj = uniform(s_slot[t * k + jj]);
                         if (sj < 0 || sj >= p.n_slots) continue;  // a dead pair's h is never read
-                        unsigned* c = pair_ctr(p.bar, t * k + jj);
+                        unsigned* f = p.flags + (t * k + jj) * WS_FLAG_WORDS;
                         int spins = 0;
-                        while (ld_relaxed(c) < need) {
+                        for (;;) {
+                            bool done = true;
+                            for (int i = lane; i < tiles; i += 64) done &= ld_relaxed(f + i) != 0u;
+                            if (__all(done)) break;
                             __builtin_amdgcn_s_sleep(8);
                             if (++spins > SPIN_LIMIT) {
                                 __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -304,14 +308,18 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
         __syncthreads();
         if (aborted) break;
     }
-    // ---- leave: the last phase B workgroup out resets the counters for the next launch
-    if (did_b && tid == 0) {
-        const unsigned nbw = (unsigned)(p.nB < p.grid ? p.nB : p.grid);
-        const unsigned done = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done == nbw - 1) {
-            for (int i = 0; i < T * k; ++i)
-                __hip_atomic_store(pair_ctr(p.bar, i), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- leave: the last phase B workgroup out clears the flags for the next launch
+    if (did_b) {
+        if (tid == 0) {
+            const unsigned nbw = (unsigned)(p.nB < p.grid ? p.nB : p.grid);
+            const unsigned done = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_flag[1] = done == nbw - 1;
+        }
+        __syncthreads();
+        if (s_flag[1]) {
+            for (int i = tid; i < T * k * WS_FLAG_WORDS; i += blockDim.x)
+                __hip_atomic_store(&p.flags[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -384,6 +392,7 @@ int mxt_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_
     p.y = y;
     p.y_dtype = y_dtype;
     p.bar = reinterpret_cast<unsigned*>(ws);
+    p.flags = reinterpret_cast<unsigned*>(ws + WS_FLAG_OFF);
     p.h = reinterpret_cast<uint16_t*>(ws + WS_HDR);
     p.nA = (int)(T * k * (L.inter / 32));
     p.nB = (int)(T * (L.hidden / 16));
