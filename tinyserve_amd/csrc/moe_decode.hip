@@ -189,6 +189,18 @@ hipError_t launch_gguf_b(const Launch& s, const tsa_expert_layout& L, const uint
 }  // namespace
 
 int64_t mx_fused_ws_bytes(const tsa_expert_layout& L, int64_t T, int k);
+const char* gq_unsupported(const tsa_expert_layout& L);
+int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
+              const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
+              float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws,
+              int64_t ws_bytes, hipStream_t st);
+
+// GGUF experts with 2-byte aligned tensors, one gate/up type and k <= 16 run on the
+// super-block streaming kernels of moe_decode_gq.hip; the row kernels below cover the rest.
+static bool use_gq(const tsa_expert_layout& L, const uint8_t* pl, int k) {
+    const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
+    return L.format == TSA_EXPERT_GGUF && a2 && k <= 16 && !*gq_unsupported(L);
+}
 int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
@@ -368,6 +380,9 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
         TSA_LAUNCH_CHECK();
         return TSA_OK;
     }
+    if (use_gq(L, pl, k))
+        return gq_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
+                         y, y_dtype, ws, WS_HDR + h_region(L, T, k), st);
     const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
     switch (L.gate_type) {
         case 8: e = a2 ? launch_gguf_a<8, 2>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
@@ -424,6 +439,9 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
                              w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
         if (rc <= 0) return rc;
     }
+    if (use_gq(L, pl, k) && E <= 256 && T <= 4)
+        return gq_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
+                         T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
     // separate routing, slot mapping and the two-launch decode
     const int64_t tk = (T * k * 4 + 255) / 256 * 256;
     uint8_t* extra = ws + WS_HDR + h_region(L, T, k);

@@ -1,0 +1,383 @@
+// Top-k MoE decode over GGUF experts (gate, up and down as native Q8_0 / Q4_K / Q5_K / Q6_K
+// block streams): two launches, both routing in-kernel when router logits are given.
+//
+//   gq_phase_a: workgroup = one (token, expert) pair and 4 waves x GQ_RW rows of the
+//     intermediate dimension. Each wave streams the super-blocks of its GQ_RW gate rows and
+//     GQ_RW up rows (gguf_dot.h: one unit per lane, 16-byte loads, dot2 over bf16 codes),
+//     reduces them across the wave and writes h = act(gate, up) as bf16 (the reference
+//     runs its experts in bf16) into the workspace.
+//   gq_phase_b: workgroup = one token and GQ_RB output rows, 8 waves. Wave w takes expert
+//     w % kk (kk = min(k, 8); further experts in rounds) and row slice w / kk, stages that
+//     expert's h in its LDS area, streams the down rows the same way and keeps the
+//     router-weighted partial per row; the workgroup sums the partials over experts in a
+//     fixed order, so every output has one writer and the result is deterministic.
+//
+// Semantics: tinyserve/ggml_forward.py:88-115 (GGUF expert: silu(W_g x) * (W_u x), then
+// W_d), tinyserve/csrc/expert_loop.cpp:83-121 (weighted top-k sum), :85 (slot < 0
+// contributes nothing), tinyserve/_model_hooks.py:456-473 (routing).
+#include "fused_common.h"
+#include "mfma_tile.h"
+#include "gguf_dot.h"
+
+namespace tsa {
+namespace {
+
+constexpr int GQ_RW = 4;         // phase A: intermediate rows per wave
+constexpr int GQ_RB = 16;        // phase B: output rows per workgroup
+constexpr int GQ_B_WAVES = 8;
+constexpr int GQ_MISC = 2048;    // slot / weight tables, per-(expert, row) partials
+
+// Super-blocks (or Q8_0 blocks) touched by the values [lo, hi) of a TYPE stream, and the
+// LDS bytes a wave needs to stage them (16-byte aligned start, rounded up).
+template <int TYPE>
+__host__ __device__ constexpr uint32_t gq_sb_count(uint32_t lo, uint32_t hi) {
+    constexpr uint32_t VS = TYPE == 8 ? 32 : 256;
+    return (hi + VS - 1) / VS - lo / VS;
+}
+__host__ __device__ constexpr uint32_t gq_raw_bytes(uint32_t nsb, uint32_t sb) { return (nsb * sb + 15 + 15) / 16 * 16; }
+
+struct GqParams {
+    tsa_expert_layout L;
+    const uint8_t* pool;
+    int64_t n_slots;
+    const int32_t* slots;        // [T, k] (unrouted) or null
+    const float* wts;            // [T, k] (unrouted) or null
+    const void* logits;          // [T, E] (routed) or null
+    const int32_t* expert_slot;  // [E] (routed)
+    int32_t* idx_out;            // [T, k] (routed, optional)
+    float* w_out;                // [T, k] (routed, optional)
+    int logits_dtype, route_mode, E;
+    int T, k;
+    const void* x;
+    int x_dtype;
+    void* y;
+    int y_dtype;
+    uint16_t* h;  // bf16 [T k, I]
+    int raw_off_a, raw_stride_a;  // phase A: LDS offset and per-wave stride of the raw super-block areas
+    int vec_stride_b;             // phase B: per-wave stride of the staged h vectors (16-byte multiple)
+    int raw_off_b, raw_stride_b;  // phase B: raw areas
+};
+
+// LDS bytes of a staged vector of n values: bf16 values, then per-32 and per-16 sums.
+__host__ __device__ constexpr int gq_vec_bytes(int n) { return ((2 * n + 15) / 16) * 16 + 4 * (n / 32) + 4 * (n / 16); }
+
+// The LDS layout of a staged vector of n values at dst.
+__device__ __forceinline__ GqVec gq_vec(uint8_t* dst, int n) {
+    GqVec vec;
+    vec.v = dst;
+    vec.s32 = reinterpret_cast<float*>(dst + ((2 * n + 15) / 16) * 16);
+    vec.s16 = vec.s32 + n / 32;
+    return vec;
+}
+
+// Stages n values of src (dtype, starting at element off) into LDS at dst as bf16 (RNE),
+// with the sums of the bf16 values over every 32 and 16 consecutive positions. Threads
+// tid of nthr (nthr > 0), each handling 32-value groups with 16-byte loads (src + off
+// 16-byte aligned for bf16 / f16, as the callers' rows are).
+__device__ void gq_stage(uint8_t* dst, const void* src, int dtype, int64_t off, int n, int tid, int nthr) {
+    const GqVec vec = gq_vec(dst, n);
+    float* s32 = const_cast<float*>(vec.s32);
+    float* s16 = const_cast<float*>(vec.s16);
+    for (int g = tid; g < n / 32; g += nthr) {
+        uint32_t bits[16];  // 32 bf16 values, two per word
+        if (dtype == TSA_BF16) {
+            const u32x4* p4 = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + off + 32 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 v = p4[i];
+                bits[4 * i] = v[0]; bits[4 * i + 1] = v[1]; bits[4 * i + 2] = v[2]; bits[4 * i + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float f0 = load_act(src, dtype, off + 32 * g + 2 * i);
+                const float f1 = load_act(src, dtype, off + 32 * g + 2 * i + 1);
+                bits[i] = (uint32_t)f32_to_bf16_bits(f0) | ((uint32_t)f32_to_bf16_bits(f1) << 16);
+            }
+        }
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float r = bf16_bits_to_f32(bits[i] & 0xFFFFu) + bf16_bits_to_f32(bits[i] >> 16);
+            if (i < 8) a += r; else b += r;
+        }
+        u32x4* d4 = reinterpret_cast<u32x4*>(dst + 64 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d4[i] = u32x4{bits[4 * i], bits[4 * i + 1], bits[4 * i + 2], bits[4 * i + 3]};
+        s16[2 * g] = a;
+        s16[2 * g + 1] = b;
+        s32[g] = a + b;
+    }
+}
+
+__device__ __forceinline__ float gq_act(const tsa_expert_layout& L, float gate, float up) {
+    if (L.act == TSA_ACT_SWIGLU_OAI) return swiglu_oai(L, gate, up);
+    return gate * sigmoidf_(gate) * up;
+}
+
+// Routing (wave 0) or the given slot table for token t into s_slot / s_w; expert j of the
+// token is at index gq_sel(p, t) + j (routing writes the whole [T, k] table, T <= 4).
+__device__ __forceinline__ int gq_sel(const GqParams& p, int t) { return p.logits ? t * p.k : 0; }
+__device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, float* s_w) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (p.logits) {
+        if (tid < 64) {
+            int es[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+            const int sel = route_token(p, t, lane, es, s_slot, s_w);
+            if (write_out && p.idx_out && lane < p.k) {
+                p.idx_out[t * p.k + lane] = sel;
+                p.w_out[t * p.k + lane] = s_w[t * p.k + lane];
+            }
+        }
+    } else if (tid < p.k) {
+        s_slot[tid] = p.slots[(int64_t)t * p.k + tid];
+        s_w[tid] = p.wts[(int64_t)t * p.k + tid];
+    }
+}
+
+template <int TG>
+__global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
+    const int a = blockIdx.y, t = a / k;
+    int* s_slot = reinterpret_cast<int*>(smem);
+    float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
+    const GqVec xv = gq_vec(smem + GQ_MISC, H);
+    gq_route(p, t, blockIdx.x == 0 && a % k == 0, s_slot, s_w);
+    if (!p.logits) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid, 256);
+    else if (tid >= 64) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid - 64, 192);
+    __syncthreads();
+    const int64_t slot = uniform(s_slot[gq_sel(p, t) + a % k]);
+    if (slot < 0 || slot >= p.n_slots) return;  // a dead pair's h is never read
+    const int n0 = ((int)blockIdx.x * 4 + wave) * GQ_RW;
+    if (n0 >= I) return;
+    const int n1 = n0 + GQ_RW < I ? n0 + GQ_RW : I;
+    const uint8_t* base = p.pool + slot * L.slot_bytes;
+    using U = GqUnit<TG>;
+    constexpr uint32_t VS = TG == 8 ? 32 : 256, SB = U::SB;
+    const uint32_t lo = (uint32_t)n0 * H, hi = (uint32_t)n1 * H;
+    const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
+    // stage the super-blocks of rows [n0, n1) of gate and up into this wave's LDS area
+    const uint32_t s0 = lo / VS, nsb = gq_sb_count<TG>(lo, hi);
+    const uint32_t raw = gq_raw_bytes(nsb, SB);
+    uint8_t* rbuf = smem + p.raw_off_a + wave * p.raw_stride_a;
+    const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
+    uint32_t shift[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const uint32_t first = (uint32_t)(m ? L.up_off : L.gate_off) + s0 * SB;  // slot-relative byte
+        shift[m] = first & 15u;
+        gq_stage_raw(base, (uint32_t)L.slot_bytes, first - shift[m], raw, lds_r + m * raw, lane);
+    }
+    gq_wait_dma();
+    float acc[2][GQ_RW];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < GQ_RW; ++r) acc[m][r] = 0.0f;
+    for (uint32_t i = lane; i < 2 * nu; i += 64) {
+        const bool up = i >= nu;
+        const uint32_t u = u0 + (up ? i - nu : i);
+        const uint32_t g0 = u * U::V, row = g0 / (uint32_t)H, kk0 = g0 - row * (uint32_t)H;
+        const uint8_t* sb = rbuf + (up ? raw : 0) + shift[up] + (g0 / VS - s0) * SB;
+        float pa = 0.0f, pb = 0.0f;
+        gq_unit<TG>(sb, u, kk0, H, lo, hi, xv, pa, pb);
+        const int r = (int)row - n0;
+        if (up) {
+            acc_add(acc[1], r, pa);
+            acc_add(acc[1], r + 1, pb);
+        } else {
+            acc_add(acc[0], r, pa);
+            acc_add(acc[0], r + 1, pb);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GQ_RW; ++r) {
+        const float g = wave_sum_u(acc[0][r]), u = wave_sum_u(acc[1][r]);
+        if (lane == r && n0 + r < n1)
+            p.h[(int64_t)a * I + n0 + r] = f32_to_bf16_bits(gq_act(L, g, u));
+    }
+}
+
+template <int TD>
+__global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
+    const int t = blockIdx.y;
+    int* s_slot = reinterpret_cast<int*>(smem);
+    float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
+    float* s_part = reinterpret_cast<float*>(smem + 8 * FUSED_MAXT * FUSED_MAXK);  // [8 waves][GQ_RB]
+    uint8_t* hbuf = smem + GQ_MISC + wave * p.vec_stride_b;
+    gq_route(p, t, false, s_slot, s_w);
+    for (int i = tid; i < GQ_B_WAVES * GQ_RB; i += blockDim.x) s_part[i] = 0.0f;
+    __syncthreads();
+
+    const int kk = k < GQ_B_WAVES ? k : GQ_B_WAVES;          // experts per round
+    const int S = GQ_B_WAVES / kk;                            // row slices
+    const int slice = wave / kk, jw = wave % kk;
+    const int rows_per = GQ_RB / S;
+    const int nb0 = (int)blockIdx.x * GQ_RB;
+    const int n0 = nb0 + slice * rows_per;
+    const int n1 = n0 + rows_per < H ? n0 + rows_per : H;
+    using U = GqUnit<TD>;
+    float acc[GQ_RB];
+#pragma unroll
+    for (int r = 0; r < GQ_RB; ++r) acc[r] = 0.0f;
+    if (slice < S && n0 < n1) {
+        const uint32_t lo = (uint32_t)n0 * I, hi = (uint32_t)n1 * I;
+        const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
+        constexpr uint32_t VS = TD == 8 ? 32 : 256, SB = U::SB;
+        const uint32_t s0 = lo / VS, raw = gq_raw_bytes(gq_sb_count<TD>(lo, hi), SB);
+        uint8_t* rbuf = smem + p.raw_off_b + wave * p.raw_stride_b;
+        const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
+        for (int j = jw; j < k; j += kk) {
+            const int pair = t * k + j;
+            const int64_t slot = uniform(s_slot[gq_sel(p, t) + j]);
+            if (slot < 0 || slot >= p.n_slots) continue;
+            const float wj = s_w[gq_sel(p, t) + j];
+            const GqVec hv = gq_vec(hbuf, I);
+            gq_stage(hbuf, p.h, TSA_BF16, (int64_t)pair * I, I, lane, 64);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            const uint8_t* base = p.pool + slot * L.slot_bytes;
+            const uint32_t first = (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
+            gq_stage_raw(base, (uint32_t)L.slot_bytes, first - shift, raw, lds_r, lane);
+            gq_wait_dma();
+            for (uint32_t i = lane; i < nu; i += 64) {
+                const uint32_t u = u0 + i;
+                const uint32_t g0 = u * U::V, row = g0 / (uint32_t)I, kk0 = g0 - row * (uint32_t)I;
+                const uint8_t* sb = rbuf + shift + (g0 / VS - s0) * SB;
+                float pa = 0.0f, pb = 0.0f;
+                gq_unit<TD>(sb, u, kk0, I, lo, hi, hv, pa, pb);
+                const int r = (int)row - n0;
+                acc_add(acc, r, wj * pa);
+                acc_add(acc, r + 1, wj * pb);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();  // every lane is done with hbuf before it is restaged
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GQ_RB; ++r) {
+        const float v = wave_sum_u(acc[r]);
+        if (lane == 0 && r < rows_per) s_part[wave * GQ_RB + r] = v;
+    }
+    __syncthreads();
+    if (tid < GQ_RB) {  // row nb0 + tid = slice tid / rows_per, row tid % rows_per of that slice
+        const int sl = tid / rows_per, r = tid % rows_per;
+        float sum = 0.0f;
+        for (int j = 0; j < kk; ++j) sum += s_part[(sl * kk + j) * GQ_RB + r];
+        if (nb0 + tid < H) store_out(p.y, p.y_dtype, (int64_t)t * H + nb0 + tid, sum);
+    }
+}
+
+template <int TG>
+const void* phase_a_fn() { return reinterpret_cast<const void*>(&gq_phase_a<TG>); }
+template <int TD>
+const void* phase_b_fn() { return reinterpret_cast<const void*>(&gq_phase_b<TD>); }
+
+const void* pick_a(int t) {
+    switch (t) {
+        case 8: return phase_a_fn<8>();
+        case 12: return phase_a_fn<12>();
+        case 13: return phase_a_fn<13>();
+        case 14: return phase_a_fn<14>();
+    }
+    return nullptr;
+}
+const void* pick_b(int t) {
+    switch (t) {
+        case 8: return phase_b_fn<8>();
+        case 12: return phase_b_fn<12>();
+        case 13: return phase_b_fn<13>();
+        case 14: return phase_b_fn<14>();
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+// Requirements beyond validate_layout: "" if met.
+const char* gq_unsupported(const tsa_expert_layout& L) {
+    if (L.format != TSA_EXPERT_GGUF) return "not a GGUF layout";
+    if (L.gate_type != L.up_type) return "gate and up must share one ggml type";
+    if (!pick_a(L.gate_type) || !pick_b(L.down_type)) return "unsupported ggml type";
+    if (L.gate_bias_off >= 0 || L.down_bias_off >= 0) return "GGUF experts carry no biases";
+    if (L.hidden % 32 || L.inter % 32) return "hidden and inter must be multiples of 32";
+    if (2 * L.inter * L.hidden >= ((int64_t)1 << 31)) return "matrices of 2^31 values or more are not supported";
+    if (L.hidden > 8192 || L.inter > 4096) return "hidden above 8192 or inter above 4096 is not supported";
+    return "";
+}
+
+int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
+              const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
+              float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws,
+              int64_t ws_bytes, hipStream_t st) {
+    const char* why = gq_unsupported(L);
+    TSA_REQUIRE(!*why, TSA_ERR_SHAPE, "GGUF decode: %s", why);
+    TSA_REQUIRE(T >= 1 && T <= 65535 && k >= 1 && k <= FUSED_MAXK && T * k <= 65535, TSA_ERR_SHAPE,
+                "GGUF decode: T %lld, k %d", (long long)T, k);
+    TSA_REQUIRE(!logits || (E <= 256 && T <= FUSED_MAXT), TSA_ERR_SHAPE, "GGUF decode routing: E %lld, T %lld",
+                (long long)E, (long long)T);
+    TSA_REQUIRE(ws_bytes >= WS_HDR + T * k * L.inter * 2, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
+    GqParams p{};
+    p.L = L;
+    p.pool = pool;
+    p.n_slots = n_slots;
+    p.slots = slots;
+    p.wts = wts;
+    p.logits = logits;
+    p.logits_dtype = logits_dtype;
+    p.route_mode = mode;
+    p.expert_slot = expert_slot;
+    p.E = (int)E;
+    p.idx_out = idx_out;
+    p.w_out = w_out;
+    p.T = (int)T;
+    p.k = k;
+    p.x = x;
+    p.x_dtype = x_dtype;
+    p.y = y;
+    p.y_dtype = y_dtype;
+    p.h = reinterpret_cast<uint16_t*>(ws + WS_HDR);
+    // raw staging per wave: phase A GQ_RW rows of gate and of up (K = hidden); phase B the
+    // rows of one expert's down slice (K = inter); the largest over row alignments
+    const int ta = L.gate_type, tb = L.down_type;
+    auto sb_bytes = [](int t) { return t == 8 ? 34u : t == 12 ? 144u : t == 13 ? 176u : 210u; };
+    auto vs = [](int t) { return t == 8 ? 32u : 256u; };
+    const uint32_t rawA = gq_raw_bytes((GQ_RW * (uint32_t)L.hidden + vs(ta) - 1) / vs(ta) + 1, sb_bytes(ta));
+    const int kk = k < GQ_B_WAVES ? k : GQ_B_WAVES;
+    const uint32_t rowsB = GQ_RB / (GQ_B_WAVES / kk);
+    const uint32_t rawB = gq_raw_bytes((rowsB * (uint32_t)L.inter + vs(tb) - 1) / vs(tb) + 1, sb_bytes(tb));
+    const size_t vecA = ((size_t)gq_vec_bytes((int)L.hidden) + 15) / 16 * 16;
+    const size_t lds_a = GQ_MISC + vecA + 4 * 2 * (size_t)rawA;
+    p.raw_off_a = (int)(GQ_MISC + vecA);
+    p.raw_stride_a = (int)(2 * rawA);
+    const size_t vecB = ((size_t)gq_vec_bytes((int)L.inter) + 15) / 16 * 16;
+    p.vec_stride_b = (int)vecB;
+    p.raw_off_b = (int)(GQ_MISC + GQ_B_WAVES * vecB);
+    p.raw_stride_b = (int)rawB;
+    const size_t lds_b = GQ_MISC + GQ_B_WAVES * (vecB + rawB);
+    TSA_REQUIRE(lds_a <= 160 * 1024 && lds_b <= 160 * 1024, TSA_ERR_SHAPE, "GGUF decode: LDS %zu / %zu bytes", lds_a,
+                lds_b);
+    const void* fa = pick_a(L.gate_type);
+    const void* fb = pick_b(L.down_type);
+    if (lds_b > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fb, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
+    if (lds_a > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fa, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_a));
+    void* args[] = {&p};
+    const dim3 ga((unsigned)((L.inter + 4 * GQ_RW - 1) / (4 * GQ_RW)), (unsigned)(T * k));
+    TSA_HIP_CHECK(hipLaunchKernel(fa, ga, dim3(256), args, lds_a, st));
+    const dim3 gb((unsigned)((L.hidden + GQ_RB - 1) / GQ_RB), (unsigned)T);
+    TSA_HIP_CHECK(hipLaunchKernel(fb, gb, dim3(64 * GQ_B_WAVES), args, lds_b, st));
+    return TSA_OK;
+}
+
+}  // namespace tsa
