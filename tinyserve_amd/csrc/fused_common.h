@@ -107,50 +107,148 @@ __device__ __forceinline__ float load_bias(const uint8_t* src, int dtype, int64_
     return dtype == TSA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
 
-// One wave routes token t (E <= 256): slots of the selected experts into s_slot (es[j] =
-// expert_slot[lane + 64 j], loaded by the caller), weights into s_w; lane r < k returns
-// the r-th selected expert id.
+// Orderable key of a logit: a larger float has a larger key, -0 and +0 share one key, and
+// NaN gets key 1, just above the key 0 of padding and of already selected entries (a
+// stable descending sort, as the reference's routing does, puts NaN last).
+__device__ __forceinline__ uint32_t route_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    u = u == 0x80000000u ? 0u : u;
+    const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return v != v ? 1u : key;
+}
+__device__ __forceinline__ float route_key_value(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+// Sum over lanes 0..15 (the first DPP row), returned to every lane.
+__device__ __forceinline__ float row16_sum(float v) {
+    const float o = v;
+    v += dpp_f<0x111, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x112, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x113, 0xF, 0xF>(o, 0.0f);
+    v += dpp_f<0x114, 0xF, 0xE>(v, 0.0f);
+    v += dpp_f<0x118, 0xF, 0xC>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+}
+
+// Number of set bits of m below this lane.
+__device__ __forceinline__ int bits_below(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Top-k selection over NV logits per lane (expert e = lane + 64 j), k <= 16:
+//  1. the threshold: a bitwise search (most significant bit first) for the largest key t
+//     with at least k keys >= t, counted with ballots; it stops as soon as exactly k keys
+//     are >= t. Otherwise t is the k-th largest key and several keys equal it; those are
+//     taken in id order (the lowest ids first).
+//  2. each selected entry's rank among the k: the number of selected entries with a larger
+//     key, or an equal key and a lower id (one scalar read per selected entry).
+//  3. entry of rank r -> s_slot / s_w[t k + r] (id and key), read back by lane r, then the
+//     slot of the entry replaces the id.
+// Lane r < k ends with the key and id of the r-th selection.
+template <int NV, class P>
+__device__ void route_select(const P& p, int t, int lane, const float v[4], const int es[4], int* s_slot, float* s_w,
+                             uint32_t& myk, int& mysel) {
+    const int k = p.k;
+    uint32_t key[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) key[j] = lane + 64 * j < p.E ? route_key(v[j]) : 0u;
+    uint32_t thr = 0;
+    int cnt = 64 * NV;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = thr | (1u << bit);
+        int n = 0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) n += __popcll(__ballot(key[j] >= c));
+        if (n >= k) {
+            thr = c;
+            cnt = n;
+            if (n == k) break;
+        }
+    }
+    bool sel[NV];
+    if (cnt == k) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) sel[j] = key[j] >= thr;
+    } else {  // ties at the k-th largest key
+        int need = k, before = 0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) need -= __popcll(__ballot(key[j] > thr));
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint64_t eq = __ballot(key[j] == thr);
+            sel[j] = key[j] > thr || (key[j] == thr && before + bits_below(eq) < need);
+            before += __popcll(eq);
+        }
+    }
+    int rank[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) rank[j] = 0;
+#pragma unroll
+    for (int jq = 0; jq < NV; ++jq) {
+        uint64_t m = __ballot(sel[jq]);
+        while (m) {
+            const int L = __ffsll((unsigned long long)m) - 1;
+            m &= m - 1;
+            const uint32_t kq = (uint32_t)__builtin_amdgcn_readlane((int)key[jq], L);
+            const int eq_id = 64 * jq + L;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                rank[j] += (kq > key[j] || (kq == key[j] && eq_id < 64 * j + lane)) ? 1 : 0;
+        }
+    }
+    uint32_t* s_key = reinterpret_cast<uint32_t*>(s_w) + t * k;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (sel[j]) {
+            s_slot[t * k + rank[j]] = 64 * j + lane;
+            s_key[rank[j]] = key[j];
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    mysel = lane < k ? s_slot[t * k + lane] : -1;
+    myk = lane < k ? s_key[lane] : 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (sel[j]) s_slot[t * k + rank[j]] = es[j];
+}
+
+// One wave routes token t (E <= 256, k <= 16): slots of the selected experts into s_slot
+// (es[j] = expert_slot[lane + 64 j], loaded by the caller), weights into s_w; lane r < k
+// returns the r-th selected expert id. Selection is by logit, descending, ties to the lower
+// id; the softmax is monotone, so this is also the top-k of the probabilities
+// (tinyserve/_model_hooks.py:456-473). Softmax over all experts, top-k and renormalisation
+// equals the softmax over the k selected logits, so that mode shares the top-k-softmax
+// path; only the unnormalised mode needs the sum over all experts.
 template <class P>
 __device__ int route_token(const P& p, int t, int lane, const int es[4], int* s_slot, float* s_w) {
     float v[4];
     load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, v);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (lane + 64 * j >= p.E) v[j] = -INFINITY;
-    unsigned taken = 0;
-    float myval = -INFINITY;  // lane r < k: the r-th selected logit
-    int mysel = -1;           // lane r < k: the r-th selected id
-    for (int r = 0; r < p.k; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {  // j ascending keeps the lowest id on ties within a lane
-            const int e = lane + 64 * j;
-            if (e < p.E && !((taken >> j) & 1u) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
-        }
-        const float m = wave_max_u(bv);
-        const int e = wave_min_u(bv == m ? bi : 0x7FFFFFFF);
-        const int je = e >> 6;
-        if ((e & 63) == lane) {
-            taken |= 1u << je;
-            s_slot[t * p.k + r] = je == 0 ? es[0] : je == 1 ? es[1] : je == 2 ? es[2] : es[3];
-        }
-        if (lane == r) { myval = m; mysel = e; }
+    uint32_t myk;
+    int mysel;
+    switch ((p.E + 63) >> 6) {
+        case 1: route_select<1>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
+        case 2: route_select<2>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
+        case 3: route_select<3>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
+        default: route_select<4>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
     }
+    const float myval = route_key_value(myk);  // lane r < k: the r-th selected logit
+    const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));  // the maximum
     float w;
-    if (p.route_mode == TSA_ROUTE_TOPK_SOFTMAX) {
-        const float top = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(myval)));  // lane 0 = max
-        const float ex = lane < p.k ? expf(myval - top) : 0.0f;
-        w = ex / wave_sum_u(ex);
-    } else {
-        const float vmax = wave_max_u(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    if (p.route_mode == TSA_ROUTE_SOFTMAX_TOPK) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j < p.E) s += expf(v[j] - vmax);
-        const float zsum = wave_sum_u(s);
-        const float pr = lane < p.k ? expf(myval - vmax) / zsum : 0.0f;
-        w = p.route_mode == TSA_ROUTE_SOFTMAX_TOPK_RENORM ? pr / wave_sum_u(pr) : pr;
+            if (lane + 64 * j < p.E) s += __expf(v[j] - top);
+        const float z = wave_sum_u(s);
+        w = lane < p.k ? __expf(myval - top) / z : 0.0f;
+    } else {
+        const float ex = lane < p.k ? __expf(myval - top) : 0.0f;
+        w = ex / row16_sum(ex);
     }
     if (lane < p.k) s_w[t * p.k + lane] = w;
     return mysel;

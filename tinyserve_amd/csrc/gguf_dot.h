@@ -105,19 +105,41 @@ __device__ __forceinline__ void gq_stage_raw(const uint8_t* base, uint32_t recor
     }
 }
 
+// Copies the n bytes (a whole number of 16-byte chunks) of a bf16 vector at a0 of the
+// buffer (base, records) into the padded vector layout at dst: one 256-byte run (16 lanes)
+// per instruction.
+__device__ __forceinline__ void gq_stage_vec_raw(const uint8_t* base, uint32_t records, uint32_t a0, uint32_t n,
+                                                 uint32_t dst, int lane) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const gq_v4i r = gq_v4i{(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)records, 0x00020000};
+    for (uint32_t c = 0; c < n; c += 256) {
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst + c + 16 * (c >> 8));
+        if (lane < 16 && c + 16 * lane < n)
+            asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(a0 + c + 16 * lane), "s"(r),
+                         "s"(m0)
+                         : "memory", "m0");
+    }
+}
+
 // This wave's loads (and LDS work) are complete; then its lanes may read what they staged.
 __device__ __forceinline__ void gq_wait_dma() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
 }
 
-// The vector in LDS: bf16 values (2 bytes each, 16-byte aligned) and per-32-value and
-// per-16-value sums (float), all indexed by position along K.
+// The vector in LDS: bf16 values and per-32-value and per-16-value sums (float), indexed by
+// position along K. Every 128 values (256 bytes) are followed by 16 bytes of padding: the
+// lanes of a wave read the vector at strides of 256 or 512 bytes (one unit each), which
+// without the padding would put every lane's 16-byte read on the same four banks.
 struct GqVec {
-    const uint8_t* v;    // bf16 [K]
+    const uint8_t* v;    // bf16 [K], padded
     const float* s32;    // [K / 32]
     const float* s16;    // [K / 16]
 };
+
+// Byte offset of value kk in the padded vector (kk a multiple of 8).
+__host__ __device__ constexpr uint32_t gq_pad(uint32_t kk) { return 2 * kk + 16 * (kk >> 7); }
+__device__ __forceinline__ const uint8_t* gq_x(const GqVec& x, uint32_t kk) { return x.v + gq_pad(kk); }
 
 // Dot products of unit u (unit index in the flat stream) with the vector; b points at the
 // unit's super-block (or block) in LDS. The unit's values start at column kk0 of some row
@@ -125,18 +147,24 @@ struct GqVec {
 // value index g lies in [lo, hi) contribute to pa (still in that row) or pb (the next row,
 // once kk reaches K; a unit spans at most two rows since K >= V). 32-bit indices
 // (matrices below 2^31 values).
-template <int TYPE>
+// WRAP = false: K is a multiple of the unit's values, so every unit lies inside one row
+// and inside [lo, hi) (the caller's units are whole rows); the row checks compile away.
+template <int TYPE, bool WRAP = true>
 __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t u, uint32_t kk0, uint32_t K, uint32_t lo,
                                         uint32_t hi, const GqVec& x, float& pa, float& pb) {
     using U = GqUnit<TYPE>;
     const uint32_t g0 = u * U::V;
     auto add = [&](uint32_t j, float part) {
-        if (kk0 + 32 * j >= K) pb += part;
+        if (WRAP && kk0 + 32 * j >= K) pb += part;
         else pa += part;
     };
-    auto col = [&](uint32_t j) { const uint32_t kk = kk0 + 32 * j; return kk >= K ? kk - K : kk; };
+    auto col = [&](uint32_t j) {
+        const uint32_t kk = kk0 + 32 * j;
+        return WRAP && kk >= K ? kk - K : kk;
+    };
+    auto outside = [&](uint32_t g) { return WRAP && (g < lo || g >= hi); };
     if constexpr (TYPE == 8) {
-        if (g0 < lo || g0 >= hi) return;
+        if (outside(g0)) return;
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b));
         const u32x4 a = ld16u(b + 2), c = ld16u(b + 18);
         uint32_t ql[8], qh[8];
@@ -149,7 +177,7 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
             qh[4 + i] = (wc >> 4) & 0x0F0F0F0Fu;
         }
         const uint32_t kk = kk0;
-        const uint8_t* xs = x.v + 2 * kk;
+        const uint8_t* xs = gq_x(x, kk);
         const float sx = x.s32[kk / 32];
         // sum q x = sum (16 qh + ql - 128) x
         const float dl = dot32(ql, xs) - 128.0f * sx, dh = dot32(qh, xs) - 128.0f * sx;
@@ -169,8 +197,7 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         const uint32_t s[3] = {hdr[1], hdr[2], hdr[3]};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t g = g0 + 32 * j;
-            if (g < lo || g >= hi) continue;
+            if (outside(g0 + 32 * j)) continue;
             uint32_t sc, m;
             k_scale_min(s, j, sc, m);
             uint32_t q[8];
@@ -183,7 +210,7 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
             }
             const uint32_t kk = col(j);
             const float sx = x.s32[kk / 32];
-            const float dq = dot32(q, x.v + 2 * kk) - 128.0f * sx;
+            const float dq = dot32(q, gq_x(x, kk)) - 128.0f * sx;
             add(j, d * (float)sc * dq - dmin * (float)m * sx);
         }
     } else {  // Q6_K, half h of super-block u / 2: ql[64h, +64), qh[32h, +32), sc[8h, +8), d @208
@@ -197,8 +224,7 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b + 208));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {  // 32-value quarter t of the half
-            const uint32_t g = g0 + 32 * t;
-            if (g < lo || g >= hi) continue;
+            if (outside(g0 + 32 * t)) continue;
             uint32_t q[8];
             const int shl = 4 * (t >> 1), shh = 2 * t;
 #pragma unroll
@@ -206,7 +232,7 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
                 q[i] = ((l[2 * (t & 1) + (i >> 2)][i & 3] >> shl) & 0x0F0F0F0Fu) |
                        (((qh[i >> 2][i & 3] >> shh) & 0x03030303u) << 4);
             const uint32_t kk = col(t);
-            const uint8_t* xs = x.v + 2 * kk;
+            const uint8_t* xs = gq_x(x, kk);
             const float s0 = x.s16[kk / 16], s1 = x.s16[kk / 16 + 1];
             const uint32_t sw = t < 2 ? scw.x : scw.y;
             const float sc0 = (float)(int8_t)((sw >> (16 * (t & 1))) & 0xFFu);

@@ -23,7 +23,7 @@ namespace tsa {
 namespace {
 
 constexpr int GQ_RW = 4;         // phase A: intermediate rows per wave
-constexpr int GQ_RB = 16;        // phase B: output rows per workgroup
+constexpr int GQ_RB = 8;         // phase B: output rows per workgroup
 constexpr int GQ_B_WAVES = 8;
 constexpr int GQ_MISC = 2048;    // slot / weight tables, per-(expert, row) partials
 
@@ -53,19 +53,24 @@ struct GqParams {
     void* y;
     int y_dtype;
     uint16_t* h;  // bf16 [T k, I]
+    int64_t h_bytes;              // bytes of h (the records of its buffer resource)
+    int32_t* tab_slot;            // routed: the slots and weights phase A chose, [T, k]
+    float* tab_w;
     int raw_off_a, raw_stride_a;  // phase A: LDS offset and per-wave stride of the raw super-block areas
     int vec_stride_b;             // phase B: per-wave stride of the staged h vectors (16-byte multiple)
     int raw_off_b, raw_stride_b;  // phase B: raw areas
 };
 
-// LDS bytes of a staged vector of n values: bf16 values, then per-32 and per-16 sums.
-__host__ __device__ constexpr int gq_vec_bytes(int n) { return ((2 * n + 15) / 16) * 16 + 4 * (n / 32) + 4 * (n / 16); }
+// LDS bytes of a staged vector of n values (n % 32 == 0): padded bf16 values, then the
+// per-32 and per-16 sums.
+__host__ __device__ constexpr int gq_vec_vbytes(int n) { return (int)gq_pad((uint32_t)((n + 127) / 128 * 128)); }
+__host__ __device__ constexpr int gq_vec_bytes(int n) { return gq_vec_vbytes(n) + 4 * (n / 32) + 4 * (n / 16); }
 
 // The LDS layout of a staged vector of n values at dst.
 __device__ __forceinline__ GqVec gq_vec(uint8_t* dst, int n) {
     GqVec vec;
     vec.v = dst;
-    vec.s32 = reinterpret_cast<float*>(dst + ((2 * n + 15) / 16) * 16);
+    vec.s32 = reinterpret_cast<float*>(dst + gq_vec_vbytes(n));
     vec.s16 = vec.s32 + n / 32;
     return vec;
 }
@@ -101,9 +106,31 @@ __device__ void gq_stage(uint8_t* dst, const void* src, int dtype, int64_t off, 
             const float r = bf16_bits_to_f32(bits[i] & 0xFFFFu) + bf16_bits_to_f32(bits[i] >> 16);
             if (i < 8) a += r; else b += r;
         }
-        u32x4* d4 = reinterpret_cast<u32x4*>(dst + 64 * g);
+        u32x4* d4 = reinterpret_cast<u32x4*>(dst + gq_pad(32 * g));
 #pragma unroll
         for (int i = 0; i < 4; ++i) d4[i] = u32x4{bits[4 * i], bits[4 * i + 1], bits[4 * i + 2], bits[4 * i + 3]};
+        s16[2 * g] = a;
+        s16[2 * g + 1] = b;
+        s32[g] = a + b;
+    }
+}
+
+// The per-32 and per-16 sums of a bf16 vector already in LDS at vec (n values), one wave.
+__device__ void gq_vec_sums(const GqVec& vec, int n, int lane) {
+    float* s32 = const_cast<float*>(vec.s32);
+    float* s16 = const_cast<float*>(vec.s16);
+    for (int g = lane; g < n / 32; g += 64) {
+        const u32x4* p4 = reinterpret_cast<const u32x4*>(gq_x(vec, 32 * g));
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 w = p4[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float r = bf16_bits_to_f32(w[e] & 0xFFFFu) + bf16_bits_to_f32(w[e] >> 16);
+                if (i < 2) a += r; else b += r;
+            }
+        }
         s16[2 * g] = a;
         s16[2 * g + 1] = b;
         s32[g] = a + b;
@@ -126,14 +153,62 @@ __device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, 
 #pragma unroll
             for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
             const int sel = route_token(p, t, lane, es, s_slot, s_w);
-            if (write_out && p.idx_out && lane < p.k) {
-                p.idx_out[t * p.k + lane] = sel;
-                p.w_out[t * p.k + lane] = s_w[t * p.k + lane];
+            if (write_out && lane < p.k) {
+                if (p.idx_out) {
+                    p.idx_out[t * p.k + lane] = sel;
+                    p.w_out[t * p.k + lane] = s_w[t * p.k + lane];
+                }
+                p.tab_slot[t * p.k + lane] = s_slot[t * p.k + lane];  // written by this lane
+                p.tab_w[t * p.k + lane] = s_w[t * p.k + lane];
             }
         }
     } else if (tid < p.k) {
         s_slot[tid] = p.slots[(int64_t)t * p.k + tid];
         s_w[tid] = p.wts[(int64_t)t * p.k + tid];
+    }
+}
+
+// Phase A units of one wave: lane i takes units i, i + 64, ... of gate (i < nu) then up.
+template <int TG, bool WRAP>
+__device__ __forceinline__ void gq_a_units(const uint8_t* rbuf, uint32_t raw, const uint32_t shift[2], uint32_t s0,
+                                           uint32_t u0, uint32_t nu, int n0, int H, uint32_t lo, uint32_t hi,
+                                           const GqVec& xv, int lane, float (&acc)[2][GQ_RW]) {
+    using U = GqUnit<TG>;
+    constexpr uint32_t VS = TG == 8 ? 32 : 256, SB = U::SB;
+    for (uint32_t i = lane; i < 2 * nu; i += 64) {
+        const bool up = i >= nu;
+        const uint32_t u = u0 + (up ? i - nu : i);
+        const uint32_t g0 = u * U::V, row = g0 / (uint32_t)H, kk0 = g0 - row * (uint32_t)H;
+        const uint8_t* sb = rbuf + (up ? raw : 0) + shift[up] + (g0 / VS - s0) * SB;
+        float pa = 0.0f, pb = 0.0f;
+        gq_unit<TG, WRAP>(sb, u, kk0, H, lo, hi, xv, pa, pb);
+        const int r = (int)row - n0;
+        if (up) {
+            acc_add(acc[1], r, pa);
+            if (WRAP) acc_add(acc[1], r + 1, pb);
+        } else {
+            acc_add(acc[0], r, pa);
+            if (WRAP) acc_add(acc[0], r + 1, pb);
+        }
+    }
+}
+
+// Phase B units of one wave (one expert's rows [n0, n1) of down), weighted by wj.
+template <int TD, bool WRAP>
+__device__ __forceinline__ void gq_b_units(const uint8_t* rbuf, uint32_t shift, uint32_t s0, uint32_t u0, uint32_t nu,
+                                           int n0, int I, uint32_t lo, uint32_t hi, const GqVec& hv, float wj,
+                                           int lane, float (&acc)[GQ_RB]) {
+    using U = GqUnit<TD>;
+    constexpr uint32_t VS = TD == 8 ? 32 : 256, SB = U::SB;
+    for (uint32_t i = lane; i < nu; i += 64) {
+        const uint32_t u = u0 + i;
+        const uint32_t g0 = u * U::V, row = g0 / (uint32_t)I, kk0 = g0 - row * (uint32_t)I;
+        const uint8_t* sb = rbuf + shift + (g0 / VS - s0) * SB;
+        float pa = 0.0f, pb = 0.0f;
+        gq_unit<TD, WRAP>(sb, u, kk0, I, lo, hi, hv, pa, pb);
+        const int r = (int)row - n0;
+        acc_add(acc, r, wj * pa);
+        if (WRAP) acc_add(acc, r + 1, wj * pb);
     }
 }
 
@@ -179,22 +254,10 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int r = 0; r < GQ_RW; ++r) acc[m][r] = 0.0f;
-    for (uint32_t i = lane; i < 2 * nu; i += 64) {
-        const bool up = i >= nu;
-        const uint32_t u = u0 + (up ? i - nu : i);
-        const uint32_t g0 = u * U::V, row = g0 / (uint32_t)H, kk0 = g0 - row * (uint32_t)H;
-        const uint8_t* sb = rbuf + (up ? raw : 0) + shift[up] + (g0 / VS - s0) * SB;
-        float pa = 0.0f, pb = 0.0f;
-        gq_unit<TG>(sb, u, kk0, H, lo, hi, xv, pa, pb);
-        const int r = (int)row - n0;
-        if (up) {
-            acc_add(acc[1], r, pa);
-            acc_add(acc[1], r + 1, pb);
-        } else {
-            acc_add(acc[0], r, pa);
-            acc_add(acc[0], r + 1, pb);
-        }
-    }
+    if (H % U::V == 0)
+        gq_a_units<TG, false>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
+    else
+        gq_a_units<TG, true>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
 #pragma unroll
     for (int r = 0; r < GQ_RW; ++r) {
         const float g = wave_sum_u(acc[0][r]), u = wave_sum_u(acc[1][r]);
@@ -242,24 +305,20 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
             if (slot < 0 || slot >= p.n_slots) continue;
             const float wj = s_w[gq_sel(p, t) + j];
             const GqVec hv = gq_vec(hbuf, I);
-            gq_stage(hbuf, p.h, TSA_BF16, (int64_t)pair * I, I, lane, 64);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             const uint8_t* base = p.pool + slot * L.slot_bytes;
             const uint32_t first = (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
             gq_stage_raw(base, (uint32_t)L.slot_bytes, first - shift, raw, lds_r, lane);
+            gq_stage_vec_raw(reinterpret_cast<const uint8_t*>(p.h), (uint32_t)p.h_bytes, (uint32_t)pair * I * 2u,
+                             2u * I, (uint32_t)reinterpret_cast<uintptr_t>(hbuf), lane);
             gq_wait_dma();
-            for (uint32_t i = lane; i < nu; i += 64) {
-                const uint32_t u = u0 + i;
-                const uint32_t g0 = u * U::V, row = g0 / (uint32_t)I, kk0 = g0 - row * (uint32_t)I;
-                const uint8_t* sb = rbuf + shift + (g0 / VS - s0) * SB;
-                float pa = 0.0f, pb = 0.0f;
-                gq_unit<TD>(sb, u, kk0, I, lo, hi, hv, pa, pb);
-                const int r = (int)row - n0;
-                acc_add(acc, r, wj * pa);
-                acc_add(acc, r + 1, wj * pb);
-            }
+            gq_vec_sums(hv, I, lane);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            if (I % U::V == 0)
+                gq_b_units<TD, false>(rbuf, shift, s0, u0, nu, n0, I, lo, hi, hv, wj, lane, acc);
+            else
+                gq_b_units<TD, true>(rbuf, shift, s0, u0, nu, n0, I, lo, hi, hv, wj, lane, acc);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_wave_barrier();  // every lane is done with hbuf before it is restaged
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -327,7 +386,9 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
                 "GGUF decode: T %lld, k %d", (long long)T, k);
     TSA_REQUIRE(!logits || (E <= 256 && T <= FUSED_MAXT), TSA_ERR_SHAPE, "GGUF decode routing: E %lld, T %lld",
                 (long long)E, (long long)T);
-    TSA_REQUIRE(ws_bytes >= WS_HDR + T * k * L.inter * 2, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
+    // h (bf16) then, for routed calls, the slot / weight table phase A writes for phase B
+    const int64_t h_bytes = T * k * L.inter * 2, tab_off = WS_HDR + (h_bytes + 255) / 256 * 256;
+    TSA_REQUIRE(ws_bytes >= tab_off + T * k * 8, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
     GqParams p{};
     p.L = L;
     p.pool = pool;
@@ -348,6 +409,9 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     p.y = y;
     p.y_dtype = y_dtype;
     p.h = reinterpret_cast<uint16_t*>(ws + WS_HDR);
+    p.h_bytes = h_bytes;
+    p.tab_slot = reinterpret_cast<int32_t*>(ws + tab_off);
+    p.tab_w = reinterpret_cast<float*>(ws + tab_off + T * k * 4);
     // raw staging per wave: phase A GQ_RW rows of gate and of up (K = hidden); phase B the
     // rows of one expert's down slice (K = inter); the largest over row alignments
     const int ta = L.gate_type, tb = L.down_type;
@@ -375,8 +439,15 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     void* args[] = {&p};
     const dim3 ga((unsigned)((L.inter + 4 * GQ_RW - 1) / (4 * GQ_RW)), (unsigned)(T * k));
     TSA_HIP_CHECK(hipLaunchKernel(fa, ga, dim3(256), args, lds_a, st));
+    GqParams pb = p;  // phase B takes the routed table as its slot / weight input
+    if (logits) {
+        pb.logits = nullptr;
+        pb.slots = p.tab_slot;
+        pb.wts = p.tab_w;
+    }
+    void* args_b[] = {&pb};
     const dim3 gb((unsigned)((L.hidden + GQ_RB - 1) / GQ_RB), (unsigned)T);
-    TSA_HIP_CHECK(hipLaunchKernel(fb, gb, dim3(64 * GQ_B_WAVES), args, lds_b, st));
+    TSA_HIP_CHECK(hipLaunchKernel(fb, gb, dim3(64 * GQ_B_WAVES), args_b, lds_b, st));
     return TSA_OK;
 }
 
