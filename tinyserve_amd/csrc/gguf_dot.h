@@ -22,7 +22,8 @@
 // (y = deq(W) x in fp32).
 #pragma once
 
-#include "formats.h"
+#include "fused_common.h"
+#include "mfma_tile.h"
 
 namespace tsa {
 namespace {
@@ -75,6 +76,60 @@ __device__ __forceinline__ float dot16(const uint32_t* q, const uint8_t* xs) {
     a = dot4(q[2], x1[0], x1[1], a);
     b = dot4(q[3], x1[2], x1[3], b);
     return a + b;
+}
+
+// dot32 / dot16 over the hi and lo halves of a split vector, sharing the code pairs.
+__device__ __forceinline__ float dot32s(const uint32_t q[8], const uint8_t* xs, const uint8_t* xl) {
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 h = *reinterpret_cast<const u32x4*>(xs + 16 * i);
+        const u32x4 l = *reinterpret_cast<const u32x4*>(xl + 16 * i);
+        a = dot4(q[2 * i], h[0], h[1], a);
+        b = dot4(q[2 * i + 1], h[2], h[3], b);
+        a = dot4(q[2 * i], l[0], l[1], a);
+        b = dot4(q[2 * i + 1], l[2], l[3], b);
+    }
+    return a + b;
+}
+__device__ __forceinline__ float dot16s(const uint32_t* q, const uint8_t* xs, const uint8_t* xl) {
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const u32x4 h = *reinterpret_cast<const u32x4*>(xs + 16 * i);
+        const u32x4 l = *reinterpret_cast<const u32x4*>(xl + 16 * i);
+        a = dot4(q[2 * i], h[0], h[1], a);
+        b = dot4(q[2 * i + 1], h[2], h[3], b);
+        a = dot4(q[2 * i], l[0], l[1], a);
+        b = dot4(q[2 * i + 1], l[2], l[3], b);
+    }
+    return a + b;
+}
+
+// A sub-block's 32 activations in registers (hi and, for split vectors, lo) with its sums.
+struct GqXr {
+    u32x4 h[4], l[4];
+    float s[2];  // per-32 sum (Q4_K / Q5_K) or the two per-16 sums (Q6_K)
+};
+template <bool SPLIT>
+__device__ __forceinline__ float dot16x(const uint32_t* q, const GqXr& r, int half) {
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const u32x4 h = r.h[2 * half + i];
+        a = dot4(q[2 * i], h[0], h[1], a);
+        b = dot4(q[2 * i + 1], h[2], h[3], b);
+        if (SPLIT) {
+            const u32x4 l = r.l[2 * half + i];
+            a = dot4(q[2 * i], l[0], l[1], a);
+            b = dot4(q[2 * i + 1], l[2], l[3], b);
+        }
+    }
+    return a + b;
+}
+template <bool SPLIT>
+__device__ __forceinline__ float dot32x(const uint32_t q[8], const GqXr& r) {
+    return dot16x<SPLIT>(q, r, 0) + dot16x<SPLIT>(q + 4, r, 1);
 }
 
 template <int TYPE> struct GqUnit;
@@ -131,8 +186,12 @@ __device__ __forceinline__ void gq_wait_dma() {
 // position along K. Every 128 values (256 bytes) are followed by 16 bytes of padding: the
 // lanes of a wave read the vector at strides of 256 or 512 bytes (one unit each), which
 // without the padding would put every lane's 16-byte read on the same four banks.
+// fp32 / fp16 activations are held as two bf16 vectors, hi = bf16(x) and lo = bf16(x - hi)
+// (hi + lo carries 16 significant bits, an fp16 value exactly); the dot products then run
+// over both and the sums are of hi + lo.
 struct GqVec {
     const uint8_t* v;    // bf16 [K], padded
+    const uint8_t* lo;   // bf16 [K], padded, or null
     const float* s32;    // [K / 32]
     const float* s16;    // [K / 16]
 };
@@ -140,6 +199,140 @@ struct GqVec {
 // Byte offset of value kk in the padded vector (kk a multiple of 8).
 __host__ __device__ constexpr uint32_t gq_pad(uint32_t kk) { return 2 * kk + 16 * (kk >> 7); }
 __device__ __forceinline__ const uint8_t* gq_x(const GqVec& x, uint32_t kk) { return x.v + gq_pad(kk); }
+__device__ __forceinline__ const uint8_t* gq_xl(const GqVec& x, uint32_t kk) { return x.lo + gq_pad(kk); }
+
+// LDS bytes of a staged vector of n values (n % 32 == 0): padded bf16 values, then the
+// per-32 and per-16 sums.
+__host__ __device__ constexpr int gq_vec_vbytes(int n) { return (int)gq_pad((uint32_t)((n + 127) / 128 * 128)); }
+__host__ __device__ constexpr int gq_vec_bytes(int n, bool split = false) {
+    return gq_vec_vbytes(n) * (split ? 2 : 1) + 4 * (n / 32) + 4 * (n / 16);
+}
+
+// The LDS layout of a staged vector of n values at dst.
+__device__ __forceinline__ GqVec gq_vec(uint8_t* dst, int n, bool split = false) {
+    GqVec vec;
+    vec.v = dst;
+    vec.lo = split ? dst + gq_vec_vbytes(n) : nullptr;
+    vec.s32 = reinterpret_cast<float*>(dst + gq_vec_vbytes(n) * (split ? 2 : 1));
+    vec.s16 = vec.s32 + n / 32;
+    return vec;
+}
+
+// Stages nv vectors of n values (n % 32 == 0): vector jj from src (dtype) at element
+// off0 + jj * src_stride into LDS at dst0 + jj * dst_stride as bf16 (RNE; non-bf16 sources
+// as the hi / lo pair, the layout gq_vec(.., n, true) describes), with the sums over every
+// 32 and 16 consecutive positions. Threads tid of nthr (nthr a multiple of 64, whole waves
+// calling) take 8-value chunks in lane order, so each load instruction reads one
+// contiguous span (16 bytes per lane for bf16 / fp16, 32 for fp32; rows 16-byte aligned,
+// as the callers' are); the 16- and 32-value sums come from neighbouring lanes by DPP.
+__device__ void gq_stage_vecs(uint8_t* dst0, int dst_stride, const void* src, int dtype, int64_t off0,
+                              int64_t src_stride, int n, int nv, int tid, int nthr) {
+    const bool split = dtype != TSA_BF16;
+    const int cpv = n / 8, total = cpv * nv;  // chunks per vector (a multiple of 4)
+    for (int base = 0; base < total; base += nthr) {
+        const int i = base + tid;
+        const bool valid = i < total;
+        const int jj = valid ? i / cpv : 0, c = valid ? i - jj * cpv : 0;
+        const int64_t e = off0 + jj * src_stride + 8 * (int64_t)c;  // first element of the chunk
+        uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+        float s8 = 0.0f;
+        if (valid) {
+            float f[8];
+            if (dtype == TSA_BF16) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + e);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    hw[q] = v[q];
+                    s8 += bf16_bits_to_f32(v[q] & 0xFFFFu) + bf16_bits_to_f32(v[q] >> 16);
+                }
+            } else {
+                if (dtype == TSA_F32) {
+                    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + e);
+                    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + e + 4);
+                    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+                } else {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + e);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        f[2 * q] = f16_bits_to_f32(v[q] & 0xFFFFu);
+                        f[2 * q + 1] = f16_bits_to_f32(v[q] >> 16);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const uint32_t h = f32_to_bf16_bits(f[q]);
+                    const float hf = bf16_bits_to_f32(h);
+                    const uint32_t l = f32_to_bf16_bits(f[q] - hf);
+                    hw[q / 2] |= h << (16 * (q & 1));
+                    lw[q / 2] |= l << (16 * (q & 1));
+                    s8 += hf + bf16_bits_to_f32(l);  // hi + lo exactly: 16 significant bits
+                }
+            }
+        }
+        // lanes 4m .. 4m + 3 hold chunks 4m' .. 4m' + 3 of one vector (cpv % 4 == 0)
+        const float s16 = s8 + dpp_f<0xB1, 0xF, 0xF>(s8, 0.0f);    // quad_perm [1,0,3,2]
+        const float s32 = s16 + dpp_f<0x4E, 0xF, 0xF>(s16, 0.0f);  // quad_perm [2,3,0,1]
+        if (valid) {
+            uint8_t* dst = dst0 + jj * dst_stride;
+            const GqVec vec = gq_vec(dst, n, split);
+            *reinterpret_cast<u32x4*>(dst + gq_pad(8 * c)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            if (split)
+                *reinterpret_cast<u32x4*>(const_cast<uint8_t*>(vec.lo) + gq_pad(8 * c)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+            if ((c & 1) == 0) const_cast<float*>(vec.s16)[c / 2] = s16;
+            if ((c & 3) == 0) const_cast<float*>(vec.s32)[c / 4] = s32;
+        }
+    }
+}
+__device__ void gq_stage(uint8_t* dst, const void* src, int dtype, int64_t off, int n, int tid, int nthr) {
+    gq_stage_vecs(dst, 0, src, dtype, off, 0, n, 1, tid, nthr);
+}
+
+// The per-32 and per-16 sums of a bf16 vector already in LDS at vec (n values), one wave.
+__device__ void gq_vec_sums(const GqVec& vec, int n, int lane) {
+    float* s32 = const_cast<float*>(vec.s32);
+    float* s16 = const_cast<float*>(vec.s16);
+    for (int g = lane; g < n / 32; g += 64) {
+        const u32x4* p4 = reinterpret_cast<const u32x4*>(gq_x(vec, 32 * g));
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 w = p4[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float r = bf16_bits_to_f32(w[e] & 0xFFFFu) + bf16_bits_to_f32(w[e] >> 16);
+                if (i < 2) a += r; else b += r;
+            }
+        }
+        s16[2 * g] = a;
+        s16[2 * g + 1] = b;
+        s32[g] = a + b;
+    }
+}
+
+// Super-blocks (or Q8_0 blocks) touched by the values [lo, hi) of a TYPE stream, and the
+// LDS bytes a wave needs to stage them (16-byte aligned start, rounded up).
+template <int TYPE>
+__host__ __device__ constexpr uint32_t gq_sb_count(uint32_t lo, uint32_t hi) {
+    constexpr uint32_t VS = TYPE == 8 ? 32 : 256;
+    return (hi + VS - 1) / VS - lo / VS;
+}
+__host__ __device__ constexpr uint32_t gq_raw_bytes(uint32_t nsb, uint32_t sb) { return (nsb * sb + 15 + 15) / 16 * 16; }
+
+// Host-side shape choice shared by the launches over unit streams. A wave that reduces
+// `units` units (one per lane per round) takes ceil(units / 64) rounds; a SIMD issues its
+// waves' rounds back to back when it holds several (throughput), while a lone wave waits
+// on its own LDS and dot-product chains, measured at about 4x its issue time (latency).
+// The cost is the larger of the two; the launchers pick the rows per wave with the least
+// cost, and on a tie the most rows (fewer workgroups stage the activations).
+__host__ inline double gq_cost(double units, double waves, int cus) {
+    const double rounds = __builtin_ceil(units / 64.0), per_simd = waves / (4.0 * cus);
+    return rounds * (per_simd > 4.0 ? per_simd : 4.0);
+}
+// Units a wave of `rows` rows of K values reduces (unit size v; rows that start inside a
+// unit cost one more).
+__host__ inline double gq_units(int rows, int64_t K, uint32_t v) {
+    return K % v == 0 ? (double)rows * (double)(K / v) : __builtin_ceil((double)rows * (double)K / v) + 1.0;
+}
 
 // Dot products of unit u (unit index in the flat stream) with the vector; b points at the
 // unit's super-block (or block) in LDS. The unit's values start at column kk0 of some row
@@ -149,9 +342,13 @@ __device__ __forceinline__ const uint8_t* gq_x(const GqVec& x, uint32_t kk) { re
 // (matrices below 2^31 values).
 // WRAP = false: K is a multiple of the unit's values, so every unit lies inside one row
 // and inside [lo, hi) (the caller's units are whole rows); the row checks compile away.
-template <int TYPE, bool WRAP = true>
+template <int TYPE, bool WRAP = true, bool SPLIT = false>
 __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t u, uint32_t kk0, uint32_t K, uint32_t lo,
                                         uint32_t hi, const GqVec& x, float& pa, float& pb) {
+    auto d32 = [&](const uint32_t q[8], uint32_t kk) {
+        return SPLIT ? dot32s(q, gq_x(x, kk), gq_xl(x, kk)) : dot32(q, gq_x(x, kk));
+    };
+
     using U = GqUnit<TYPE>;
     const uint32_t g0 = u * U::V;
     auto add = [&](uint32_t j, float part) {
@@ -163,6 +360,25 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         return WRAP && kk >= K ? kk - K : kk;
     };
     auto outside = [&](uint32_t g) { return WRAP && (g < lo || g >= hi); };
+    // sub-block j's activations into r (issued a sub-block ahead of their use: the LDS
+    // latency then overlaps the previous sub-block's arithmetic)
+    auto ldx = [&](uint32_t j, GqXr& r) {
+        const uint32_t kk = col(j);
+        const uint8_t* ph = gq_x(x, kk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.h[i] = ld16u(ph + 16 * i);
+        if (SPLIT) {
+            const uint8_t* pl = gq_xl(x, kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.l[i] = ld16u(pl + 16 * i);
+        }
+        if (TYPE == 14) {
+            r.s[0] = x.s16[kk / 16];
+            r.s[1] = x.s16[kk / 16 + 1];
+        } else {
+            r.s[0] = x.s32[kk / 32];
+        }
+    };
     if constexpr (TYPE == 8) {
         if (outside(g0)) return;
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b));
@@ -177,10 +393,9 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
             qh[4 + i] = (wc >> 4) & 0x0F0F0F0Fu;
         }
         const uint32_t kk = kk0;
-        const uint8_t* xs = gq_x(x, kk);
         const float sx = x.s32[kk / 32];
         // sum q x = sum (16 qh + ql - 128) x
-        const float dl = dot32(ql, xs) - 128.0f * sx, dh = dot32(qh, xs) - 128.0f * sx;
+        const float dl = d32(ql, kk) - 128.0f * sx, dh = d32(qh, kk) - 128.0f * sx;
         pa += d * (16.0f * dh + dl - 128.0f * sx);
     } else if constexpr (TYPE == 12 || TYPE == 13) {
         constexpr int QS = TYPE == 12 ? 16 : 48;
@@ -195,8 +410,12 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         }
         const float d = f16_bits_to_f32(hdr[0] & 0xFFFFu), dmin = f16_bits_to_f32(hdr[0] >> 16);
         const uint32_t s[3] = {hdr[1], hdr[2], hdr[3]};
+        GqXr xr[2];
+        ldx(0, xr[0]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
+            if (j + 1 < 8) ldx(j + 1, xr[(j + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
             if (outside(g0 + 32 * j)) continue;
             uint32_t sc, m;
             k_scale_min(s, j, sc, m);
@@ -208,9 +427,8 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
                 if constexpr (TYPE == 13) n |= ((hv[i >> 2][i & 3] >> j) & 0x01010101u) << 4;
                 q[i] = n;
             }
-            const uint32_t kk = col(j);
-            const float sx = x.s32[kk / 32];
-            const float dq = dot32(q, gq_x(x, kk)) - 128.0f * sx;
+            const float sx = xr[j & 1].s[0];
+            const float dq = dot32x<SPLIT>(q, xr[j & 1]) - 128.0f * sx;
             add(j, d * (float)sc * dq - dmin * (float)m * sx);
         }
     } else {  // Q6_K, half h of super-block u / 2: ql[64h, +64), qh[32h, +32), sc[8h, +8), d @208
@@ -222,8 +440,12 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         qh[1] = ld16u(b + 144 + 32 * hh);
         const uint2 scw = *reinterpret_cast<const uint2*>(b + 192 + 8 * hh);
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b + 208));
+        GqXr xr[2];
+        ldx(0, xr[0]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {  // 32-value quarter t of the half
+            if (t + 1 < 4) ldx(t + 1, xr[(t + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
             if (outside(g0 + 32 * t)) continue;
             uint32_t q[8];
             const int shl = 4 * (t >> 1), shh = 2 * t;
@@ -231,14 +453,13 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
             for (int i = 0; i < 8; ++i)
                 q[i] = ((l[2 * (t & 1) + (i >> 2)][i & 3] >> shl) & 0x0F0F0F0Fu) |
                        (((qh[i >> 2][i & 3] >> shh) & 0x03030303u) << 4);
-            const uint32_t kk = col(t);
-            const uint8_t* xs = gq_x(x, kk);
-            const float s0 = x.s16[kk / 16], s1 = x.s16[kk / 16 + 1];
+            const float s0 = xr[t & 1].s[0], s1 = xr[t & 1].s[1];
             const uint32_t sw = t < 2 ? scw.x : scw.y;
             const float sc0 = (float)(int8_t)((sw >> (16 * (t & 1))) & 0xFFu);
             const float sc1 = (float)(int8_t)((sw >> (16 * (t & 1) + 8)) & 0xFFu);
             // codes are q + 32 (0..63): sum (q) x = sum (128 + q + 32) x - 160 sum x
-            const float a0 = dot16(q, xs) - 160.0f * s0, a1 = dot16(q + 4, xs + 32) - 160.0f * s1;
+            const float a0 = dot16x<SPLIT>(q, xr[t & 1], 0) - 160.0f * s0;
+            const float a1 = dot16x<SPLIT>(q + 4, xr[t & 1], 1) - 160.0f * s1;
             add(t, d * (sc0 * a0 + sc1 * a1));
         }
     }

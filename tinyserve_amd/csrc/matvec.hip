@@ -138,7 +138,18 @@ int pick_tch(int64_t T, int64_t K) {
 }  // namespace
 }  // namespace tsa
 
+namespace tsa {
+const char* gq_matvec_unsupported(int type, const void* w, int64_t T, int64_t K, int64_t N, int x_dtype);
+int gq_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T, int64_t K, void* y,
+              int y_dtype, int64_t N, hipStream_t st);
+}  // namespace tsa
+
 using namespace tsa;
+
+// Up to this many tokens per call run on the super-block streaming matvec (gguf_matvec.hip,
+// one workgroup column per token); more tokens reuse each decoded unit across a chunk of
+// tokens in the row kernel above.
+constexpr int64_t GQ_MATVEC_MAX_T = 8;
 
 extern "C" int tsa_gguf_matvec(int ggml_type, const void* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T,
                                int64_t K, void* y, int y_dtype, int64_t N, void* stream) {
@@ -161,9 +172,11 @@ extern "C" int tsa_gguf_matvec(int ggml_type, const void* w, int64_t w_bytes, co
     if (N == 0 || T == 0) return TSA_OK;
     TSA_REQUIRE(w && x && y, TSA_ERR_INVALID_ARG, "null pointer");
     const uint8_t* wb = static_cast<const uint8_t*>(w);
+    hipStream_t st = as_stream(stream);
+    if (T <= GQ_MATVEC_MAX_T && !*gq_matvec_unsupported(ggml_type, w, T, K, N, x_dtype))
+        return gq_matvec(ggml_type, wb, w_bytes, x, x_dtype, T, K, y, y_dtype, N, st);
     const bool a16 = (reinterpret_cast<uintptr_t>(w) & 15) == 0, a2 = (reinterpret_cast<uintptr_t>(w) & 1) == 0;
     const int tch = pick_tch(T, K);
-    hipStream_t st = as_stream(stream);
     hipError_t e;
     switch (ggml_type) {
         case 8: e = a2 ? launch_gguf<8, 2>(wb, x, x_dtype, T, K, y, y_dtype, N, tch, st)

@@ -1,13 +1,14 @@
 // Top-k MoE decode over GGUF experts (gate, up and down as native Q8_0 / Q4_K / Q5_K / Q6_K
 // block streams): two launches, both routing in-kernel when router logits are given.
 //
-//   gq_phase_a: workgroup = one (token, expert) pair and 4 waves x GQ_RW rows of the
-//     intermediate dimension. Each wave streams the super-blocks of its GQ_RW gate rows and
-//     GQ_RW up rows (gguf_dot.h: one unit per lane, 16-byte loads, dot2 over bf16 codes),
+//   gq_phase_a: workgroup = one (token, expert) pair and 4 waves x rw rows (rw <= GQ_RW) of
+//     the intermediate dimension. Each wave streams the super-blocks of its rw gate rows and
+//     rw up rows (gguf_dot.h: one unit per lane, 16-byte loads, dot2 over bf16 codes),
 //     reduces them across the wave and writes h = act(gate, up) as bf16 (the reference
 //     runs its experts in bf16) into the workspace.
-//   gq_phase_b: workgroup = one token and GQ_RB output rows, 8 waves. Wave w takes expert
-//     w % kk (kk = min(k, 8); further experts in rounds) and row slice w / kk, stages that
+//   gq_phase_b: workgroup = one token and 8 waves. Wave w takes expert w % kk (kk =
+//     min(k, 8); further experts in rounds) and slice w / kk of rb output rows (rb <=
+//     GQ_RB; the workgroup covers 8 / kk slices), stages that
 //     expert's h in its LDS area, streams the down rows the same way and keeps the
 //     router-weighted partial per row; the workgroup sums the partials over experts in a
 //     fixed order, so every output has one writer and the result is deterministic.
@@ -22,19 +23,10 @@
 namespace tsa {
 namespace {
 
-constexpr int GQ_RW = 4;         // phase A: intermediate rows per wave
-constexpr int GQ_RB = 8;         // phase B: output rows per workgroup
+constexpr int GQ_RW = 4;         // phase A: intermediate rows per wave, at most
+constexpr int GQ_RB = 8;         // phase B: output rows per wave, at most
 constexpr int GQ_B_WAVES = 8;
 constexpr int GQ_MISC = 2048;    // slot / weight tables, per-(expert, row) partials
-
-// Super-blocks (or Q8_0 blocks) touched by the values [lo, hi) of a TYPE stream, and the
-// LDS bytes a wave needs to stage them (16-byte aligned start, rounded up).
-template <int TYPE>
-__host__ __device__ constexpr uint32_t gq_sb_count(uint32_t lo, uint32_t hi) {
-    constexpr uint32_t VS = TYPE == 8 ? 32 : 256;
-    return (hi + VS - 1) / VS - lo / VS;
-}
-__host__ __device__ constexpr uint32_t gq_raw_bytes(uint32_t nsb, uint32_t sb) { return (nsb * sb + 15 + 15) / 16 * 16; }
 
 struct GqParams {
     tsa_expert_layout L;
@@ -56,86 +48,11 @@ struct GqParams {
     int64_t h_bytes;              // bytes of h (the records of its buffer resource)
     int32_t* tab_slot;            // routed: the slots and weights phase A chose, [T, k]
     float* tab_w;
+    int rw, rb;                   // rows per wave of phase A and of phase B (host-chosen)
     int raw_off_a, raw_stride_a;  // phase A: LDS offset and per-wave stride of the raw super-block areas
     int vec_stride_b;             // phase B: per-wave stride of the staged h vectors (16-byte multiple)
     int raw_off_b, raw_stride_b;  // phase B: raw areas
 };
-
-// LDS bytes of a staged vector of n values (n % 32 == 0): padded bf16 values, then the
-// per-32 and per-16 sums.
-__host__ __device__ constexpr int gq_vec_vbytes(int n) { return (int)gq_pad((uint32_t)((n + 127) / 128 * 128)); }
-__host__ __device__ constexpr int gq_vec_bytes(int n) { return gq_vec_vbytes(n) + 4 * (n / 32) + 4 * (n / 16); }
-
-// The LDS layout of a staged vector of n values at dst.
-__device__ __forceinline__ GqVec gq_vec(uint8_t* dst, int n) {
-    GqVec vec;
-    vec.v = dst;
-    vec.s32 = reinterpret_cast<float*>(dst + gq_vec_vbytes(n));
-    vec.s16 = vec.s32 + n / 32;
-    return vec;
-}
-
-// Stages n values of src (dtype, starting at element off) into LDS at dst as bf16 (RNE),
-// with the sums of the bf16 values over every 32 and 16 consecutive positions. Threads
-// tid of nthr (nthr > 0), each handling 32-value groups with 16-byte loads (src + off
-// 16-byte aligned for bf16 / f16, as the callers' rows are).
-__device__ void gq_stage(uint8_t* dst, const void* src, int dtype, int64_t off, int n, int tid, int nthr) {
-    const GqVec vec = gq_vec(dst, n);
-    float* s32 = const_cast<float*>(vec.s32);
-    float* s16 = const_cast<float*>(vec.s16);
-    for (int g = tid; g < n / 32; g += nthr) {
-        uint32_t bits[16];  // 32 bf16 values, two per word
-        if (dtype == TSA_BF16) {
-            const u32x4* p4 = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + off + 32 * g);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4 v = p4[i];
-                bits[4 * i] = v[0]; bits[4 * i + 1] = v[1]; bits[4 * i + 2] = v[2]; bits[4 * i + 3] = v[3];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float f0 = load_act(src, dtype, off + 32 * g + 2 * i);
-                const float f1 = load_act(src, dtype, off + 32 * g + 2 * i + 1);
-                bits[i] = (uint32_t)f32_to_bf16_bits(f0) | ((uint32_t)f32_to_bf16_bits(f1) << 16);
-            }
-        }
-        float a = 0.0f, b = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float r = bf16_bits_to_f32(bits[i] & 0xFFFFu) + bf16_bits_to_f32(bits[i] >> 16);
-            if (i < 8) a += r; else b += r;
-        }
-        u32x4* d4 = reinterpret_cast<u32x4*>(dst + gq_pad(32 * g));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d4[i] = u32x4{bits[4 * i], bits[4 * i + 1], bits[4 * i + 2], bits[4 * i + 3]};
-        s16[2 * g] = a;
-        s16[2 * g + 1] = b;
-        s32[g] = a + b;
-    }
-}
-
-// The per-32 and per-16 sums of a bf16 vector already in LDS at vec (n values), one wave.
-__device__ void gq_vec_sums(const GqVec& vec, int n, int lane) {
-    float* s32 = const_cast<float*>(vec.s32);
-    float* s16 = const_cast<float*>(vec.s16);
-    for (int g = lane; g < n / 32; g += 64) {
-        const u32x4* p4 = reinterpret_cast<const u32x4*>(gq_x(vec, 32 * g));
-        float a = 0.0f, b = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 w = p4[i];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float r = bf16_bits_to_f32(w[e] & 0xFFFFu) + bf16_bits_to_f32(w[e] >> 16);
-                if (i < 2) a += r; else b += r;
-            }
-        }
-        s16[2 * g] = a;
-        s16[2 * g + 1] = b;
-        s32[g] = a + b;
-    }
-}
 
 __device__ __forceinline__ float gq_act(const tsa_expert_layout& L, float gate, float up) {
     if (L.act == TSA_ACT_SWIGLU_OAI) return swiglu_oai(L, gate, up);
@@ -169,7 +86,7 @@ __device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, 
 }
 
 // Phase A units of one wave: lane i takes units i, i + 64, ... of gate (i < nu) then up.
-template <int TG, bool WRAP>
+template <int TG, bool WRAP, bool SPLIT>
 __device__ __forceinline__ void gq_a_units(const uint8_t* rbuf, uint32_t raw, const uint32_t shift[2], uint32_t s0,
                                            uint32_t u0, uint32_t nu, int n0, int H, uint32_t lo, uint32_t hi,
                                            const GqVec& xv, int lane, float (&acc)[2][GQ_RW]) {
@@ -181,7 +98,7 @@ __device__ __forceinline__ void gq_a_units(const uint8_t* rbuf, uint32_t raw, co
         const uint32_t g0 = u * U::V, row = g0 / (uint32_t)H, kk0 = g0 - row * (uint32_t)H;
         const uint8_t* sb = rbuf + (up ? raw : 0) + shift[up] + (g0 / VS - s0) * SB;
         float pa = 0.0f, pb = 0.0f;
-        gq_unit<TG, WRAP>(sb, u, kk0, H, lo, hi, xv, pa, pb);
+        gq_unit<TG, WRAP, SPLIT>(sb, u, kk0, H, lo, hi, xv, pa, pb);
         const int r = (int)row - n0;
         if (up) {
             acc_add(acc[1], r, pa);
@@ -221,16 +138,17 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     const int a = blockIdx.y, t = a / k;
     int* s_slot = reinterpret_cast<int*>(smem);
     float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
-    const GqVec xv = gq_vec(smem + GQ_MISC, H);
+    const bool split = p.x_dtype != TSA_BF16;
+    const GqVec xv = gq_vec(smem + GQ_MISC, H, split);
     gq_route(p, t, blockIdx.x == 0 && a % k == 0, s_slot, s_w);
     if (!p.logits) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid, 256);
     else if (tid >= 64) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid - 64, 192);
     __syncthreads();
     const int64_t slot = uniform(s_slot[gq_sel(p, t) + a % k]);
     if (slot < 0 || slot >= p.n_slots) return;  // a dead pair's h is never read
-    const int n0 = ((int)blockIdx.x * 4 + wave) * GQ_RW;
+    const int n0 = ((int)blockIdx.x * 4 + wave) * p.rw;
     if (n0 >= I) return;
-    const int n1 = n0 + GQ_RW < I ? n0 + GQ_RW : I;
+    const int n1 = n0 + p.rw < I ? n0 + p.rw : I;
     const uint8_t* base = p.pool + slot * L.slot_bytes;
     using U = GqUnit<TG>;
     constexpr uint32_t VS = TG == 8 ? 32 : 256, SB = U::SB;
@@ -254,10 +172,15 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int r = 0; r < GQ_RW; ++r) acc[m][r] = 0.0f;
-    if (H % U::V == 0)
-        gq_a_units<TG, false>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
+    const bool wrap = H % U::V != 0;
+    if (!wrap && !split)
+        gq_a_units<TG, false, false>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
+    else if (!wrap)
+        gq_a_units<TG, false, true>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
+    else if (!split)
+        gq_a_units<TG, true, false>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
     else
-        gq_a_units<TG, true>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
+        gq_a_units<TG, true, true>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
 #pragma unroll
     for (int r = 0; r < GQ_RW; ++r) {
         const float g = wave_sum_u(acc[0][r]), u = wave_sum_u(acc[1][r]);
@@ -276,7 +199,7 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
     int* s_slot = reinterpret_cast<int*>(smem);
     float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
     float* s_part = reinterpret_cast<float*>(smem + 8 * FUSED_MAXT * FUSED_MAXK);  // [8 waves][GQ_RB]
-    uint8_t* hbuf = smem + GQ_MISC + wave * p.vec_stride_b;
+    uint8_t* hbuf = smem + GQ_MISC + (wave % (k < GQ_B_WAVES ? k : GQ_B_WAVES)) * p.vec_stride_b;  // this wave's expert
     gq_route(p, t, false, s_slot, s_w);
     for (int i = tid; i < GQ_B_WAVES * GQ_RB; i += blockDim.x) s_part[i] = 0.0f;
     __syncthreads();
@@ -284,53 +207,52 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
     const int kk = k < GQ_B_WAVES ? k : GQ_B_WAVES;          // experts per round
     const int S = GQ_B_WAVES / kk;                            // row slices
     const int slice = wave / kk, jw = wave % kk;
-    const int rows_per = GQ_RB / S;
-    const int nb0 = (int)blockIdx.x * GQ_RB;
+    const int rows_per = p.rb;
+    const int nb0 = (int)blockIdx.x * S * rows_per;
     const int n0 = nb0 + slice * rows_per;
     const int n1 = n0 + rows_per < H ? n0 + rows_per : H;
     using U = GqUnit<TD>;
+    constexpr uint32_t VS = TD == 8 ? 32 : 256, SB = U::SB;
     float acc[GQ_RB];
 #pragma unroll
     for (int r = 0; r < GQ_RB; ++r) acc[r] = 0.0f;
-    if (slice < S && n0 < n1) {
-        const uint32_t lo = (uint32_t)n0 * I, hi = (uint32_t)n1 * I;
-        const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
-        constexpr uint32_t VS = TD == 8 ? 32 : 256, SB = U::SB;
-        const uint32_t s0 = lo / VS, raw = gq_raw_bytes(gq_sb_count<TD>(lo, hi), SB);
-        uint8_t* rbuf = smem + p.raw_off_b + wave * p.raw_stride_b;
-        const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
-        for (int j = jw; j < k; j += kk) {
-            const int pair = t * k + j;
-            const int64_t slot = uniform(s_slot[gq_sel(p, t) + j]);
-            if (slot < 0 || slot >= p.n_slots) continue;
+    const bool mine = slice < S && n0 < n1;
+    const uint32_t lo = (uint32_t)n0 * I, hi = (uint32_t)(mine ? n1 : n0) * I;
+    const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
+    const uint32_t s0 = lo / VS, raw = gq_raw_bytes(gq_sb_count<TD>(lo, hi), SB);
+    uint8_t* rbuf = smem + p.raw_off_b + wave * p.raw_stride_b;
+    const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
+    for (int j0 = 0; j0 < k; j0 += kk) {  // rounds of kk experts (workgroup-uniform)
+        const int j = j0 + jw, nj = k - j0 < kk ? k - j0 : kk;
+        const int64_t slot = j < k ? uniform(s_slot[gq_sel(p, t) + j]) : -1;
+        const bool live = mine && j < k && slot >= 0 && slot < p.n_slots;
+        const uint32_t first = (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
+        if (live) gq_stage_raw(p.pool + slot * L.slot_bytes, (uint32_t)L.slot_bytes, first - shift, raw, lds_r, lane);
+        // the round's h vectors (bf16 from phase A) into LDS once for the workgroup: vector jj
+        // at smem + GQ_MISC + jj * vec_stride_b, staged by all threads together
+        gq_stage_vecs(smem + GQ_MISC, p.vec_stride_b, p.h, TSA_BF16, (int64_t)(t * k + j0) * I, I, I, nj, tid,
+                      blockDim.x);
+        gq_wait_dma();
+        __syncthreads();
+        if (live) {
             const float wj = s_w[gq_sel(p, t) + j];
             const GqVec hv = gq_vec(hbuf, I);
-            const uint8_t* base = p.pool + slot * L.slot_bytes;
-            const uint32_t first = (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
-            gq_stage_raw(base, (uint32_t)L.slot_bytes, first - shift, raw, lds_r, lane);
-            gq_stage_vec_raw(reinterpret_cast<const uint8_t*>(p.h), (uint32_t)p.h_bytes, (uint32_t)pair * I * 2u,
-                             2u * I, (uint32_t)reinterpret_cast<uintptr_t>(hbuf), lane);
-            gq_wait_dma();
-            gq_vec_sums(hv, I, lane);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             if (I % U::V == 0)
                 gq_b_units<TD, false>(rbuf, shift, s0, u0, nu, n0, I, lo, hi, hv, wj, lane, acc);
             else
                 gq_b_units<TD, true>(rbuf, shift, s0, u0, nu, n0, I, lo, hi, hv, wj, lane, acc);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();  // every lane is done with hbuf before it is restaged
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         }
+        __syncthreads();  // the round's h and raw areas are free again
     }
 #pragma unroll
     for (int r = 0; r < GQ_RB; ++r) {
-        const float v = wave_sum_u(acc[r]);
-        if (lane == 0 && r < rows_per) s_part[wave * GQ_RB + r] = v;
+        if (r < rows_per) {
+            const float v = wave_sum_u(acc[r]);
+            if (lane == 0) s_part[wave * GQ_RB + r] = v;
+        }
     }
     __syncthreads();
-    if (tid < GQ_RB) {  // row nb0 + tid = slice tid / rows_per, row tid % rows_per of that slice
+    if (tid < S * rows_per) {  // row nb0 + tid = slice tid / rows_per, row tid % rows_per of that slice
         const int sl = tid / rows_per, r = tid % rows_per;
         float sum = 0.0f;
         for (int j = 0; j < kk; ++j) sum += s_part[(sl * kk + j) * GQ_RB + r];
@@ -412,20 +334,38 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     p.h_bytes = h_bytes;
     p.tab_slot = reinterpret_cast<int32_t*>(ws + tab_off);
     p.tab_w = reinterpret_cast<float*>(ws + tab_off + T * k * 4);
-    // raw staging per wave: phase A GQ_RW rows of gate and of up (K = hidden); phase B the
-    // rows of one expert's down slice (K = inter); the largest over row alignments
+    // rows per wave (gq_cost) and the raw staging per wave: phase A rw rows of gate and of
+    // up (K = hidden); phase B rb rows of one expert's down (K = inter); the largest over
+    // row alignments
     const int ta = L.gate_type, tb = L.down_type;
     auto sb_bytes = [](int t) { return t == 8 ? 34u : t == 12 ? 144u : t == 13 ? 176u : 210u; };
     auto vs = [](int t) { return t == 8 ? 32u : 256u; };
-    const uint32_t rawA = gq_raw_bytes((GQ_RW * (uint32_t)L.hidden + vs(ta) - 1) / vs(ta) + 1, sb_bytes(ta));
+    auto uv = [](int t) { return t == 8 ? 32u : t == 14 ? 128u : 256u; };
+    const int cus = num_cus();
+    const size_t vecA = ((size_t)gq_vec_bytes((int)L.hidden, x_dtype != TSA_BF16) + 15) / 16 * 16;
+    const size_t vecB = ((size_t)gq_vec_bytes((int)L.inter) + 15) / 16 * 16;
+    auto raw_a = [&](int rw) { return gq_raw_bytes((rw * (uint32_t)L.hidden + vs(ta) - 1) / vs(ta) + 1, sb_bytes(ta)); };
+    auto raw_b = [&](int rb) { return gq_raw_bytes((rb * (uint32_t)L.inter + vs(tb) - 1) / vs(tb) + 1, sb_bytes(tb)); };
     const int kk = k < GQ_B_WAVES ? k : GQ_B_WAVES;
-    const uint32_t rowsB = GQ_RB / (GQ_B_WAVES / kk);
-    const uint32_t rawB = gq_raw_bytes((rowsB * (uint32_t)L.inter + vs(tb) - 1) / vs(tb) + 1, sb_bytes(tb));
-    const size_t vecA = ((size_t)gq_vec_bytes((int)L.hidden) + 15) / 16 * 16;
+    const int S = GQ_B_WAVES / kk;
+    double best_a = 0.0, best_b = 0.0;
+    for (int rw = 1; rw <= GQ_RW; ++rw) {
+        if (GQ_MISC + vecA + 8 * (size_t)raw_a(rw) > 160 * 1024) break;
+        const double c = gq_cost(2 * gq_units(rw, L.hidden, uv(ta)), (double)((L.inter + rw - 1) / rw) * T * k, cus);
+        if (p.rw == 0 || c <= best_a) { best_a = c; p.rw = rw; }
+    }
+    for (int rb = 1; rb <= GQ_RB; ++rb) {
+        if (GQ_MISC + GQ_B_WAVES * (vecB + raw_b(rb)) > 160 * 1024) break;
+        const double c = gq_cost(gq_units(rb, L.inter, uv(tb)) * ((k + kk - 1) / kk),
+                                 (double)((L.hidden + S * rb - 1) / (S * rb)) * GQ_B_WAVES * T, cus);
+        if (p.rb == 0 || c <= best_b) { best_b = c; p.rb = rb; }
+    }
+    TSA_REQUIRE(p.rw > 0 && p.rb > 0, TSA_ERR_SHAPE, "GGUF decode: rows of %lld / %lld values exceed LDS",
+                (long long)L.hidden, (long long)L.inter);
+    const uint32_t rawA = raw_a(p.rw), rawB = raw_b(p.rb);
     const size_t lds_a = GQ_MISC + vecA + 4 * 2 * (size_t)rawA;
     p.raw_off_a = (int)(GQ_MISC + vecA);
     p.raw_stride_a = (int)(2 * rawA);
-    const size_t vecB = ((size_t)gq_vec_bytes((int)L.inter) + 15) / 16 * 16;
     p.vec_stride_b = (int)vecB;
     p.raw_off_b = (int)(GQ_MISC + GQ_B_WAVES * vecB);
     p.raw_stride_b = (int)rawB;
@@ -437,7 +377,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     if (lds_b > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fb, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
     if (lds_a > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fa, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_a));
     void* args[] = {&p};
-    const dim3 ga((unsigned)((L.inter + 4 * GQ_RW - 1) / (4 * GQ_RW)), (unsigned)(T * k));
+    const dim3 ga((unsigned)((L.inter + 4 * p.rw - 1) / (4 * p.rw)), (unsigned)(T * k));
     TSA_HIP_CHECK(hipLaunchKernel(fa, ga, dim3(256), args, lds_a, st));
     GqParams pb = p;  // phase B takes the routed table as its slot / weight input
     if (logits) {
@@ -446,7 +386,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
         pb.wts = p.tab_w;
     }
     void* args_b[] = {&pb};
-    const dim3 gb((unsigned)((L.hidden + GQ_RB - 1) / GQ_RB), (unsigned)T);
+    const dim3 gb((unsigned)((L.hidden + S * pb.rb - 1) / (S * pb.rb)), (unsigned)T);
     TSA_HIP_CHECK(hipLaunchKernel(fb, gb, dim3(64 * GQ_B_WAVES), args_b, lds_b, st));
     return TSA_OK;
 }
