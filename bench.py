@@ -19,7 +19,10 @@ MXFP4 MFMA GEMMs (one step = one whole prefill of the layer: routing, grouping, 
 SwiGLU, down, weighted combine); value = algorithmic FLOPs / time (TFLOP/s), against the
 dense bf16 MFMA peak.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {3,4,5}]
+--workload 1 / 2 / 4 measure the GGUF paths (a Q8_0 matvec, one Q4_K/Q6_K expert, a
+Qwen3-30B-A3B-shaped Q5_K/Q6_K MoE layer) the same way, in GB/s of algorithmic bytes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5}]
 """
 from __future__ import annotations
 
@@ -184,6 +187,87 @@ class MoEWorkload:
             _lib.BF16, self.idx[s].data_ptr(), self.w[s].data_ptr(), self.ws.data_ptr(), self.ws.numel(), st))
 
 
+class GgufWorkload:
+    """Workloads 1 and 2: one GGUF matrix (Q8_0 2880 x 2880, fp32 x; tsa_gguf_matvec) or one
+    GGUF expert (Q4_K gate/up, Q6_K down, bf16 x; tsa_moe_decode with k = 1), over copies of
+    the seeded weights rotated per step (about 0.5 GB) so the 256 MB Infinity Cache cannot
+    serve them."""
+
+    def __init__(self, wl: int, n_steps: int, dev: torch.device):
+        self.wl = wl
+        base = synth.workload(wl)
+        self.tiled = False
+        if wl == 1:
+            self.N, self.K = base["N"], base["K"]
+            self.w_bytes = base["w"].size
+            self.copies = 64
+            self.w = torch.from_numpy(np.tile(base["w"], self.copies)).to(dev)
+            self.x = torch.from_numpy(base["x"]).to(dev).view(1, -1)
+            self.y = torch.empty((1, self.N), device=dev)
+        else:
+            self.H, self.I = base["hidden"], base["inter"]
+            self.L = gguf_expert_layout(base["layout"], {"gate": 12, "up": 12, "down": 14},
+                                        {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
+            self.copies = 32
+            self.pool = torch.from_numpy(np.tile(base["slot"], self.copies)).to(dev).view(self.copies, -1)
+            self.x = _bf16(base["x_bits"], dev).view(1, -1)
+            self.y = torch.empty((1, self.H), device=dev, dtype=torch.bfloat16)
+            self.slots = (torch.arange(n_steps, dtype=torch.int32, device=dev) % self.copies).view(-1, 1)
+            self.one = torch.ones((1, 1), device=dev)
+            self.ws = ops.moe_decode_workspace(self.L, 1, 1, dev)
+            self.slot_bytes = base["layout"].total_bytes
+        self.logits = self.x  # the step count source for the warmup loop
+
+    def bytes_per_step(self) -> int:
+        """Algorithmic bytes: weights + activations in and out (fp32 for workload 1, bf16 for 2)."""
+        if self.wl == 1:
+            return self.w_bytes + 2 * 4 * self.K
+        return self.slot_bytes + 2 * 2 * self.H
+
+    def step(self, s: int) -> None:
+        lib = _lib.load()
+        st = torch.cuda.current_stream().cuda_stream
+        if self.wl == 1:
+            w = self.w[(s % self.copies) * self.w_bytes:]
+            _lib.check(lib.tsa_gguf_matvec(8, w.data_ptr(), self.w_bytes, self.x.data_ptr(), _lib.F32, 1, self.K,
+                                           self.y.data_ptr(), _lib.F32, self.N, st))
+        else:
+            _lib.check(lib.tsa_moe_decode(ctypes.byref(self.L), self.pool.data_ptr(), self.copies,
+                                          self.slots[s].data_ptr(), self.one.data_ptr(), 1, 1, self.x.data_ptr(),
+                                          _lib.BF16, self.y.data_ptr(), _lib.BF16, self.ws.data_ptr(), self.ws.numel(),
+                                          st))
+
+
+def cpu_baseline_gguf(wl_id: int, budget_s: float = 12.0) -> dict:
+    """The oracle's workload 1 / 2 path (numpy dequant of the whole matrix or expert, then
+    fp32 matvec; SURVEY's CPU restatement of gguf_dequant_torch + F.linear) on this host."""
+    from threadpoolctl import threadpool_info
+
+    from oracle import expert as oex
+    from oracle import gguf as og
+
+    wl = synth.workload(wl_id)
+    if wl_id == 1:
+        x = wl["x"].reshape(1, -1)
+        fn = lambda: x @ og.dequant_tensor(wl["w"], 8, (wl["N"], wl["K"])).T  # noqa: E731
+        nbytes = wl["w"].size + 2 * 4 * wl["K"]
+    else:
+        x = synth.bf16_to_f32(wl["x_bits"]).reshape(1, -1)
+        fn = lambda: oex.gguf_expert_forward(x, wl["expert"])  # noqa: E731
+        nbytes = wl["layout"].total_bytes + 2 * 2 * wl["hidden"]
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"{len(times)} calls of workload {wl_id} (median {med * 1e3:.1f} ms; numpy dequant + fp32 BLAS)"}
+
+
 class PrefillWorkload:
     """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
     2048-token prefill; one step = one layer's whole batched MoE."""
@@ -336,7 +420,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
-    ap.add_argument("--workload", type=int, default=3, choices=[3, 4, 5])
+    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--layers-prefill", type=int, default=3, help="workload 5: distinct layers rotated per step")
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -350,7 +434,7 @@ def main() -> int:
     ap.add_argument("--pmc-command", default="", help="the profiled command, recorded with --summarize-pmc")
     args = ap.parse_args()
     kernel_key = "mxt_decode_kernel" if args.workload == 3 and not args.checkpoint_order else (
-        "mx_decode_kernel" if args.workload == 3 else "gguf_phase")
+        "mx_decode_kernel" if args.workload == 3 else "gq_matvec_kernel" if args.workload == 1 else "gq_phase")
     if args.summarize_pmc:
         t = summarize_pmc(*args.summarize_pmc, kernel_key, args.workload, args.pmc_command)
         os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
@@ -373,12 +457,16 @@ def main() -> int:
     n_layers = args.layers
     if args.copy_calibration:
         copy_calibration(dev)
-    wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev, tiled=not args.checkpoint_order)
+    if args.workload in (1, 2):
+        wl = GgufWorkload(args.workload, max(K, W), dev)
+        n_layers = wl.copies
+    else:
+        wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev, tiled=not args.checkpoint_order)
     torch.cuda.synchronize()
 
     # warmup (eager), also validates every call
     for s in range(W):
-        wl.step(s % len(wl.logits))
+        wl.step(s % max(len(wl.logits), 1) if args.workload > 2 else s)
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream()
@@ -421,12 +509,16 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4 weights (e2m1 x e8m0), bf16 activations, fp32 accumulate" if args.workload == 3
-        else "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate",
-        "data": f"synthetic: seeded native-format weights, {n_layers} resident layers rotated per step",
+        "dtype": {1: "gguf q8_0 weights, fp32 activations (bf16 hi/lo pairs), fp32 accumulate",
+                  2: "gguf q4_k/q6_k weights, bf16 activations, fp32 accumulate",
+                  3: "mxfp4 weights (e2m1 x e8m0), bf16 activations, fp32 accumulate",
+                  4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate"}[args.workload],
+        "data": f"synthetic: seeded native-format weights, {n_layers} resident layers (or copies) rotated per step",
         "config": {
-            "workload": "gpt-oss-20b-shaped mxfp4 moe layer decode (hidden 2880, 32 experts, top-4, batch 1)"
-            if args.workload == 3 else "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)",
+            "workload": {1: "gguf q8_0 matvec 2880 x 2880 (GGMLLinear, batch 1)",
+                         2: "one gguf expert ffn, q4_k gate/up 2880 -> 2880, q6_k down (batch 1)",
+                         3: "gpt-oss-20b-shaped mxfp4 moe layer decode (hidden 2880, 32 experts, top-4, batch 1)",
+                         4: "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)"}[args.workload],
             "bytes_per_step": nbytes,
             "layers_rotated": n_layers,
             "pool_layout": "mxfp4 16-row mfma tiles" if wl.tiled else "checkpoint order",
@@ -452,7 +544,7 @@ def main() -> int:
             f"counter's reading for a {4 * COPY_ELEMS >> 20} MiB copy (factors {tr['FETCH_SIZE']['copy_factor']:.3f}, "
             f"{tr['WRITE_SIZE']['copy_factor']:.3f}); algorithmic bytes {nbytes}")
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.workload)
+        line["cpu_baseline"] = cpu_baseline(args.workload) if args.workload > 2 else cpu_baseline_gguf(args.workload)
     print(json.dumps(line))
     return 0
 
