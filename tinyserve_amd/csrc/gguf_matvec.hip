@@ -82,11 +82,9 @@ __global__ void __launch_bounds__(64 * MV_MAX_WAVES) gq_matvec_kernel(MvParams p
         mv_units<TY, true, false>(rbuf, shift, s0, u0, nu, n0, K, lo, hi, xv, lane, acc);
     else
         mv_units<TY, true, true>(rbuf, shift, s0, u0, nu, n0, K, lo, hi, xv, lane, acc);
-#pragma unroll
-    for (int r = 0; r < MV_RW; ++r) {
-        const float v = wave_sum_u(acc[r]);
-        if (lane == r && n0 + r < n1) store_out(p.y, p.y_dtype, (int64_t)t * N + n0 + r, v);
-    }
+    const float tot = wave_sum_rows<MV_RW>(acc, lane);  // lane 16 r: row r
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && n0 + r < n1) store_out(p.y, p.y_dtype, (int64_t)t * N + n0 + r, tot);
 }
 
 const void* mv_kernel(int type) {

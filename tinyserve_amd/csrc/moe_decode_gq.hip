@@ -181,12 +181,14 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
         gq_a_units<TG, true, false>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
     else
         gq_a_units<TG, true, true>(rbuf, raw, shift, s0, u0, nu, n0, H, lo, hi, xv, lane, acc);
-#pragma unroll
-    for (int r = 0; r < GQ_RW; ++r) {
-        const float g = wave_sum_u(acc[0][r]), u = wave_sum_u(acc[1][r]);
-        if (lane == r && n0 + r < n1)
-            p.h[(int64_t)a * I + n0 + r] = f32_to_bf16_bits(gq_act(L, g, u));
-    }
+    static_assert(GQ_RW == 4, "gate and up rows fill the 8 rows of one wave_sum_rows");
+    const float rows8[8] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3], acc[1][0], acc[1][1], acc[1][2], acc[1][3]};
+    const float tot = wave_sum_rows<8>(rows8, lane);     // lane 8 i: gate row i (i < 4) / up row i - 4
+    // up row r (lane 32 + 8 r) lands beside gate row r: the swap's second half, lower lanes
+    const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(tot), __float_as_uint(tot), false, false)[1]);
+    const int r = lane >> 3;
+    if ((lane & 7) == 0 && r < GQ_RW && n0 + r < n1)
+        p.h[(int64_t)a * I + n0 + r] = f32_to_bf16_bits(gq_act(L, tot, up));
 }
 
 template <int TD>
@@ -244,13 +246,9 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
         }
         __syncthreads();  // the round's h and raw areas are free again
     }
-#pragma unroll
-    for (int r = 0; r < GQ_RB; ++r) {
-        if (r < rows_per) {
-            const float v = wave_sum_u(acc[r]);
-            if (lane == 0) s_part[wave * GQ_RB + r] = v;
-        }
-    }
+    static_assert(GQ_RB == 8, "one wave_sum_rows over the rows");
+    const float tot = wave_sum_rows<GQ_RB>(acc, lane);  // lane 8 r: row r
+    if ((lane & 7) == 0 && (lane >> 3) < rows_per) s_part[wave * GQ_RB + (lane >> 3)] = tot;
     __syncthreads();
     if (tid < S * rows_per) {  // row nb0 + tid = slice tid / rows_per, row tid % rows_per of that slice
         const int sl = tid / rows_per, r = tid % rows_per;
