@@ -20,6 +20,10 @@
 //     waves' weighted rows are summed in a fixed order in LDS, so each output has one
 //     writer and the result is deterministic.
 //
+// Schedule: one workgroup per phase A task; a workgroup takes its phase B task (if any)
+// after its phase A task, so its down-tile loads queue behind its gate_up loads and the
+// gate_up bytes that every phase B task waits for arrive first.
+//
 // Synchronisation: per-(token, expert) completion counters as in moe_decode_mx.hip, but
 // only wave 0 of a phase B workgroup polls (the token's k counters, spaced by s_sleep),
 // after every wave has issued its down-tile loads, and the others wait at a barrier:
@@ -65,6 +69,7 @@ struct MxtParams {
     unsigned* flags;  // [T k][WS_FLAG_WORDS]: gate_up task kb of pair (t, j) is published
     int nA, nB, grid;
     int64_t gu_tile, gu_stile, dn_tile, dn_stile;  // bytes per 16-row tile: blocks, scale words
+    int b_off;  // phase B task 0 goes to workgroup b_off (then b_off + 1, ... modulo grid)
 };
 
 // A wave's 16-row tile: MM pieces of 1 KB and the scale words (byte m%4 of word m/4).
@@ -237,6 +242,11 @@ __global__ void __launch_bounds__(256, 3) mxt_decode_kernel(MxtParams p) {
     const int RB = H / 16;
     const int rounds = (k + WAVES - 1) / WAVES;
     uint8_t* hs = vec + wave * KP * 2;
+    {
+        int bt = (int)blockIdx.x - p.b_off;
+        if (bt < 0) bt += p.grid;
+        task = p.nA + bt;
+    }
     for (; task < p.nA + p.nB; task += p.grid) {
         did_b = true;
         const int b = task - p.nA;
@@ -406,7 +416,15 @@ int mxt_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_
     const int cus = num_cus();
     TSA_REQUIRE(per_cu > 0 && cus > 0, TSA_ERR_HIP, "tiled decode kernel cannot be resident (lds %zu)", lds);
     const int resident = per_cu * cus;
-    p.grid = p.nA + p.nB < resident ? p.nA + p.nB : resident;
+    // One workgroup per gate_up task (when they fit): each runs its phase B task after its
+    // phase A task, so down-tile loads are issued behind that workgroup's gate_up loads and
+    // the gate_up stream, which every phase B task waits for, is served first. Phase B task
+    // 0 goes to workgroup grid % cus: workgroups b and b + cus share a CU, so the first
+    // grid % cus CUs already hold two phase A tasks and the phase B tasks go to the others
+    // first (measured at 19.6 us per layer-token against 21.6 with one task per workgroup).
+    const int need = p.nA > p.nB ? p.nA : p.nB;
+    p.grid = need < resident ? need : resident;
+    p.b_off = p.grid % cus;
     void* args[] = {&p};
     TSA_HIP_CHECK(hipLaunchKernel(kfn, dim3(p.grid), dim3(256), args, lds, st));
     return TSA_OK;
