@@ -1,0 +1,165 @@
+"""GGUF experts as packed slots (gate || up || down raw bytes), read from a memory-mapped file.
+
+Mirrors the reference's ``MmapExpertStore`` (tinyserve/mmap_store.py:31-274): the same
+attributes (``num_layers``, ``num_experts``, ``layout``, ``expert_bytes``,
+``buffer_expert_bytes``, ``ggml_types``, ``proj_shapes``) and methods
+(``get_expert_data``, ``allocate_buffer``, ``copy_to_buffer``, ``copy_to_buffer_slot``,
+``from_fused``, ``close``). A slot is the expert's gate, up and down tensors in their
+native GGUF block streams, each padded to the largest size that projection has in any
+layer (mixed quantisation, e.g. Q4_K_M: some layers' tensors are smaller), which is the
+layout the decode kernels read (``expert_forward.gguf_expert_layout``; the per-layer
+ggml types are in ``layer_ggml_types``).
+
+What this build adds: ``load_layer`` copies a whole layer's experts into one device pool
+(all experts resident, as the 288 GB of one GPU allows) and ``expert_layout`` gives the
+matching ``tsa_expert_layout`` for that layer.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .expert_store import ExpertBuffer, TensorLayout
+from .gguf_reader import GGUFReader, GGUFTensorInfo, tensor_nbytes
+
+_PROJS = ("gate", "up", "down")
+
+
+class MmapExpertStore:
+    """Per-expert GGUF tensors (``blk.<L>.ffn_<proj>.<E>.weight``) as packed slots."""
+
+    def __init__(self, path: str | Path):
+        reader = GGUFReader(path)
+        groups = reader.list_expert_tensors()
+        if not groups:
+            reader.close()
+            raise ValueError(f"No per-expert tensors found in {path}")
+        for key, projs in groups.items():
+            missing = set(_PROJS) - set(projs)
+            if missing:
+                reader.close()
+                raise ValueError(f"{path}: layer {key[0]} expert {key[1]} lacks {sorted(missing)}")
+        self._init(reader, groups, sorted({k[0] for k in groups}), sorted({k[1] for k in groups}))
+
+    @classmethod
+    def from_fused(cls, path: str | Path) -> "MmapExpertStore":
+        """Fused tensors ``blk.<L>.ffn_<proj>_exps.weight`` with ne = [in, out, experts]:
+        expert i of a projection is the byte range offset + i * bytes_per_expert
+        (tinyserve/mmap_store.py:166-274); nothing is converted."""
+        reader = GGUFReader(path)
+        fused = reader.list_fused_expert_tensors()
+        if not fused:
+            reader.close()
+            raise ValueError(f"No fused expert tensors in {path}")
+        layers = sorted(fused)
+        groups: dict[tuple[int, int], dict[str, GGUFTensorInfo]] = {}
+        n_experts = None
+        for li in layers:
+            if set(_PROJS) - set(fused[li]):
+                reader.close()
+                raise ValueError(f"{path}: layer {li} lacks fused {sorted(set(_PROJS) - set(fused[li]))}")
+            for proj in _PROJS:
+                info = fused[li][proj]
+                if len(info.shape) != 3:
+                    reader.close()
+                    raise ValueError(f"{path}: {info.name} has {len(info.shape)} dims, fused experts have 3")
+                if n_experts is None:
+                    n_experts = int(info.shape[2])
+                elif int(info.shape[2]) != n_experts:
+                    reader.close()
+                    raise ValueError(f"{path}: {info.name} holds {info.shape[2]} experts, expected {n_experts}")
+                per = tensor_nbytes(info.ggml_type, info.shape[:2])
+                for e in range(n_experts):
+                    groups.setdefault((li, e), {})[proj] = GGUFTensorInfo(
+                        name=f"blk.{li}.ffn_{proj}.{e}.weight", shape=tuple(int(d) for d in info.shape[:2]),
+                        ggml_type=info.ggml_type, ggml_type_name=info.ggml_type_name,
+                        offset=info.offset + e * per, nbytes=per, block_size=info.block_size)
+        store = cls.__new__(cls)
+        store._init(reader, groups, layers, list(range(n_experts)))
+        return store
+
+    def _init(self, reader: GGUFReader, groups, layers: list[int], experts: list[int]) -> None:
+        self._reader = reader
+        self._groups = groups
+        self.num_layers = len(layers)
+        self.num_experts = len(experts)
+        self._layers = layers
+        self._experts = experts
+        self._layer_map = {li: i for i, li in enumerate(layers)}
+        self._expert_map = {e: i for i, e in enumerate(experts)}
+        first = groups[(layers[0], experts[0])]
+        self.ggml_types = {p: first[p].ggml_type for p in _PROJS}
+        self.proj_shapes = {p: tuple(first[p].shape[:2]) for p in _PROJS}
+        self.layer_ggml_types: dict[int, dict[str, int]] = {}
+        nbytes = {p: 0 for p in _PROJS}
+        for (li, _e), projs in groups.items():
+            types = {p: projs[p].ggml_type for p in _PROJS}
+            if self.layer_ggml_types.setdefault(li, types) != types:
+                raise ValueError(f"layer {li}: experts with different ggml types {types}")
+            for p in _PROJS:
+                if tuple(projs[p].shape[:2]) != self.proj_shapes[p]:
+                    raise ValueError(f"{projs[p].name}: shape {projs[p].shape} differs from {self.proj_shapes[p]}")
+                nbytes[p] = max(nbytes[p], projs[p].nbytes)
+        self.layout = TensorLayout({p: ((nbytes[p],), torch.uint8) for p in _PROJS})
+        self._bf16_layout = self.layout
+        self.expert_bytes = self.layout.total_bytes
+        self.buffer_expert_bytes = self.expert_bytes
+        self._staging: torch.Tensor | None = None
+
+    # ---- one expert
+    def _fill(self, dest: np.ndarray, layer_idx: int, expert_idx: int) -> None:
+        projs = self._groups[(layer_idx, expert_idx)]
+        for p in _PROJS:
+            info, off, size = projs[p], self.layout.offsets[p], self.layout.sizes[p]
+            dest[off : off + info.nbytes] = self._reader.tensor_view(info)
+            dest[off + info.nbytes : off + size] = 0  # padding of a smaller (mixed-quant) tensor
+
+    def get_expert_data(self, layer_idx: int, expert_idx: int) -> torch.Tensor:
+        """The packed expert (gate || up || down, padded) as a CPU uint8 tensor."""
+        out = np.empty(self.expert_bytes, dtype=np.uint8)
+        self._fill(out, layer_idx, expert_idx)
+        return torch.from_numpy(out)
+
+    def _staged(self, layer_idx: int, expert_idx: int) -> torch.Tensor:
+        if self._staging is None:
+            self._staging = torch.empty(self.expert_bytes, dtype=torch.uint8,
+                                        pin_memory=torch.cuda.is_available())
+        self._fill(self._staging.numpy(), layer_idx, expert_idx)
+        return self._staging
+
+    def allocate_buffer(self, device: torch.device | str) -> ExpertBuffer:
+        return ExpertBuffer(self.layout, device)
+
+    def copy_to_buffer(self, buf: ExpertBuffer, layer_idx: int, expert_idx: int, non_blocking: bool = False) -> None:
+        buf.packed.copy_(self._staged(layer_idx, expert_idx), non_blocking=non_blocking)
+        if non_blocking and buf.packed.is_cuda:
+            torch.cuda.current_stream(buf.packed.device).synchronize()  # the staging buffer is reused
+
+    def copy_to_buffer_slot(self, cache, slot: int, layer_idx: int, expert_idx: int) -> None:
+        """Copy into row ``slot`` of a slot pool (an object with ``_packed`` [slots, bytes], or the tensor)."""
+        packed = getattr(cache, "_packed", cache)
+        packed[slot].copy_(self._staged(layer_idx, expert_idx))
+
+    # ---- whole layers
+    def load_layer(self, layer_idx: int, device: torch.device | str = "cuda") -> torch.Tensor:
+        """All experts of a layer as a [num_experts, expert_bytes] uint8 pool on ``device``
+        (expert e in slot e)."""
+        host = np.empty((self.num_experts, self.expert_bytes), dtype=np.uint8)
+        for i, e in enumerate(self._experts):
+            self._fill(host[i], layer_idx, e)
+        return torch.from_numpy(host).to(device)
+
+    def expert_layout(self, layer_idx: int):
+        """The kernels' tsa_expert_layout for this layer's slots (its own ggml types)."""
+        from .expert_forward import gguf_expert_layout
+
+        return gguf_expert_layout(self.layout, self.layer_ggml_types[layer_idx], self.proj_shapes, self.expert_bytes)
+
+    @property
+    def layers(self) -> list[int]:
+        return list(self._layers)
+
+    def close(self) -> None:
+        self._reader.close()
