@@ -132,6 +132,15 @@ int tsa_mxfp4_matvec(const void* blocks, const void* scales, const void* bias, i
 int tsa_route_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int k, int mode,
                    int32_t* idx, float* weights, void* stream);
 
+/* Router logits of the MoE block's linear gate: out [T, E] = x [T, H] . w [E, H]^T (+ bias [E],
+ * optional), fp32 accumulation and one rounding to out_dtype, as the router nn.Linear
+ * computes them (bf16 for GPT-OSS). H a multiple of 8; x and w 16-byte aligned (32 for
+ * f32). Feeds tsa_route_topk / tsa_moe_decode_routed on the device: replaces the router
+ * call ahead of the routing closures (tinyserve/_model_hooks.py:424-476; GPT-OSS router
+ * with bias :441-444). */
+int tsa_router_logits(const void* x, int x_dtype, int64_t T, int64_t H, const void* w, int w_dtype,
+                      const void* bias, int bias_dtype, int64_t E, void* out, int out_dtype, void* stream);
+
 /* Workspace bytes tsa_moe_decode needs for T tokens with top-k experts. */
 int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t* bytes);
 

@@ -74,6 +74,7 @@ SIGNATURES = {
     "tsa_mxfp4_tile": (_I32, [_P, _P, _I64, _I64, _P, _P, _P]),
     "tsa_mxfp4_matvec": (_I32, [_P, _P, _P, _I32, _P, _I32, _I64, _P, _I32, _I64, _I64, _P]),
     "tsa_route_topk": (_I32, [_P, _I32, _I64, _I64, _I32, _I32, _P, _P, _P]),
+    "tsa_router_logits": (_I32, [_P, _I32, _I64, _I64, _P, _I32, _P, _I32, _I64, _P, _I32, _P]),
     "tsa_moe_decode_workspace_size": (_I32, [_LP, _I64, _I32, ctypes.POINTER(_I64)]),
     "tsa_moe_decode": (_I32, [_LP, _P, _I64, _P, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I64, _P]),
     "tsa_moe_decode_routed": (_I32, [_LP, _P, _I64, _P, _I64, _P, _I32, _I32, _I64, _I32, _P, _I32, _P, _I32, _P, _P,

@@ -465,44 +465,6 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
     }
 }
 
-// Sums each of R rows (R = 4 or 8; one partial per row per lane) over the 64 lanes: on
-// return every lane holds its group's total, row (lane >> log2(64 / R)), so lane (64 / R) r
-// holds row r. Halving steps first: v_permlane32_swap / v_permlane16_swap hand each half of
-// the wave the other half's partials of the rows it keeps (rows 0 .. n/2-1 stay in the lower
-// lanes), then (R = 8) lanes 8 apart via row_ror:8, which is xor 8 inside a 16-lane row; DPP
-// sums the remaining lane group. All VALU, no LDS round trip: about R + 6 cross-lane steps
-// instead of R full wave reductions.
-__device__ __forceinline__ void permlane_halves(float& lo, float& hi, int off) {
-    // lo: the rows the lower lanes keep, hi: the rows the upper lanes keep; on return
-    // lo = lo + partner's lo in the lower lanes and hi + partner's hi in the upper ones
-    const auto r = off == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false)
-                             : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-    lo = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-template <int R>
-__device__ __forceinline__ float wave_sum_rows(const float (&a)[R], int lane) {
-    static_assert(R == 4 || R == 8, "4 or 8 rows");
-    float v[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = a[i];
-#pragma unroll
-    for (int i = 0; i < R / 2; ++i) permlane_halves(v[i], v[R / 2 + i], 32);
-#pragma unroll
-    for (int i = 0; i < R / 4; ++i) permlane_halves(v[i], v[R / 4 + i], 16);
-    float t = v[0];
-    if (R == 8) {
-        const bool hi = (lane & 8) != 0;
-        const float keep = hi ? v[1] : v[0], send = hi ? v[0] : v[1];
-        t = keep + dpp_f<0x128, 0xF, 0xF>(send, 0.0f);  // row_ror:8
-    }
-    t += dpp_f<0xB1, 0xF, 0xF>(t, 0.0f);   // quad_perm [1,0,3,2]
-    t += dpp_f<0x4E, 0xF, 0xF>(t, 0.0f);   // quad_perm [2,3,0,1]: every lane holds its quad's sum
-    t += dpp_f<0x141, 0xF, 0xF>(t, 0.0f);  // row_half_mirror (lane i reads 7 - i): octet sums
-    if (R == 4) t += dpp_f<0x140, 0xF, 0xF>(t, 0.0f);  // row_mirror (lane i reads 15 - i): 16-lane sums
-    return t;
-}
-
 // Adds v to acc[r] for a row index r known only at run time (0 <= r < N; others dropped).
 template <int N>
 __device__ __forceinline__ void acc_add(float (&acc)[N], int r, float v) {

@@ -1,9 +1,10 @@
 // Router top-k: one wave64 per token; up to 16 logits per lane (E <= 1024).
+// Router logits (router_logits_kernel): the MoE block's linear gate ahead of it.
 //
 // Selection is by logit value, descending, ties to the lower expert id; the
 // softmax is monotone in the logits, so the selected set and order equal a top-k
 // over the softmax probabilities (tinyserve/_model_hooks.py:456-473).
-#include "tsa_common.h"
+#include "fused_common.h"
 
 namespace tsa {
 namespace {
@@ -77,10 +78,90 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const void* __restrict_
     }
 }
 
+// 8 consecutive values of a row (16-byte aligned for 2-byte dtypes, 32 for f32) as fp32.
+__device__ __forceinline__ void load8(const void* base, int dtype, int64_t i, float (&v)[8]) {
+    if (dtype == TSA_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        return;
+    }
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = u[q] & 0xFFFFu, hi = u[q] >> 16;
+        v[2 * q] = dtype == TSA_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+        v[2 * q + 1] = dtype == TSA_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+    }
+}
+
+// out[t, e] = sum_h x[t, h] w[e, h] (+ bias[e]), fp32 accumulation, rounded once to the
+// output dtype (as the router nn.Linear computes it). Workgroup = 4 waves, wave = one
+// expert row e against RT = 8 tokens: lane l takes the 8-value chunks l, l + 64, ... of the
+// row (each load instruction reads 1 KB of w contiguously), each chunk is used for all 8
+// tokens, and one multi-row wave reduction (wave_sum_rows<8>) finishes the 8 dot products.
+constexpr int RT = 8;
+__global__ void __launch_bounds__(256) router_logits_kernel(const void* __restrict__ x, int xdt, int64_t T, int H,
+                                                            const void* __restrict__ w, int wdt,
+                                                            const void* __restrict__ bias, int bdt, int E,
+                                                            void* __restrict__ out, int odt) {
+    const int lane = threadIdx.x & 63;
+    const int e = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int64_t t0 = (int64_t)blockIdx.y * RT;
+    if (e >= E) return;  // whole waves
+    const int nt = T - t0 < RT ? (int)(T - t0) : RT;
+    float acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = 0.0f;
+    for (int c = 8 * lane; c < H; c += 512) {
+        float wv[8];
+        load8(w, wdt, (int64_t)e * H + c, wv);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            if (r < nt) {
+                float xv[8];
+                load8(x, xdt, (t0 + r) * H + c, xv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[r] = fmaf(xv[i], wv[i], acc[r]);
+            }
+        }
+    }
+    const float tot = wave_sum_rows<RT>(acc, lane);  // lane 8 r: token t0 + r
+    const int r = lane >> 3;
+    if ((lane & 7) == 0 && r < nt) {
+        const float b = bias ? load_act(bias, bdt, e) : 0.0f;
+        store_out(out, odt, (t0 + r) * E + e, tot + b);
+    }
+}
+
 }  // namespace
 }  // namespace tsa
 
 using namespace tsa;
+
+extern "C" int tsa_router_logits(const void* x, int x_dtype, int64_t T, int64_t H, const void* w, int w_dtype,
+                                 const void* bias, int bias_dtype, int64_t E, void* out, int out_dtype, void* stream) {
+    clear_error();
+    TSA_REQUIRE(valid_dtype(x_dtype) && valid_dtype(w_dtype) && valid_dtype(out_dtype) &&
+                    (!bias || valid_dtype(bias_dtype)),
+                TSA_ERR_INVALID_ARG, "bad dtype (x %d, w %d, bias %d, out %d)", x_dtype, w_dtype, bias_dtype,
+                out_dtype);
+    TSA_REQUIRE(T >= 0 && E >= 1 && E <= (1 << 20) && H >= 8 && H % 8 == 0 && H <= (1 << 20), TSA_ERR_SHAPE,
+                "router shapes: T %lld, H %lld (a multiple of 8), E %lld", (long long)T, (long long)H, (long long)E);
+    if (T == 0) return TSA_OK;
+    TSA_REQUIRE(x && w && out, TSA_ERR_INVALID_ARG, "null pointer");
+    const auto aligned = [](const void* p, int dt) {
+        return (reinterpret_cast<uintptr_t>(p) & (dt == TSA_F32 ? 31u : 15u)) == 0;
+    };
+    TSA_REQUIRE(aligned(x, x_dtype) && aligned(w, w_dtype), TSA_ERR_INVALID_ARG,
+                "x and w must be 16-byte aligned (32 for f32)");
+    TSA_REQUIRE(T <= (int64_t)65535 * RT, TSA_ERR_SHAPE, "router: more than %d tokens per call", 65535 * RT);
+    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)((T + RT - 1) / RT)), dim3(256), 0,
+                       as_stream(stream), x, x_dtype, T, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype);
+    TSA_LAUNCH_CHECK();
+    return TSA_OK;
+}
 
 extern "C" int tsa_route_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int k, int mode,
                               int32_t* idx, float* weights, void* stream) {

@@ -143,6 +143,23 @@ def route_topk(logits: torch.Tensor, top_k: int, mode: str = "topk_then_softmax"
     return idx, w
 
 
+def router_logits(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The router linear on the GPU: [T, E] = x [T, H] @ weight [E, H]^T (+ bias), fp32
+    accumulation, rounded once to ``out_dtype`` (default: the weight's dtype, as
+    ``F.linear`` returns it)."""
+    _lib.require_device(x, weight, *([bias] if bias is not None else []), what="tensor")
+    E, H = weight.shape
+    x2 = x.reshape(-1, H).contiguous()
+    w = weight.contiguous()
+    b = bias.contiguous() if bias is not None else None
+    out = torch.empty((x2.shape[0], E), dtype=out_dtype or weight.dtype, device=x.device)
+    _lib.check(_lib.load().tsa_router_logits(
+        x2.data_ptr(), _lib.tsa_dtype(x2.dtype), x2.shape[0], H, w.data_ptr(), _lib.tsa_dtype(w.dtype), _lib.ptr(b),
+        _lib.tsa_dtype(b.dtype) if b is not None else 0, E, out.data_ptr(), _lib.tsa_dtype(out.dtype), _stream(x)))
+    return out
+
+
 # ----------------------------------------------------------------------------- MoE
 def _n_slots(pool: torch.Tensor, layout: _lib.ExpertLayout) -> int:
     """Whole slots of ``layout.slot_bytes`` in a contiguous uint8 pool (the kernels index
@@ -209,6 +226,15 @@ def moe_decode_routed(layout: _lib.ExpertLayout, pool: torch.Tensor, expert_slot
         out.data_ptr(), _lib.tsa_dtype(out.dtype), _lib.ptr(idx), _lib.ptr(w), workspace.data_ptr(), workspace.numel(),
         _stream(x)))
     return (out, idx, w) if return_routing else out
+
+
+def moe_decode_gated(layout: _lib.ExpertLayout, pool: torch.Tensor, expert_slot: torch.Tensor, x: torch.Tensor,
+                     router_weight: torch.Tensor, router_bias: torch.Tensor | None, top_k: int,
+                     mode: str = "topk_then_softmax", **kw):
+    """Hidden states to the weighted expert sum without leaving the GPU: the router linear
+    (router_logits), then moe_decode_routed on its logits (keyword arguments pass through)."""
+    logits = router_logits(x, router_weight, router_bias)
+    return moe_decode_routed(layout, pool, expert_slot, logits, x, top_k, mode, **kw)
 
 
 def group_by_expert(idx: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
