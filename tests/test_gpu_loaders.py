@@ -61,3 +61,28 @@ def test_safetensors_checkpoint_decode(tmp_path, tiled):
     ridx, rw = oex.route_topk_then_softmax(logits, k)
     ref = oex.moe_combine(synth.bf16_to_f32(x_bits), ridx, rw, lambda e, xx: oex.mxfp4_expert_forward(xx, exs[0][e]))
     assert_close_bf16(y, ref, f"safetensors checkpoint tiled={tiled}")
+
+
+def test_gguf_linears_into_a_module(tmp_path):
+    """Non-expert weights of a GGUF file run as GGMLLinear after replace_linear_with_ggml
+    (tinyserve/gguf_loader.py:610-665 selection, ggml_linear.py:120-173 replacement)."""
+    from oracle import gguf as og
+    from tests.gguf_writer import write_gguf as _w
+    from tinyserve_amd import gguf_reader as gr
+    from tinyserve_amd.ggml_linear import GGMLLinear, replace_linear_with_ggml
+    from tinyserve_amd.gguf_store import gguf_linear_weights
+
+    rng = np.random.default_rng(13)
+    K, N = 512, 768
+    q = synth.make_gguf(rng, 13, N * K)
+    _w(tmp_path / "l.gguf", [("blk.0.attn_q.weight", (K, N), 13, q)])
+    model = torch.nn.Module()
+    model.q_proj = torch.nn.Linear(K, N, bias=True)
+    with gr.GGUFReader(tmp_path / "l.gguf") as r:
+        lw = gguf_linear_weights(r, {"blk.0.attn_q.weight": "q_proj.weight"})
+    assert replace_linear_with_ggml(model, lw, "cuda") == 1 and isinstance(model.q_proj, GGMLLinear)
+    x = torch.randn(3, K).to(torch.bfloat16)
+    with torch.no_grad():
+        y = model.q_proj(x.cuda()).float().cpu().numpy()
+    ref = x.float().numpy() @ og.dequant_tensor(q, 13, (N, K)).T + model.q_proj.bias.detach().float().cpu().numpy()
+    assert_close_bf16(y, ref, "GGMLLinear from a GGUF file")

@@ -217,3 +217,27 @@ def test_safetensors_store_without_experts(tmp_path):
     save_file({"model.layers.0.self_attn.q_proj.weight": torch.zeros(4, 4)}, str(tmp_path / "model.safetensors"))
     with pytest.raises(ValueError, match="No expert tensors"):
         ExpertStore.from_safetensors(str(tmp_path))
+
+
+def test_gguf_linear_weights_selection(tmp_path):
+    """Quantised 2-D .weight tensors named by the map become replace_linear_with_ggml input
+    ((out, in) from ne = [in, out]); norms, embeddings' F32 and unmapped names are left out."""
+    from tinyserve_amd.gguf_store import gguf_linear_weights
+
+    rng = np.random.default_rng(8)
+    q = synth.make_gguf(rng, 12, 256 * 512)
+    tensors = [("blk.0.attn_q.weight", (256, 512), 12, q),
+               ("blk.0.attn_norm.weight", (256,), 0, np.ones(256, np.float32)),
+               ("blk.0.ffn_gate_inp.weight", (256, 8), 0, np.zeros(256 * 8, np.float32)),
+               ("output.weight", (256, 512), 12, q)]
+    p = tmp_path / "lin.gguf"
+    write_gguf(p, tensors)
+    names = {"blk.0.attn_q.weight": "model.layers.0.self_attn.q_proj.weight",
+             "blk.0.attn_norm.weight": "model.layers.0.input_layernorm.weight",
+             "blk.0.ffn_gate_inp.weight": "model.layers.0.mlp.gate.weight"}
+    with gr.GGUFReader(p) as r:
+        lw = gguf_linear_weights(r, names)
+        assert list(lw) == ["model.layers.0.self_attn.q_proj"]
+        raw, t, shape = lw["model.layers.0.self_attn.q_proj"]
+        assert (t, shape) == (12, (512, 256)) and np.array_equal(raw.numpy(), q)
+        assert list(gguf_linear_weights(r, lambda n: "lm_head.weight" if n == "output.weight" else None)) == ["lm_head"]

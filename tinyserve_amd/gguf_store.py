@@ -163,3 +163,29 @@ class MmapExpertStore:
 
     def close(self) -> None:
         self._reader.close()
+
+
+_QUANT_TYPES = (2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 15)
+
+
+def gguf_linear_weights(reader: GGUFReader, name_map) -> dict[str, tuple[torch.Tensor, int, tuple[int, int]]]:
+    """Native-quantised 2-D ``.weight`` tensors of a GGUF file as ``replace_linear_with_ggml``
+    input: module path -> (raw bytes, ggml type, (out_features, in_features)), the selection
+    the reference's loader makes for non-expert linears (tinyserve/gguf_loader.py:610-623:
+    GGUF ne = [in, out]). ``name_map`` maps GGUF tensor names to model parameter names (a
+    dict, or a callable returning None to skip); only types ``GGMLLinear`` can run are kept
+    (the row kernels serve Q8_0 / Q4_K / Q5_K / Q6_K)."""
+    from .ops import gguf_block_info
+
+    out: dict[str, tuple[torch.Tensor, int, tuple[int, int]]] = {}
+    for info in reader.tensors:
+        hf = name_map(info.name) if callable(name_map) else name_map.get(info.name)
+        if hf is None or not hf.endswith(".weight") or len(info.shape) != 2 or info.ggml_type not in _QUANT_TYPES:
+            continue
+        try:
+            gguf_block_info(info.ggml_type)
+        except Exception:
+            continue  # a quantisation the kernels do not implement: left to the caller
+        out[hf.rsplit(".weight", 1)[0]] = (torch.from_numpy(reader.tensor_view(info).copy()), info.ggml_type,
+                                           (int(info.shape[1]), int(info.shape[0])))
+    return out
