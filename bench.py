@@ -240,7 +240,7 @@ class GgufWorkload:
 
 def cpu_baseline_gguf(wl_id: int, budget_s: float = 12.0) -> dict:
     """The oracle's workload 1 / 2 path (numpy dequant of the whole matrix or expert, then
-    fp32 matvec; SURVEY's CPU restatement of gguf_dequant_torch + F.linear) on this host."""
+    fp32 matvec: the CPU restatement of gguf_dequant_torch + F.linear) on this host."""
     from threadpoolctl import threadpool_info
 
     from oracle import expert as oex
