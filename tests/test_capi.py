@@ -122,3 +122,14 @@ def test_null_and_bad_routing_args(lib):
     assert rc == _lib.ERR_SHAPE and b"E 2000" in lib.tsa_last_error()
     rc = lib.tsa_route_topk(None, 0, 1, 8, 4, 9, None, None, None)
     assert rc == _lib.ERR_INVALID_ARG
+
+
+def test_router_logits_argument_checks(lib):
+    """Shapes, dtypes and pointers are checked before anything is launched; T = 0 is a no-op."""
+    rc = lib.tsa_router_logits(None, 2, 1, 12, None, 2, None, 2, 4, None, 2, None)
+    assert rc == _lib.ERR_SHAPE and b"multiple of 8" in lib.tsa_last_error()
+    rc = lib.tsa_router_logits(None, 7, 1, 16, None, 2, None, 2, 4, None, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"bad dtype" in lib.tsa_last_error()
+    rc = lib.tsa_router_logits(None, 2, 1, 16, None, 2, None, 2, 4, None, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"null pointer" in lib.tsa_last_error()
+    assert lib.tsa_router_logits(None, 2, 0, 16, None, 2, None, 2, 4, None, 2, None) == 0
