@@ -36,6 +36,7 @@ def _ref(experts, xf, idx, w):
     (2880, 2880, 4, 2, 45),    # the GPT-OSS shape: K % 128 = 64, 22.5 weight tiles of gate_up
     (256, 160, 5, 3, 333),     # K = 160 (two pieces, the second a quarter full)
     (1024, 256, 33, 1, 97),    # more experts than the tile table's first rows; k = 1
+    (256, 128, 256, 8, 300),   # over 128 partial row tiles spread over the 8 XCD groups
 ])
 def test_prefill_tiled_vs_oracle(H, I, E, k, T):
     rng, L, experts, pool = _pool(H, I, E, seed=H + I + E + k + T)
@@ -45,6 +46,19 @@ def test_prefill_tiled_vs_oracle(H, I, E, k, T):
                         torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(), bf16_dev(x_bits))
     assert y.dtype == torch.bfloat16 and y.shape == (T, H)
     assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w), f"prefill H={H} I={I} E={E} k={k} T={T}")
+
+
+def test_prefill_only_full_row_tiles():
+    """Every expert gets exactly 128 or 256 rows: the tile table holds full entries only."""
+    H, I, E, k, T = 512, 256, 5, 2, 384
+    rng, L, experts, pool = _pool(H, I, E, seed=31)
+    idx = np.array([[0, 1]] * 128 + [[0, 2]] * 128 + [[3, 4]] * 128)
+    assert np.bincount(idx.reshape(-1), minlength=E).tolist() == [256, 128, 128, 128, 128]
+    w = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    y = ops.moe_prefill(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                        torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(), bf16_dev(x_bits))
+    assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w), "prefill, full row tiles only")
 
 
 def test_prefill_missing_experts_and_dropped_assignments():

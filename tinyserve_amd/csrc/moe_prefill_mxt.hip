@@ -19,9 +19,13 @@
 // in). Activations are the B operand. Both reach LDS by direct buffer-to-LDS loads issued
 // ahead of use (weights, which mostly come from HBM or the MALL, 4 pieces ahead in a 5-deep
 // ring; activations, which mostly hit L2, 1 piece ahead), with one wait + barrier per piece.
-// Workgroups are persistent, one per CU; the tile list is split into 8 contiguous ranges,
-// one per XCD (workgroup b runs on XCD b % 8), in row-tile-major order, so the workgroups
-// running together on an XCD share the row tile's activations in its L2.
+// Workgroups are persistent, one per CU. XCD x (workgroup b runs on XCD b % 8) owns a
+// group of row tiles, with all their weight tiles, in row-tile-major order, so the
+// workgroups running together on an XCD share a row tile's activations in its L2. The
+// table kernel forms the 8 groups to balance an estimated cost (a tile costs 96 + rows, in
+// rows: partial row tiles are cheaper, not free), and each group ends on its cheapest row
+// tiles. An XCD's workgroups take its tiles one at a time from a per-XCD counter (the next
+// one is requested when a tile starts), so they finish together whatever the tiles cost.
 //
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases,
@@ -51,6 +55,9 @@ constexpr int PF_SBYTES = (PF_BN / 16) * 256;     // one scale word per lane of 
 constexpr int PF_WOFF = PF_XST * PF_XBYTES;
 constexpr int PF_SOFF = PF_WOFF + PF_WST * PF_WBYTES;
 constexpr int PF_LDS = PF_SOFF + 2 * PF_SBYTES;   // 152 KB
+constexpr int PF_CTR_STRIDE = 32;                 // ints between per-XCD tile counters (one 128-byte line each)
+constexpr int PF_CTR_INTS = 2 * 8 * PF_CTR_STRIDE;  // gate_up's 8 counters, then down's
+constexpr int PF_COST0 = 96;  // a tile's estimated cost is PF_COST0 + rows (measured: 16 rows ~0.5 x 128 rows)
 
 struct PfEntry {
     int slot, row0, rows, expert;
@@ -59,11 +66,12 @@ struct PfEntry {
 struct PfGemm {
     tsa_expert_layout L;
     const uint8_t* pool;
-    const int* n_entries;     // device: valid table entries
+    const int* n_entries;     // device: [0] all table entries, [1 + x] .. [2 + x] XCD x's group
     const PfEntry* table;
     const uint16_t* src;      // gate_up: x [T, K] rows gathered through perm; down: h [n, K] sorted
     int64_t src_rows;         // rows of src (bounds of its buffer resource)
     const int32_t* perm;      // sorted position -> assignment id (token * k + j)
+    int* ctr;                 // 8 per-XCD tile counters (stride PF_CTR_STRIDE), zero at launch
     int k;
     uint16_t* out;            // gate_up: h [n, N / 2]; down: yk [T k, N]
     int N, K, NT, MP;         // weight rows, reduction length, tiles along N, pieces along K
@@ -206,15 +214,21 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
     const int wn = wave & 3, wt = wave >> 2;
     const int g = lane >> 5, rr = lane & 31;
     const int N = p.N, K = p.K, MP = p.MP;
-    const int total = uniform(*p.n_entries) * p.NT;
     const int xcd = blockIdx.x & 7, R = gridDim.x >> 3;
-    const int lo = (int)((int64_t)total * xcd / 8), hi = (int)((int64_t)total * (xcd + 1) / 8);
+    const int m0 = uniform(p.n_entries[1 + xcd]);
+    const int total = (uniform(p.n_entries[2 + xcd]) - m0) * p.NT;  // this XCD's tiles
+    int* const ctr = p.ctr + PF_CTR_STRIDE * xcd;
+    __shared__ int s_next;
     const int W = (int)(p.stile_bytes >> 8);  // scale words per lane
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const v4i xr = buf_desc(p.src, (uint32_t)(p.src_rows * K * 2));
 
-    for (int t = lo + (int)(blockIdx.x >> 3); t < hi; t += R) {
-        const int m = t / p.NT, nt = t % p.NT;
+    // The first tile of workgroup b is b / 8; later ones come from the counter (offset by R,
+    // so the first R are never handed out twice).
+    for (int tl = (int)(blockIdx.x >> 3); tl < total;) {
+        const int m = m0 + tl / p.NT, nt = tl % p.NT;
+        int grabbed = 0;
+        if (tid == 0) grabbed = R + __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const PfEntry e = p.table[m];
         const int slot = uniform(e.slot), row0 = uniform(e.row0), rows = uniform(e.rows);
         const uint8_t* base = p.pool + (int64_t)slot * p.L.slot_bytes;
@@ -289,7 +303,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         if (!active) pf_kloop<0>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
         else if (nsub == 2) pf_kloop<2>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
         else pf_kloop<1>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        if (tid == 0) s_next = grabbed;
         __syncthreads();  // every wave is done with the last stages before the next tile refills them
+        tl = uniform(s_next);  // rewritten only after the next tile's K loop, which has a barrier per piece
 
         if (!active) continue;
         // Epilogue: acc[rb][b][4u + r] is row 32 rb + 8u + 4g + r of the wave's 64 (r = 0..3),
@@ -310,14 +326,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
                     if (b >= nsub || tk >= rows) continue;
                     const v4f v = v4f{acc[rb][b][4 * u], acc[rb][b][4 * u + 1], acc[rb][b][4 * u + 2], acc[rb][b][4 * u + 3]} + bias;
                     if (GATE_UP) {
-                        const float h0 = swiglu_oai(p.L, v[0], v[1]), h1 = swiglu_oai(p.L, v[2], v[3]);
-                        const uint32_t packed = (uint32_t)f32_to_bf16_bits(h0) | ((uint32_t)f32_to_bf16_bits(h1) << 16);
+                        const uint32_t packed = pack_bf16x2(swiglu_oai_fast(p.L, v[0], v[1]), swiglu_oai_fast(p.L, v[2], v[3]));
                         *reinterpret_cast<uint32_t*>(p.out + (int64_t)(row0 + tk) * (N / 2) + r0 / 2) = packed;
                     } else {
                         const int64_t asg = p.perm[row0 + tk];
-                        const uint32_t w0 = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-                        const uint32_t w1 = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
-                        *reinterpret_cast<uint2*>(p.out + asg * N + r0) = make_uint2(w0, w1);
+                        *reinterpret_cast<uint2*>(p.out + asg * N + r0) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     }
                 }
             }
@@ -326,34 +339,99 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
 }
 
 // Tile table: expert e with a resident slot and c_e sorted rows gets ceil(c_e / 128)
-// entries (slot, first sorted row, rows, e), experts in order. E <= 1024.
+// entries (slot, first sorted row, rows, e), in 8 contiguous groups, one per XCD of the
+// GEMM launches: n_entries[1 + x] .. n_entries[2 + x] for XCD x, n_entries[0] = all. The
+// full 128-row entries are dealt round-robin (experts in order); then the partial ones,
+// largest first, each go to the group with the least estimated cost so far (PF_COST0 +
+// rows per entry). Within a group the full entries come first, then the partial ones
+// largest first. Equal-row partial entries are ranked in any order: the results do not
+// depend on the order. Also zeroes the GEMMs' tile counters. E <= 1024.
 __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restrict__ counts,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ expert_slot, int E,
                                                         int64_t n_slots, int* __restrict__ n_entries,
-                                                        PfEntry* __restrict__ table) {
+                                                        PfEntry* __restrict__ table, int* __restrict__ ctr) {
     __shared__ int pre[1024];
+    __shared__ int hist[PF_BM];    // partial entries with r rows
+    __shared__ int pos[PF_BM];     // rank (offset by the full entries) of the next partial entry with r rows
+    __shared__ int prow[1024];     // partial entries by rank: rows
+    __shared__ int pgrp[1024], pidx[1024];  // ... group and place among the group's partial entries
+    __shared__ int gstart[8], gfull[8];
     const int e = threadIdx.x;
-    int slot = -1, c = 0, nt = 0;
+    if (e < PF_CTR_INTS) ctr[e] = 0;
+    if (e < PF_BM) hist[e] = 0;
+    int slot = -1, c = 0, nt = 0, r = 0;
     if (e < E) {
         slot = expert_slot[e];
         c = counts[e];
-        nt = (slot >= 0 && slot < n_slots) ? (c + PF_BM - 1) / PF_BM : 0;
+        if (slot >= 0 && slot < n_slots) {
+            nt = c / PF_BM;
+            r = c % PF_BM;
+        }
     }
     pre[e] = nt;
     __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
+    if (r > 0) atomicAdd(&hist[r], 1);
+    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan of the full entries
         const int v = e >= d ? pre[e - d] : 0;
         __syncthreads();
         pre[e] += v;
         __syncthreads();
     }
-    const int start = pre[e] - nt;
-    for (int j = 0; j < nt; ++j) {
-        const int r = c - PF_BM * j;
-        table[start + j] = PfEntry{slot, offsets[e] + PF_BM * j, r < PF_BM ? r : PF_BM, e};
+    const int F = pre[1023];
+    if (e < PF_BM) {  // partial entries with more rows than e rank first; pos[0] = all entries
+        int s = F;
+        for (int b = e + 1; b < PF_BM; ++b) s += hist[b];
+        pos[e] = s;
     }
-    if (e == 1023) *n_entries = pre[1023];
+    __syncthreads();
+    const int P = pos[0] - F;
+    __syncthreads();  // pos[0] is read before the partial entries take ranks (r > 0 never touches it)
+    int q = -1;
+    if (r > 0) {
+        q = atomicAdd(&pos[r], 1) - F;
+        prow[q] = r;
+    }
+    __syncthreads();
+    if (e == 0) {  // the groups: sequential, P <= E steps of an argmin over 8 costs
+        int cost[8], np[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            gfull[x] = F / 8 + (x < F % 8 ? 1 : 0);
+            cost[x] = gfull[x] * (PF_COST0 + PF_BM);
+            np[x] = 0;
+        }
+        for (int i = 0; i < P; ++i) {
+            int b = 0, cb = cost[0];
+#pragma unroll
+            for (int x = 1; x < 8; ++x)
+                if (cost[x] < cb) { b = x; cb = cost[x]; }
+            int n = 0;
+#pragma unroll
+            for (int x = 0; x < 8; ++x)
+                if (x == b) { n = np[x]; np[x] = n + 1; cost[x] = cb + PF_COST0 + prow[i]; }
+            pgrp[i] = b;
+            pidx[i] = n;
+        }
+        int s = 0;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            gstart[x] = s;
+            n_entries[1 + x] = s;
+            s += gfull[x] + np[x];
+        }
+        n_entries[9] = s;
+        n_entries[0] = s;
+    }
+    __syncthreads();
+    for (int j = 0; j < nt; ++j) {
+        const int f = pre[e] - nt + j;  // full entry f goes to group f % 8, place f / 8
+        table[gstart[f & 7] + (f >> 3)] = PfEntry{slot, offsets[e] + PF_BM * j, PF_BM, e};
+    }
+    if (q >= 0) {
+        const int x = pgrp[q];
+        table[gstart[x] + gfull[x] + pidx[q]] = PfEntry{slot, offsets[e] + PF_BM * nt, r, e};
+    }
 }
 
 // y[t] = sum_j w[t, j] yk[t k + j] over the live assignments, j in order; 8 columns per thread.
@@ -401,7 +479,7 @@ bool pf_mxt_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k)
 static int64_t al256(int64_t v) { return (v + 255) / 256 * 256; }
 
 struct PfWs {
-    int64_t counts, offsets, perm, nent, table, h, yk, total;
+    int64_t counts, offsets, perm, nent, ctr, table, h, yk, total;
 };
 
 static PfWs pf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
@@ -412,6 +490,7 @@ static PfWs pf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E
     w.offsets = o; o += al256(4 * (E + 1));
     w.perm = o; o += al256(4 * n);
     w.nent = o; o += 256;
+    w.ctr = o; o += al256(4 * PF_CTR_INTS);
     w.table = o; o += al256((int64_t)sizeof(PfEntry) * (n / PF_BM + E + 1));
     w.h = o; o += al256(2 * n * L.inter);
     w.yk = o; o += al256(2 * n * L.hidden);
@@ -434,6 +513,7 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     int32_t* offsets = reinterpret_cast<int32_t*>(ws + w.offsets);
     int32_t* perm = reinterpret_cast<int32_t*>(ws + w.perm);
     int* nent = reinterpret_cast<int*>(ws + w.nent);
+    int* ctr = reinterpret_cast<int*>(ws + w.ctr);
     PfEntry* table = reinterpret_cast<PfEntry*>(ws + w.table);
     uint16_t* h = reinterpret_cast<uint16_t*>(ws + w.h);
     uint16_t* yk = reinterpret_cast<uint16_t*>(ws + w.yk);
@@ -442,7 +522,7 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     int rc = launch_group_kernel(idx, T * k, (int)E, counts, offsets, perm, stream);
     if (rc) return rc;
     hipLaunchKernelGGL(pf_table_kernel, dim3(1), dim3(1024), 0, stream, counts, offsets, expert_slot, (int)E, n_slots,
-                       nent, table);
+                       nent, table, ctr);
     TSA_LAUNCH_CHECK();
 
     static std::once_flag lds_once;
@@ -462,6 +542,7 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     g.n_entries = nent;
     g.table = table;
     g.perm = perm;
+    g.ctr = ctr;
     g.k = k;
     // gate_up: [2I, H] -> h
     g.src = x;
@@ -481,6 +562,7 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     // down: [H, I] -> yk
     g.src = h;
     g.src_rows = T * k;
+    g.ctr = ctr + 8 * PF_CTR_STRIDE;
     g.out = yk;
     g.N = H;
     g.K = I;
