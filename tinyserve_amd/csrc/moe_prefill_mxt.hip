@@ -341,10 +341,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
 // Tile table: expert e with a resident slot and c_e sorted rows gets ceil(c_e / 128)
 // entries (slot, first sorted row, rows, e), in 8 contiguous groups, one per XCD of the
 // GEMM launches: n_entries[1 + x] .. n_entries[2 + x] for XCD x, n_entries[0] = all. The
-// full 128-row entries are dealt round-robin (experts in order); then the partial ones,
-// largest first, each go to the group with the least estimated cost so far (PF_COST0 +
-// rows per entry). Within a group the full entries come first, then the partial ones
-// largest first. Equal-row partial entries are ranked in any order: the results do not
+// full 128-row entries (experts in order) are cut into 8 contiguous runs, so an expert's
+// row tiles stay on few XCDs and share its weights in L2; then the partial ones, largest
+// first, each go to the group with the least estimated cost so far (PF_COST0 + rows per
+// entry). Within a group the full entries come first, then the partial ones largest first. Equal-row partial entries are ranked in any order: the results do not
 // depend on the order. Also zeroes the GEMMs' tile counters. E <= 1024.
 __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restrict__ counts,
                                                         const int32_t* __restrict__ offsets,
@@ -379,11 +379,16 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
         __syncthreads();
     }
     const int F = pre[1023];
-    if (e < PF_BM) {  // partial entries with more rows than e rank first; pos[0] = all entries
-        int s = F;
-        for (int b = e + 1; b < PF_BM; ++b) s += hist[b];
-        pos[e] = s;
+    // pos[b] = F + partial entries with more than b rows (an exclusive suffix scan of hist)
+    if (e < PF_BM) pos[e] = e + 1 < PF_BM ? hist[e + 1] : 0;
+    __syncthreads();
+    for (int d = 1; d < PF_BM; d <<= 1) {
+        const int v = e < PF_BM && e + d < PF_BM ? pos[e + d] : 0;
+        __syncthreads();
+        if (e < PF_BM) pos[e] += v;
+        __syncthreads();
     }
+    if (e < PF_BM) pos[e] += F;
     __syncthreads();
     const int P = pos[0] - F;
     __syncthreads();  // pos[0] is read before the partial entries take ranks (r > 0 never touches it)
@@ -393,40 +398,46 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
         prow[q] = r;
     }
     __syncthreads();
-    if (e == 0) {  // the groups: sequential, P <= E steps of an argmin over 8 costs
-        int cost[8], np[8];
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            gfull[x] = F / 8 + (x < F % 8 ? 1 : 0);
-            cost[x] = gfull[x] * (PF_COST0 + PF_BM);
-            np[x] = 0;
-        }
+    if (e < 64) {  // the groups, by wave 0: lane x < 8 holds group x; P <= E steps of an argmin
+        const int x = e;
+        const int nf = x < 8 ? F * (x + 1) / 8 - F * x / 8 : 0;
+        int cost = x < 8 ? nf * (PF_COST0 + PF_BM) : 0x7FFFFFFF, np = 0;
+        int rn = P > 0 ? prow[0] : 0;
         for (int i = 0; i < P; ++i) {
-            int b = 0, cb = cost[0];
-#pragma unroll
-            for (int x = 1; x < 8; ++x)
-                if (cost[x] < cb) { b = x; cb = cost[x]; }
-            int n = 0;
-#pragma unroll
-            for (int x = 0; x < 8; ++x)
-                if (x == b) { n = np[x]; np[x] = n + 1; cost[x] = cb + PF_COST0 + prow[i]; }
-            pgrp[i] = b;
-            pidx[i] = n;
+            const int r_i = rn;
+            if (i + 1 < P) rn = prow[i + 1];  // read ahead, off the cost dependency
+            int key = x < 8 ? (cost << 3) | x : 0x7FFFFFFF;  // the least cost, ties to the lower group
+            key = min(key, dpp_i<0xB1, 0xF, 0xF>(key, key));   // quad_perm [1,0,3,2]
+            key = min(key, dpp_i<0x4E, 0xF, 0xF>(key, key));   // quad_perm [2,3,0,1]
+            key = min(key, dpp_i<0x141, 0xF, 0xF>(key, key));  // row_half_mirror: the other quad of the 8
+            if (x == (key & 7)) {
+                pgrp[i] = x;
+                pidx[i] = np++;
+                cost += PF_COST0 + r_i;
+            }
         }
-        int s = 0;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-            gstart[x] = s;
-            n_entries[1 + x] = s;
-            s += gfull[x] + np[x];
+        int s = x < 8 ? nf + np : 0;  // exclusive scan over the 8 groups
+        for (int d = 1; d < 8; d <<= 1) {
+            const int v = __shfl_up(s, d);
+            if (x >= d) s += v;
         }
-        n_entries[9] = s;
-        n_entries[0] = s;
+        if (x < 8) {
+            gfull[x] = nf;
+            gstart[x] = s - nf - np;
+            n_entries[1 + x] = s - nf - np;
+            if (x == 7) {
+                n_entries[9] = s;
+                n_entries[0] = s;
+            }
+        }
     }
     __syncthreads();
     for (int j = 0; j < nt; ++j) {
-        const int f = pre[e] - nt + j;  // full entry f goes to group f % 8, place f / 8
-        table[gstart[f & 7] + (f >> 3)] = PfEntry{slot, offsets[e] + PF_BM * j, PF_BM, e};
+        const int f = pre[e] - nt + j;  // full entry f: run x with F x / 8 <= f < F (x + 1) / 8
+        int x = 0;
+#pragma unroll
+        for (int y = 1; y < 8; ++y) x += F * y / 8 <= f ? 1 : 0;
+        table[gstart[x] + f - F * x / 8] = PfEntry{slot, offsets[e] + PF_BM * j, PF_BM, e};
     }
     if (q >= 0) {
         const int x = pgrp[q];
