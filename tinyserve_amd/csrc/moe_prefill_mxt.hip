@@ -57,6 +57,9 @@ constexpr int PF_SOFF = PF_WOFF + PF_WST * PF_WBYTES;
 constexpr int PF_LDS = PF_SOFF + 2 * PF_SBYTES;   // 152 KB
 constexpr int PF_CTR_STRIDE = 32;                 // ints between per-XCD tile counters (one 128-byte line each)
 constexpr int PF_CTR_INTS = 2 * 8 * PF_CTR_STRIDE;  // gate_up's 8 counters, then down's
+constexpr int PF_HS_GU = 272;   // LDS row stride (bytes) of the staged gate_up outputs: 128 h + 16 B
+constexpr int PF_HS_DN = 528;   // ... of the staged down outputs: 256 values + 16 B
+static_assert(PF_BM * PF_HS_DN <= PF_LDS, "the staged outputs fit in the stages");
 constexpr int PF_COST0 = 96;  // a tile's estimated cost is PF_COST0 + rows (measured: 16 rows ~0.5 x 128 rows)
 
 struct PfEntry {
@@ -291,6 +294,21 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         nsub = nsub < 0 ? 0 : (nsub > 2 ? 2 : nsub);
         const bool active = rows_live && nsub > 0;
 
+        // The epilogue's bias, loaded now so its latency is hidden by the K loop (rows past N
+        // read zero: the buffer range check).
+        u32x4 braw[2][4];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) braw[rb][u] = u32x4{0u, 0u, 0u, 0u};
+        if (active && p.b_off >= 0) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    braw[rb][u] = bias_raw(base + p.b_off, p.L.bias_dtype, N, 16 * rt0 + 32 * rb + 8 * u + 4 * g);
+        }
+
         v16f acc[2][2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -307,34 +325,53 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         __syncthreads();  // every wave is done with the last stages before the next tile refills them
         tl = uniform(s_next);  // rewritten only after the next tile's K loop, which has a barrier per piece
 
-        if (!active) continue;
-        // Epilogue: acc[rb][b][4u + r] is row 32 rb + 8u + 4g + r of the wave's 64 (r = 0..3),
-        // token column 64 wt + 32 b + (lane % 32).
+        // Epilogue, 1: the outputs (bias added; SwiGLU for gate_up) as bf16 into LDS, one row
+        // per token (the stages are free: every wave is past the K loop's last LDS read).
+        // acc[rb][b][4u + r] is row 32 rb + 8u + 4g + r of the wave's 64 (r = 0..3), token
+        // column 64 wt + 32 b + (lane % 32).
+        constexpr int HS = GATE_UP ? PF_HS_GU : PF_HS_DN;
+        if (active) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int rbase = 16 * rt0 + 32 * rb;
-            if (rbase >= N) break;
+            for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int r0 = rbase + 8 * u + 4 * g;
-                if (r0 >= N) continue;  // N % 32 == 16: the block's second row tile is past N
-                v4f bias = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                if (p.b_off >= 0) bias = bias_value(bias_raw(base + p.b_off, p.L.bias_dtype, N, r0), p.L.bias_dtype);
+                for (int u = 0; u < 4; ++u) {
+                    const int c = 64 * wn + 32 * rb + 8 * u + 4 * g;  // weight row within the workgroup tile
+                    if (16 * rtw + c >= N) continue;  // N % 32 == 16: the block's second row tile is past N
+                    const v4f bias = p.b_off >= 0 ? bias_value(braw[rb][u], p.L.bias_dtype) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int tk = 64 * wt + 32 * b + rr;
-                    if (b >= nsub || tk >= rows) continue;
-                    const v4f v = v4f{acc[rb][b][4 * u], acc[rb][b][4 * u + 1], acc[rb][b][4 * u + 2], acc[rb][b][4 * u + 3]} + bias;
-                    if (GATE_UP) {
-                        const uint32_t packed = pack_bf16x2(swiglu_oai_fast(p.L, v[0], v[1]), swiglu_oai_fast(p.L, v[2], v[3]));
-                        *reinterpret_cast<uint32_t*>(p.out + (int64_t)(row0 + tk) * (N / 2) + r0 / 2) = packed;
-                    } else {
-                        const int64_t asg = p.perm[row0 + tk];
-                        *reinterpret_cast<uint2*>(p.out + asg * N + r0) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    for (int b = 0; b < 2; ++b) {
+                        const int tk = 64 * wt + 32 * b + rr;
+                        if (b >= nsub || tk >= rows) continue;
+                        const v4f v = v4f{acc[rb][b][4 * u], acc[rb][b][4 * u + 1], acc[rb][b][4 * u + 2], acc[rb][b][4 * u + 3]} + bias;
+                        if (GATE_UP)
+                            *reinterpret_cast<uint32_t*>(smem + tk * HS + c) =
+                                pack_bf16x2(swiglu_oai_fast(p.L, v[0], v[1]), swiglu_oai_fast(p.L, v[2], v[3]));
+                        else
+                            *reinterpret_cast<uint2*>(smem + tk * HS + 2 * c) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     }
                 }
             }
         }
+        __syncthreads();
+        // 2: whole rows out, 16 bytes (8 values) per lane, consecutive lanes along a row:
+        // gate_up h[row0 + tk, 128 nt ..] (256 B a row), down yk[perm[row0 + tk], 256 nt ..] (512 B).
+        {
+            constexpr int CPR = GATE_UP ? 16 : 32;  // 16-byte chunks per row
+            const int ncol = GATE_UP ? N / 2 - 128 * nt : N - 256 * nt;  // live values in the row (multiple of 8)
+#pragma unroll
+            for (int j = 0; j < PF_BM * CPR / PF_THREADS; ++j) {
+                const int i = tid + PF_THREADS * j, tk = i / CPR, ch = i % CPR;
+                if (tk >= rows || 8 * ch >= ncol) continue;
+                const uint4 v = *reinterpret_cast<const uint4*>(smem + tk * HS + 16 * ch);
+                if (GATE_UP) {
+                    *reinterpret_cast<uint4*>(p.out + (int64_t)(row0 + tk) * (N / 2) + 128 * nt + 8 * ch) = v;
+                } else {
+                    const int64_t asg = p.perm[row0 + tk];
+                    *reinterpret_cast<uint4*>(p.out + asg * N + 256 * nt + 8 * ch) = v;
+                }
+            }
+        }
+        __syncthreads();  // the staged rows are read before the next tile's loads refill the stages
     }
 }
 
