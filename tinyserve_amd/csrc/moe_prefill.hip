@@ -15,6 +15,7 @@ namespace {
 constexpr int GROUP_THREADS = 512;
 constexpr int GROUP_WAVES = GROUP_THREADS / 64;
 constexpr int MAX_GROUP_E = 1024;
+constexpr int GROUP_AHEAD = 8;  // id batches loaded ahead per wave
 
 // Lanes of the wave holding the same expert as this lane (e >= 0; lanes with e < 0 are in
 // no group), found with one ballot per bit of the expert id instead of a loop over the
@@ -51,12 +52,22 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __r
     __syncthreads();
     const int64_t chunk = ((n + GROUP_WAVES - 1) / GROUP_WAVES + 63) / 64 * 64;
     const int64_t a0 = wave * chunk, a1 = a0 + chunk < n ? a0 + chunk : n;
-    for (int64_t b = a0; b < a1; b += 64) {
-        const int64_t a = b + lane;
-        int e = a < a1 ? idx[a] : -1;
-        if (e >= E) e = -1;
-        const unsigned long long m = peers(e, nbits);
-        if (e >= 0 && !(m & below)) wcnt[wave][e] += __popcll(m);
+    // Batches of 64 assignments in order; the ids of GROUP_AHEAD batches are loaded together
+    // so the wave waits for one memory round trip per GROUP_AHEAD batches, not per batch.
+    for (int64_t b0 = a0; b0 < a1; b0 += 64 * GROUP_AHEAD) {
+        int ev[GROUP_AHEAD];
+#pragma unroll
+        for (int j = 0; j < GROUP_AHEAD; ++j) {
+            const int64_t a = b0 + 64 * j + lane;
+            ev[j] = a < a1 ? idx[a] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < GROUP_AHEAD; ++j) {
+            if (b0 + 64 * j >= a1) break;
+            const int e = ev[j] < E ? ev[j] : -1;
+            const unsigned long long m = peers(e, nbits);
+            if (e >= 0 && !(m & below)) wcnt[wave][e] += __popcll(m);
+        }
     }
     __syncthreads();
     for (int e = tid; e < E; e += GROUP_THREADS) {
@@ -93,14 +104,23 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __r
         if (lane == 63) offsets[E] = inc;
     }
     __syncthreads();
-    for (int64_t b = a0; b < a1; b += 64) {
-        const int64_t a = b + lane;
-        int e = a < a1 ? idx[a] : -1;
-        if (e >= E) e = -1;
-        const unsigned long long m = peers(e, nbits);
-        if (e >= 0) {
-            perm[eoff[e] + wcnt[wave][e] + __popcll(m & below)] = (int32_t)a;
-            if (!(m & below)) wcnt[wave][e] += __popcll(m);  // after every lane of the group read it
+    for (int64_t b0 = a0; b0 < a1; b0 += 64 * GROUP_AHEAD) {
+        int ev[GROUP_AHEAD];
+#pragma unroll
+        for (int j = 0; j < GROUP_AHEAD; ++j) {
+            const int64_t a = b0 + 64 * j + lane;
+            ev[j] = a < a1 ? idx[a] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < GROUP_AHEAD; ++j) {
+            if (b0 + 64 * j >= a1) break;
+            const int64_t a = b0 + 64 * j + lane;
+            const int e = ev[j] < E ? ev[j] : -1;
+            const unsigned long long m = peers(e, nbits);
+            if (e >= 0) {
+                perm[eoff[e] + wcnt[wave][e] + __popcll(m & below)] = (int32_t)a;
+                if (!(m & below)) wcnt[wave][e] += __popcll(m);  // after every lane of the group read it
+            }
         }
     }
 }
