@@ -495,18 +495,45 @@ __global__ void __launch_bounds__(256) pf_combine_kernel(const uint16_t* __restr
     const int64_t t = g / cpr;
     const int c = (int)(g % cpr);
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < k; ++j) {
-        const int e = idx[t * k + j];
-        if (e < 0 || e >= E) continue;
-        const int s = expert_slot[e];
-        if (s < 0 || s >= n_slots) continue;
-        const float wj = w[t * k + j];
-        const u32x4 v = *reinterpret_cast<const u32x4*>(yk + (t * k + j) * H + 8 * c);
+    // Four assignments at a time: their ids, weights and output rows are loaded together
+    // (a dropped assignment's row is read but not used), then the slots, then the sums in
+    // j order.
+    constexpr int JB = 4;
+    for (int j0 = 0; j0 < k; j0 += JB) {
+        int e[JB];
+        float wj[JB];
+        u32x4 v[JB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[2 * i] += wj * bf16_bits_to_f32(v[i] & 0xFFFFu);
-            acc[2 * i + 1] += wj * bf16_bits_to_f32(v[i] >> 16);
+        for (int jj = 0; jj < JB; ++jj) {
+            const int j = j0 + jj;
+            e[jj] = j < k ? idx[t * k + j] : -1;
+            wj[jj] = j < k ? w[t * k + j] : 0.0f;
+            v[jj] = j < k ? *reinterpret_cast<const u32x4*>(yk + (t * k + j) * H + 8 * c) : u32x4{0u, 0u, 0u, 0u};
         }
+        bool live[JB];
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+            live[jj] = e[jj] >= 0 && e[jj] < E;
+            if (live[jj]) {
+                const int s = expert_slot[e[jj]];
+                live[jj] = s >= 0 && s < n_slots;
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+            if (!live[jj]) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[2 * i] += wj[jj] * bf16_bits_to_f32(v[jj][i] & 0xFFFFu);
+                acc[2 * i + 1] += wj[jj] * bf16_bits_to_f32(v[jj][i] >> 16);
+            }
+        }
+    }
+    if (y_dtype == TSA_BF16) {  // one 16-byte store (H % 8 == 0 keeps it aligned)
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + t * H + 8 * c) =
+            make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
+                       pack_bf16x2(acc[6], acc[7]));
+        return;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) store_out(y, y_dtype, t * H + 8 * c + i, acc[i]);
