@@ -9,18 +9,6 @@ import torch
 COS_MIN = 0.9999
 REL_MAX = 1e-2
 
-# MoE decode workspace: a 41216-byte header (launch-wide words, one completion counter per
-# (token, expert) pair every 256 bytes, then 96 completion flags per pair), then h [T, k, I].
-WS_HDR = 41216
-
-
-def ws_header_clean(ws: torch.Tensor) -> None:
-    """Every counter and the error flag of a decode workspace header are back to zero."""
-    hdr = ws[:WS_HDR].view(torch.int32).cpu().numpy()
-    bad = np.nonzero(hdr)[0]
-    assert bad.size == 0, f"workspace header not clean: words {bad[:8].tolist()} = {hdr[bad[:8]].tolist()}"
-
-
 def to_f32(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy()
 
@@ -62,3 +50,22 @@ def dev_u8(arr: np.ndarray, offset: int = 0, device: str = "cuda") -> torch.Tens
 
 def bf16_dev(bits: np.ndarray, device: str = "cuda") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).copy()).view(torch.bfloat16).to(device)
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    """OCP fp8 e4m3 (bias 7, no infinities, 0x7F / 0xFF NaN) -> float32, exact."""
+    c = np.asarray(codes, dtype=np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e, m = (c >> 3) & 15, c & 7
+    v = sign * np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10))
+    v[(c & 0x7F) == 0x7F] = np.nan
+    return v.astype(np.float32)
+
+
+def tiled_h(ws: torch.Tensor, pairs: int, inter: int, swiglu_limit: float = 7.0) -> np.ndarray:
+    """The intermediate h [pairs, inter] the tiled decode wrote at the start of its workspace:
+    per pair two e4m3 terms (hi then lo) of inter values, scaled by 2^(7 - e) with
+    (limit + 1) * limit < 2^e."""
+    raw = ws[: pairs * 2 * inter].cpu().numpy().view(np.uint8).reshape(pairs, 2, inter)
+    e = int(np.frexp(np.float32((swiglu_limit + 1.0) * swiglu_limit))[1])
+    return (e4m3_to_f32(raw[:, 0]) + e4m3_to_f32(raw[:, 1])) * np.float32(2.0 ** (e - 7))

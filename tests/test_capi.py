@@ -83,7 +83,7 @@ def test_decode_layout_validation(lib):
     lay = synth.mxfp4_layout(2880, 2880)
     L = mxfp4_expert_layout(lay)
     rc, n = _ws(lib, L)
-    assert rc == 0 and n >= 41216 + 4 * 2880 * 4  # counter header + h
+    assert rc == 0 and n >= 4 * 2880 * 4  # float h of 4 pairs
     L.slot_bytes = lay.total_bytes - 2  # the down bias no longer fits
     assert _ws(lib, L)[0] == _lib.ERR_WEIGHT_TOO_SMALL
     L = mxfp4_expert_layout(lay)

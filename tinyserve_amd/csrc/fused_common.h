@@ -1,5 +1,5 @@
-// Device helpers shared by the fused single-launch MoE decode kernels: DPP wave
-// reductions, in-kernel top-k routing, workspace counters and the GPT-OSS activation.
+// Device helpers shared by the MoE decode kernels: DPP wave reductions, in-kernel top-k
+// routing and the GPT-OSS activation.
 #pragma once
 
 #include "tsa_common.h"
@@ -10,8 +10,6 @@ namespace {
 
 constexpr int FUSED_MAXT = 4;   // tokens per fused launch
 constexpr int FUSED_MAXK = 16;  // experts per token
-constexpr int SPIN_LIMIT = 1 << 23;  // ~2 s of s_sleep(4); never reached in a healthy run
-static_assert(FUSED_MAXT * FUSED_MAXK <= WS_MAX_PAIRS, "one header counter per (token, expert) pair");
 
 // ---------------------------------------------------------------- DPP wave reductions
 template <int CTRL, int ROW_MASK, int BANK_MASK>
@@ -108,15 +106,6 @@ __device__ __forceinline__ int wave_min_u(int v) {
 // a buffer resource built from such a value is wrapped in a waterfall loop per load.
 // Every lane reads the same entry, so lane 0's value is the wave's.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-__device__ __forceinline__ unsigned ld_relaxed(unsigned* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Completion counter of pair i = t*k + j (header layout in tsa_common.h).
-__device__ __forceinline__ unsigned* pair_ctr(unsigned* bar, int i) {
-    return bar + (WS_CTR_OFF + i * WS_CTR_STRIDE) / 4;
-}
 
 // v[j] = element base + min(lane + 64 j, n - 1) of a float/bf16/fp16 array: four
 // unconditional loads issued together (a per-element dtype branch would serialise them).

@@ -189,6 +189,7 @@ hipError_t launch_gguf_b(const Launch& s, const tsa_expert_layout& L, const uint
 }  // namespace
 
 int64_t mx_fused_ws_bytes(const tsa_expert_layout& L, int64_t T, int k);
+int64_t mxt_ws_bytes(const tsa_expert_layout& L, int64_t T, int k);
 const char* gq_unsupported(const tsa_expert_layout& L);
 int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
               const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
@@ -207,21 +208,21 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
                     int y_dtype, uint8_t* ws, int64_t ws_bytes, hipStream_t st);
 int64_t mx_tile_scale_bytes(int64_t K);
 const char* mxt_unsupported(const tsa_expert_layout& L);
-int mxt_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
-                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
-                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype,
-                     uint8_t* ws, int64_t ws_bytes, hipStream_t st);
+int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
+               const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E,
+               int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype, uint8_t* ws,
+               int64_t ws_bytes, hipStream_t st);
 
-// Workspace: the WS_HDR-byte counter header (zero before first use; the fused kernel
-// leaves it zero), then float h [T, k, I] (shared by both paths), then int32 slots / ids
-// and float weights [T, k] for routed calls.
+// Workspace: the intermediate h of every path (float [T, k, I] at most), then int32 slots /
+// ids and float weights [T, k] for routed calls. No kernel keeps state in it between
+// calls, so it needs no initialisation.
 static int64_t h_region(const tsa_expert_layout& L, int64_t T, int k) {
     const int64_t v1 = (T * k * L.inter * 4 + 255) / 256 * 256;
-    const int64_t fu = mx_fused_ws_bytes(L, T, k);
-    return v1 > fu ? v1 : fu;
+    const int64_t fu = mx_fused_ws_bytes(L, T, k), ti = mxt_ws_bytes(L, T, k);
+    return v1 > fu ? (v1 > ti ? v1 : ti) : (fu > ti ? fu : ti);
 }
 static int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
-    return WS_HDR + h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
+    return h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
 }
 
 int validate_layout(const tsa_expert_layout* L) {
@@ -300,8 +301,8 @@ __global__ void __launch_bounds__(256) tsa_map_slots_kernel(const int32_t* __res
     slots[a] = (e >= 0 && e < E) ? expert_slot[e] : -1;
 }
 
-// Tiled MXFP4 layouts: the fused MFMA kernel over chunks of up to 4 tokens (one launch
-// each, stream-ordered on the shared workspace, whose counters every launch resets).
+// Tiled MXFP4 layouts: the MFMA launch pair over chunks of up to 4 tokens (stream-ordered
+// on the shared workspace).
 static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
                         const float* weights, const void* logits, int logits_dtype, int mode,
                         const int32_t* expert_slot, int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k,
@@ -314,10 +315,10 @@ static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n
     for (int64_t t0 = 0; t0 < T; t0 += 4) {
         const int64_t tc = T - t0 < 4 ? T - t0 : 4;
         const void* lg = logits ? static_cast<const uint8_t*>(logits) + t0 * E * dtype_size(logits_dtype) : nullptr;
-        int rc = mxt_fused_decode(L, pl, n_slots, slots ? slots + t0 * k : nullptr, weights ? weights + t0 * k : nullptr,
-                                  lg, logits_dtype, mode, expert_slot, E, idx_out ? idx_out + t0 * k : nullptr,
-                                  w_out ? w_out + t0 * k : nullptr, tc, k, static_cast<const uint16_t*>(x) + t0 * H,
-                                  static_cast<uint8_t*>(y) + t0 * H * ys, y_dtype, ws, ws_bytes, st);
+        int rc = mxt_decode(L, pl, n_slots, slots ? slots + t0 * k : nullptr, weights ? weights + t0 * k : nullptr, lg,
+                            logits_dtype, mode, expert_slot, E, idx_out ? idx_out + t0 * k : nullptr,
+                            w_out ? w_out + t0 * k : nullptr, tc, k, static_cast<const uint16_t*>(x) + t0 * H,
+                            static_cast<uint8_t*>(y) + t0 * H * ys, y_dtype, ws, ws_bytes, st);
         if (rc) return rc;
     }
     return TSA_OK;
@@ -364,7 +365,7 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
                              const float* weights, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
                              uint8_t* ws, hipStream_t st) {
     const Launch s = shapes(L, T, k);
-    float* h = reinterpret_cast<float*>(ws + WS_HDR);
+    float* h = reinterpret_cast<float*>(ws);
     const bool a16 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 15) == 0;
     hipError_t e = hipSuccess;
     if (L.format == TSA_EXPERT_MXFP4) {
@@ -382,7 +383,7 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
     }
     if (use_gq(L, pl, k))
         return gq_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
-                         y, y_dtype, ws, WS_HDR + h_region(L, T, k), st);
+                         y, y_dtype, ws, h_region(L, T, k), st);
     const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
     switch (L.gate_type) {
         case 8: e = a2 ? launch_gguf_a<8, 2>(s, L, pl, n_slots, slots, k, x, x_dtype, h, st)
@@ -444,7 +445,7 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
                          T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
     // separate routing, slot mapping and the two-launch decode
     const int64_t tk = (T * k * 4 + 255) / 256 * 256;
-    uint8_t* extra = ws + WS_HDR + h_region(L, T, k);
+    uint8_t* extra = ws + h_region(L, T, k);
     int32_t* slots = reinterpret_cast<int32_t*>(extra);
     int32_t* idx = idx_out ? idx_out : reinterpret_cast<int32_t*>(extra + tk);
     float* w = w_out ? w_out : reinterpret_cast<float*>(extra + 2 * tk);

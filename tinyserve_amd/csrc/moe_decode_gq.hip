@@ -307,7 +307,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     TSA_REQUIRE(!logits || (E <= 256 && T <= FUSED_MAXT), TSA_ERR_SHAPE, "GGUF decode routing: E %lld, T %lld",
                 (long long)E, (long long)T);
     // h (bf16) then, for routed calls, the slot / weight table phase A writes for phase B
-    const int64_t h_bytes = T * k * L.inter * 2, tab_off = WS_HDR + (h_bytes + 255) / 256 * 256;
+    const int64_t h_bytes = T * k * L.inter * 2, tab_off = (h_bytes + 255) / 256 * 256;
     TSA_REQUIRE(ws_bytes >= tab_off + T * k * 8, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
     GqParams p{};
     p.L = L;
@@ -328,7 +328,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     p.x_dtype = x_dtype;
     p.y = y;
     p.y_dtype = y_dtype;
-    p.h = reinterpret_cast<uint16_t*>(ws + WS_HDR);
+    p.h = reinterpret_cast<uint16_t*>(ws);
     p.h_bytes = h_bytes;
     p.tab_slot = reinterpret_cast<int32_t*>(ws + tab_off);
     p.tab_w = reinterpret_cast<float*>(ws + tab_off + T * k * 4);

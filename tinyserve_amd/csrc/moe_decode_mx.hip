@@ -1,36 +1,25 @@
-// Fused single-launch MXFP4 MoE decode (gfx950): routing + gate_up + clamped SwiGLU +
-// down + weighted top-k sum in one persistent launch.
+// MXFP4 MoE decode over the checkpoint-order layout (gfx950): routing + gate_up + clamped
+// SwiGLU + down + weighted top-k sum in two launches.
 //
-// Work is a task list, phase A first:
-//   phase A task = (token t, expert j, 64 gate_up rows): each of the 4 waves owns 16
-//     consecutive rows (16 x 1440 B contiguous for K = 2880) and streams them with fully
-//     contiguous 16-byte-per-lane buffer loads: lane l of load s holds 16-byte group
-//     chunk c = 64 s + l of the tile, i.e. row c / G, group c % G. Each chunk (32 e2m1
-//     values) is expanded to bf16 pairs with v_cvt_scalef32_pk_bf16_fp4 (exact) and
-//     dotted with the activation's bf16 pairs from LDS by v_dot2c_f32_bf16 (fp32
-//     accumulate), then scaled by its e8m0 group scale and accumulated into the lane's
-//     partial of that row. DPP wave reductions give the 16 row sums; row pairs (gate,
-//     up) go through the clamped SwiGLU and the 8 h values are published with
-//     agent-coherent stores; once all 4 waves' stores are complete the workgroup adds 1
-//     to the completion counter of its (token, expert) pair.
-//   phase B task = (token t, 16 output rows): wave j computes expert j's 16 down rows
-//     the same way, with h (rounded to bf16, like the reference's bf16 activations)
-//     staged in LDS; the waves' weighted rows are summed in a fixed order in LDS, so each
-//     output has one writer and the result is deterministic.
+// Launch 1 (gate_up), workgroup = (token t, expert j, 64 gate_up rows): each of the 4
+//   waves owns 16 consecutive rows (16 x 1440 B contiguous for K = 2880) and streams them
+//   with fully contiguous 16-byte-per-lane buffer loads: lane l of load s holds 16-byte
+//   group chunk c = 64 s + l of the tile, i.e. row c / G, group c % G. Each chunk (32 e2m1
+//   values) is expanded to bf16 pairs with v_cvt_scalef32_pk_bf16_fp4 (exact) and dotted
+//   with the activation's bf16 pairs from LDS by v_dot2c_f32_bf16 (fp32 accumulate), then
+//   scaled by its e8m0 group scale and accumulated into the lane's partial of that row.
+//   DPP wave reductions give the 16 row sums; row pairs (gate, up) go through the clamped
+//   SwiGLU and the 8 h values go to the workspace.
+// Launch 2 (down), workgroup = (token t, 16 output rows): wave j computes expert j's 16
+//   down rows the same way, with h (rounded to bf16, like the reference's bf16
+//   activations) staged in LDS; the waves' weighted rows are summed in a fixed order in
+//   LDS, so each output has one writer and the result is deterministic.
+// No workgroup waits for another (stream order is the only synchronisation), so the
+// workspace holds no counters and nothing needs resetting between calls.
 //
-// Synchronisation: before a wave first reads h of pair (t, j) it polls that pair's
-// counter (relaxed, bounded) until all I/32 phase A tasks of the pair have counted, and
-// it issues the task's weight loads before polling, so the wait overlaps HBM traffic.
-// Each pair's counter sits in its own 256-byte block and takes one atomic per phase A
-// workgroup task: same-address agent-scope atomics serialise, so one counter per wave
-// (1440 adds for GPT-OSS-20B shapes) costs ~15 us where this costs ~1. The grid never
-// exceeds the co-resident workgroup count and every workgroup finishes its phase A
-// tasks before it polls, so every wait ends; the spin limit is a backstop that sets an
-// error flag. The last phase B workgroup to leave resets the counters for the next launch
-// (workgroups without phase B work never read them).
-//
-// Routing (optional) runs in every workgroup's prologue on wave 0 with DPP reductions
-// (descending logit, ties to the lower expert id) while the other waves stage x.
+// Routing (optional) runs in every workgroup's prologue of both launches on wave 0 with
+// DPP reductions (descending logit, ties to the lower expert id) while the other waves
+// stage x; both launches select the same experts from the same logits.
 //
 // Semantics: tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases, clamped
 // SwiGLU), :456-473 (routing), tinyserve/csrc/expert_loop.cpp:83-121 (weighted sum).
@@ -46,7 +35,7 @@ constexpr int MAXT = FUSED_MAXT;
 constexpr int MAXK = FUSED_MAXK;
 constexpr int WAVES = 4;
 constexpr int ROWS = 16;  // rows per wave tile
-constexpr int MISC_LDS = 2048;  // slot/weight/selection tables, per-wave row sums, flag
+constexpr int MISC_LDS = 2048;  // slot/weight/selection tables, per-wave row sums
 
 struct MxParams {
     tsa_expert_layout L;
@@ -63,9 +52,7 @@ struct MxParams {
     const uint16_t* x;  // bf16 [T, H]
     void* y;
     int y_dtype;
-    float* h;       // [T, k, I] published intermediate
-    unsigned* bar;  // workspace header: [1] phase B workgroups finished, [2] error flag, pair counters
-    int nA, nB, grid;
+    float* h;  // [T, k, I] intermediate (workspace)
 };
 
 
@@ -170,8 +157,8 @@ __device__ __forceinline__ float tile_rows(const Tile<G>& tl, const uint8_t* rs,
 }
 
 // A copy of v the compiler cannot see through: lane-derived addressing is then recomputed
-// inside each task instead of being hoisted out of the task loop and kept live (which
-// would cost ~4 VGPRs per load step).
+// where it is used instead of being hoisted and kept live (which would cost ~4 VGPRs per
+// load step).
 __device__ __forceinline__ int opaque(int v) {
     asm volatile("" : "+v"(v));
     return v;
@@ -201,8 +188,8 @@ __device__ __forceinline__ void stage_h(uint8_t* hs, const float* src, int I, in
     for (int base = 0; base < pieces; base += 64 * B) {
         u32x4 v[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b)  // sc1: coherent with the other XCDs' published stores
-            v[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (base + 64 * b + lane), 0, 16));
+        for (int b = 0; b < B; ++b)
+            v[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (base + 64 * b + lane), 0, 0));
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const int pc = base + 64 * b + lane;
@@ -218,7 +205,8 @@ __device__ __forceinline__ void stage_h(uint8_t* hs, const float* src, int I, in
     }
 }
 
-template <int G>
+// PHASE 0: launch 1 (workgroup b = gate_up task b); PHASE 1: launch 2 (workgroup b = down task b).
+template <int G, int PHASE>
 __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
@@ -228,13 +216,12 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
     int* s_slot = reinterpret_cast<int*>(smem);                      // [MAXT*MAXK]
     float* s_w = reinterpret_cast<float*>(smem + 4 * MAXT * MAXK);   // [MAXT*MAXK]
     float* s_y = reinterpret_cast<float*>(smem + 12 * MAXT * MAXK);  // [WAVES][16]
-    int* s_flag = reinterpret_cast<int*>(smem + 12 * MAXT * MAXK + 4 * WAVES * ROWS);
     uint8_t* rsc = smem + MISC_LDS + wave * ROWS * G;  // this wave's tile scales
-    uint8_t* vec = smem + MISC_LDS + WAVES * ROWS * G;  // phase A: x [T][H] bf16; phase B: h [WAVES][I] bf16
+    uint8_t* vec = smem + MISC_LDS + WAVES * ROWS * G;  // launch 1: x [T][H] bf16; launch 2: h [WAVES][I] bf16
 
     // ---- prologue: routing / slot table on wave 0 while the other waves stage the
-    // activations into LDS (phase A workgroups only)
-    const bool stage = (int)blockIdx.x < p.nA;
+    // activations into LDS (launch 1 only)
+    constexpr bool stage = PHASE == 0;
     if (p.logits) {
         if (wave == 0) {
             int es[4];
@@ -242,7 +229,7 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
             for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
             for (int t = 0; t < T; ++t) {
                 const int sel = route_token(p, t, lane, es, s_slot, s_w);
-                if (blockIdx.x == 0 && p.idx_out && lane < k) {
+                if (PHASE == 0 && blockIdx.x == 0 && p.idx_out && lane < k) {
                     p.idx_out[t * k + lane] = sel;
                     p.w_out[t * k + lane] = s_w[t * k + lane];
                 }
@@ -258,122 +245,75 @@ __global__ void __launch_bounds__(256, 2) mx_decode_kernel(MxParams p) {
         if (stage)
             for (int t = 0; t < T; ++t) stage_bf16(vec + t * H * 2, p.x + (int64_t)t * H, H, tid, blockDim.x);
     }
-    if (tid == 0) s_flag[0] = 0;
     __syncthreads();
 
-    // ---- phase A: gate_up rows -> SwiGLU -> publish h
-    int task = blockIdx.x;
-    const int tiles = I / 32;  // 64-row tiles per expert, 32 h values each
-    for (; task < p.nA; task += p.grid) {
+    if (PHASE == 0) {
+        // ---- gate_up rows -> SwiGLU -> h
+        const int task = blockIdx.x;
+        const int tiles = I / 32;  // 64-row tiles per expert, 32 h values each
         const int t = task / (k * tiles), j = (task / tiles) % k, kb = task % tiles;
         const int64_t slot = uniform(s_slot[t * k + j]);
-        const bool live = slot >= 0 && slot < p.n_slots;
+        if (slot < 0 || slot >= p.n_slots) return;  // a dead pair's h is never read
         const int64_t row0 = (int64_t)kb * 64 + ROWS * wave;
-        float hv = 0.0f;
-        if (live) {
-            const uint8_t* base = p.pool + slot * L.slot_bytes;
-            float bias = 0.0f;
-            if (L.gate_bias_off >= 0) bias = load_bias(base + L.gate_bias_off, L.bias_dtype, row0 + (lane & (ROWS - 1)));
-            Tile<G> tl;
-            tile_load<G>(tl, rsc, base + L.gate_off, base + L.gate_scales_off, 2 * (int64_t)I, row0, lane);
-            const float rs = tile_rows<G>(tl, rsc, vec + t * H * 2, opaque(lane)) + bias;  // lane r < 16: row r
-            const float up = __shfl_down(rs, 1, 64);                          // lane 2i: (gate, up) of h row0/2 + i
-            hv = swiglu_oai(L, rs, up);
-        }
-        if (lane < ROWS && (lane & 1) == 0)
-            __hip_atomic_store(p.h + (int64_t)(t * k + j) * I + row0 / 2 + lane / 2, hv, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's h stores are complete ...
-        __syncthreads();                // ... and so are the other waves' before the count moves
-        if (tid == 0) __hip_atomic_fetch_add(pair_ctr(p.bar, t * k + j), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint8_t* base = p.pool + slot * L.slot_bytes;
+        float bias = 0.0f;
+        if (L.gate_bias_off >= 0) bias = load_bias(base + L.gate_bias_off, L.bias_dtype, row0 + (lane & (ROWS - 1)));
+        Tile<G> tl;
+        tile_load<G>(tl, rsc, base + L.gate_off, base + L.gate_scales_off, 2 * (int64_t)I, row0, lane);
+        const float rs = tile_rows<G>(tl, rsc, vec + t * H * 2, opaque(lane)) + bias;  // lane r < 16: row r
+        const float up = __shfl_down(rs, 1, 64);                                       // lane 2i: (gate, up) of h row0/2 + i
+        const float hv = swiglu_oai(L, rs, up);
+        if (lane < ROWS && (lane & 1) == 0) p.h[(int64_t)(t * k + j) * I + row0 / 2 + lane / 2] = hv;
+        return;
     }
 
-    // ---- phase B: down rows of every selected expert, weighted sum in a fixed order
-    bool did_b = false;
-    uint64_t ready = 0;  // pairs t*k+j whose h this wave has seen complete (wave-uniform)
+    // ---- down rows of every selected expert, weighted sum in a fixed order
     const int RB = H / ROWS;
     const int rounds = (k + WAVES - 1) / WAVES;
     uint8_t* hs = vec + wave * I * 2;
-    const unsigned need = (unsigned)(I / 32);  // phase A tasks per pair
-    for (; task < p.nA + p.nB; task += p.grid) {
-        did_b = true;
-        const int b = task - p.nA;
-        const int t = b / RB;
-        const int64_t n0 = (int64_t)(b % RB) * ROWS;
-        float yv = 0.0f;  // lane r < 16: this wave's weighted row n0 + r
-        for (int rd = 0; rd < rounds; ++rd) {
-            const int j = rd * WAVES + wave;
-            const int64_t slot = j < k ? uniform(s_slot[t * k + j]) : -1;
-            const bool live = slot >= 0 && slot < p.n_slots;
-            const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
-            Tile<G> tl;
-            float bias = 0.0f;
-            if (live) {
-                if (L.down_bias_off >= 0) bias = load_bias(base + L.down_bias_off, L.bias_dtype, n0 + (lane & (ROWS - 1)));
-                tile_load<G>(tl, rsc, base + L.down_off, base + L.down_scales_off, (int64_t)H, n0, lane);
-            }
-            if (live) {
-                const int pair = t * k + j;
-                if (!((ready >> pair) & 1)) {  // the task's weights are in flight already
-                    unsigned* c = pair_ctr(p.bar, pair);
-                    int spins = 0;
-                    while (ld_relaxed(c) < need) {
-                        __builtin_amdgcn_s_sleep(4);
-                        if (++spins > SPIN_LIMIT) {
-                            __hip_atomic_store(&p.bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            s_flag[0] = 1;
-                            break;
-                        }
-                    }
-                    ready |= 1ull << pair;
-                }
-                // h of (t, j) -> bf16 in this wave's LDS area. 16-byte buffer loads with the
-                // sc1 (agent-coherent) cache policy, all issued before the first use.
-                stage_h(hs, p.h + (int64_t)(t * k + j) * I, I, lane);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                const float rs = tile_rows<G>(tl, rsc, hs, opaque(lane)) + bias;
-                yv += s_w[t * k + j] * rs;
-            }
-        }
-        if (lane < ROWS) s_y[wave * ROWS + lane] = yv;
-        __syncthreads();
-        if (wave == 0 && lane < ROWS) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) sum += s_y[w * ROWS + lane];
-            store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + lane, sum);
-        }
-        const bool aborted = s_flag[0] != 0;  // written before the barrier above
-        __syncthreads();
-        if (aborted) break;
+    const int b = blockIdx.x;
+    const int t = b / RB;
+    const int64_t n0 = (int64_t)(b % RB) * ROWS;
+    float yv = 0.0f;  // lane r < 16: this wave's weighted row n0 + r
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int j = rd * WAVES + wave;
+        const int64_t slot = j < k ? uniform(s_slot[t * k + j]) : -1;
+        if (slot < 0 || slot >= p.n_slots) continue;
+        const uint8_t* base = p.pool + slot * L.slot_bytes;
+        float bias = 0.0f;
+        if (L.down_bias_off >= 0) bias = load_bias(base + L.down_bias_off, L.bias_dtype, n0 + (lane & (ROWS - 1)));
+        Tile<G> tl;
+        tile_load<G>(tl, rsc, base + L.down_off, base + L.down_scales_off, (int64_t)H, n0, lane);
+        // h of (t, j) -> bf16 in this wave's LDS area, all loads issued before the first use
+        stage_h(hs, p.h + (int64_t)(t * k + j) * I, I, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        const float rs = tile_rows<G>(tl, rsc, hs, opaque(lane)) + bias;
+        yv += s_w[t * k + j] * rs;
     }
-    // ---- leave: the last phase B workgroup out resets the counters for the next launch.
-    // Every phase A count has landed by then (each pair was seen complete), and the
-    // workgroups without phase B work never read the counters.
-    if (did_b && tid == 0) {
-        const unsigned nbw = (unsigned)(p.nB < p.grid ? p.nB : p.grid);
-        const unsigned done = __hip_atomic_fetch_add(&p.bar[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done == nbw - 1) {
-            for (int i = 0; i < T * k; ++i)
-                __hip_atomic_store(pair_ctr(p.bar, i), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&p.bar[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    if (lane < ROWS) s_y[wave * ROWS + lane] = yv;
+    __syncthreads();
+    if (wave == 0 && lane < ROWS) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += s_y[w * ROWS + lane];
+        store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + lane, sum);
     }
 }
 
 template <int G>
-const void* kernel_ptr() {
-    return reinterpret_cast<const void*>(&mx_decode_kernel<G>);
+const void* kernel_ptr(int phase) {
+    return phase ? reinterpret_cast<const void*>(&mx_decode_kernel<G, 1>)
+                 : reinterpret_cast<const void*>(&mx_decode_kernel<G, 0>);
 }
 
-const void* kernel_for_g(int G) {
+const void* kernel_for_g(int G, int phase) {
     switch (G) {
-        case 16: return kernel_ptr<16>();
-        case 32: return kernel_ptr<32>();
-        case 64: return kernel_ptr<64>();
-        case 90: return kernel_ptr<90>();
+        case 16: return kernel_ptr<16>(phase);
+        case 32: return kernel_ptr<32>(phase);
+        case 64: return kernel_ptr<64>(phase);
+        case 90: return kernel_ptr<90>(phase);
         default: return nullptr;
     }
 }
@@ -384,8 +324,8 @@ int64_t mx_fused_ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
     return (T * k * L.inter * 4 + 255) / 256 * 256;
 }
 
-// Enqueue the fused kernel: TSA_OK, 1 if the shape/layout/dtype is outside what it handles
-// (the caller then uses the two-launch kernels), or an error status.
+// Enqueue the two launches: TSA_OK, 1 if the shape/layout/dtype is outside what they
+// handle (the caller then uses the row kernels), or an error status.
 int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
                     int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y,
@@ -393,15 +333,17 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
     if (L.format != TSA_EXPERT_MXFP4 || L.act != TSA_ACT_SWIGLU_OAI || x_dtype != TSA_BF16) return 1;
     if (T < 1 || T > MAXT || k < 1 || k > MAXK || L.hidden != L.inter) return 1;
     const int G = (int)(L.hidden / 32);
-    const void* kfn = kernel_for_g(G);
-    if (!kfn) return 1;
+    const void* ka = kernel_for_g(G, 0);
+    const void* kb = kernel_for_g(G, 1);
+    if (!ka || !kb) return 1;
     if (logits && E > 256) return 1;
     const uintptr_t al = reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(x) | (uintptr_t)L.slot_bytes |
                          (uintptr_t)L.gate_off | (uintptr_t)L.down_off;
     if (al & 15) return 1;
-    TSA_REQUIRE(ws_bytes >= WS_HDR + mx_fused_ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
+    TSA_REQUIRE(ws_bytes >= mx_fused_ws_bytes(L, T, k), TSA_ERR_WORKSPACE,
                 "workspace too small for the fused decode");
-    const size_t lds = MISC_LDS + (size_t)WAVES * ROWS * G + (size_t)((T > WAVES ? T : WAVES) * L.hidden * 2);
+    const size_t lds_a = MISC_LDS + (size_t)WAVES * ROWS * G + (size_t)(T * L.hidden * 2);
+    const size_t lds_b = MISC_LDS + (size_t)WAVES * ROWS * G + (size_t)(WAVES * L.inter * 2);
 
     MxParams p{};
     p.L = L;
@@ -421,19 +363,10 @@ int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_s
     p.x = static_cast<const uint16_t*>(x);
     p.y = y;
     p.y_dtype = y_dtype;
-    p.bar = reinterpret_cast<unsigned*>(ws);
-    p.h = reinterpret_cast<float*>(ws + WS_HDR);
-    p.nA = (int)(T * k * (L.inter / 32));
-    p.nB = (int)(T * (L.hidden / ROWS));
-
-    int per_cu = 0;
-    TSA_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 256, lds));
-    const int cus = num_cus();
-    TSA_REQUIRE(per_cu > 0 && cus > 0, TSA_ERR_HIP, "fused decode kernel cannot be resident (lds %zu)", lds);
-    const int resident = per_cu * cus;
-    p.grid = p.nA + p.nB < resident ? p.nA + p.nB : resident;
+    p.h = reinterpret_cast<float*>(ws);
     void* args[] = {&p};
-    TSA_HIP_CHECK(hipLaunchKernel(kfn, dim3(p.grid), dim3(256), args, lds, st));
+    TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / 32))), dim3(256), args, lds_a, st));
+    TSA_HIP_CHECK(hipLaunchKernel(kb, dim3((unsigned)(T * (L.hidden / ROWS))), dim3(256), args, lds_b, st));
     return TSA_OK;
 }
 

@@ -53,18 +53,6 @@ inline bool gguf_geometry(int type, int* block_elems, int* type_size) {
 
 int num_cus();  // compute units of the current device (cached per device)
 
-// MoE decode workspace header: [0, 256) launch-wide words (workgroups finished, error
-// flag), then one completion counter per (token, expert) pair, each in its own 256-byte
-// block so that their atomics do not serialise on one address, then per (token, expert)
-// pair WS_FLAG_WORDS completion flags, one per gate_up task (written with plain stores,
-// so that 90 tasks finishing together do not queue behind one atomic unit). Zero before
-// first use; every launch leaves them zero. The decode's intermediate activations follow.
-constexpr int64_t WS_CTR_OFF = 256;
-constexpr int64_t WS_CTR_STRIDE = 256;
-constexpr int64_t WS_MAX_PAIRS = 64;
-constexpr int64_t WS_FLAG_OFF = WS_CTR_OFF + WS_MAX_PAIRS * WS_CTR_STRIDE;  // 16640
-constexpr int64_t WS_FLAG_WORDS = 96;  // tasks per pair: inter / 32 <= 96 (inter <= 3072)
-constexpr int64_t WS_HDR = WS_FLAG_OFF + WS_MAX_PAIRS * WS_FLAG_WORDS * 4;  // 41216, a multiple of 256
 
 // ---------------------------------------------------------------- device helpers
 // IEEE binary16 bits -> float, exact (subnormals kept) without relying on FP modes.

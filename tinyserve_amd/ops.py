@@ -173,10 +173,10 @@ def _n_slots(pool: torch.Tensor, layout: _lib.ExpertLayout) -> int:
 
 
 def moe_decode_workspace(layout: _lib.ExpertLayout, T: int, k: int, device) -> torch.Tensor:
-    """Zero-filled decode workspace (its barrier counters must start at zero; calls keep them so)."""
+    """Decode workspace (uninitialised: the decode keeps no state in it between calls)."""
     n = ctypes.c_int64()
     _lib.check(_lib.load().tsa_moe_decode_workspace_size(ctypes.byref(layout), int(T), int(k), ctypes.byref(n)))
-    return torch.zeros(max(n.value, 1), dtype=torch.uint8, device=device)
+    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
 
 
 def moe_decode(layout: _lib.ExpertLayout, pool: torch.Tensor, slots: torch.Tensor, weights: torch.Tensor,
