@@ -88,11 +88,23 @@ def gguf_expert_forward(x: np.ndarray, e: dict, weights=None) -> np.ndarray:
 
 
 # ----------------------------------------------------------------------------- routing
+def _topk_order(v: np.ndarray) -> np.ndarray:
+    """Per row, indices in torch.topk's order: NaN first, then descending value, ties (and
+    NaNs among themselves) to the lower index."""
+    v = np.asarray(v)
+    n = v.shape[-1]
+    out = np.empty(v.shape, dtype=np.int64)
+    for r, row in zip(np.ndindex(v.shape[:-1]), v.reshape(-1, n)):
+        nan = np.isnan(row)
+        out[r] = np.lexsort((np.arange(n), -np.where(nan, 0.0, row), ~nan))
+    return out
+
+
 def route_topk_then_softmax(logits: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
     """torch.topk(logits, k) then softmax over the k values (_model_hooks.py:466-473).
-    Ties resolve to the lower expert index (stable descending sort)."""
+    Ties resolve to the lower expert index; NaN ranks above every number (torch.topk)."""
     logits = np.asarray(logits, dtype=np.float32)
-    idx = np.argsort(-logits, axis=-1, kind="stable")[..., :k]
+    idx = _topk_order(logits)[..., :k]
     vals = np.take_along_axis(logits, idx, axis=-1).astype(np.float64)
     ex = np.exp(vals - vals.max(axis=-1, keepdims=True))
     w = ex / ex.sum(axis=-1, keepdims=True)
@@ -104,7 +116,7 @@ def route_softmax_then_topk(logits: np.ndarray, k: int, renormalize: bool = True
     logits = np.asarray(logits, dtype=np.float32).astype(np.float64)
     ex = np.exp(logits - logits.max(axis=-1, keepdims=True))
     p = ex / ex.sum(axis=-1, keepdims=True)
-    idx = np.argsort(-p, axis=-1, kind="stable")[..., :k]
+    idx = _topk_order(p)[..., :k]
     w = np.take_along_axis(p, idx, axis=-1)
     if renormalize:
         w = w / w.sum(axis=-1, keepdims=True)

@@ -41,6 +41,48 @@ def test_route_ties_go_to_lower_index():
     np.testing.assert_allclose(w[0].cpu().numpy(), 0.25, rtol=1e-6)
 
 
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+@pytest.mark.parametrize("E,k", [(32, 4), (100, 8), (256, 16)])
+def test_route_nan_logits_same_in_every_router(E, k):
+    """NaN logits rank above every number (as torch.topk ranks them) in the standalone
+    router and in the routing inside both MXFP4 decode paths; a selected NaN or +inf makes
+    the token's weights NaN, as torch's softmax does. Row 3 has no NaN or inf: its output is
+    checked against the oracle."""
+    rng = np.random.default_rng(E + k)
+    T = 4
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    logits[0, 3] = np.nan
+    logits[1, 7] = np.nan
+    logits[1, E - 1] = np.nan
+    logits[2, 5] = np.inf
+    ridx, rw = oex.route_topk_then_softmax(logits, k)
+    idx, w = ops.route_topk(torch.from_numpy(logits).cuda(), k)
+    assert np.array_equal(idx.cpu().numpy(), ridx), "standalone router"
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, equal_nan=True)
+    for tiled in (False, True):
+        H, I = (512, 512) if not tiled else (256, 128)
+        rng2 = np.random.default_rng(7)
+        experts = [synth.make_mxfp4_expert(rng2, H, I) for _ in range(6)]
+        if tiled:
+            lay = synth.mxfp4_tiled_layout(H, I)
+            pool = np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in experts])
+        else:
+            lay = synth.mxfp4_layout(H, I)
+            pool = np.stack([synth.pack_mxfp4_expert(e, lay) for e in experts])
+        L = mxfp4_expert_layout(lay, tiled=tiled)
+        es = torch.arange(E, dtype=torch.int32, device="cuda") % 6
+        x_bits = synth.bf16_normal(rng, (T, H))
+        y, gidx, gw = ops.moe_decode_routed(L, torch.from_numpy(pool).cuda(), es, torch.from_numpy(logits).cuda(),
+                                            bf16_dev(x_bits), k, return_routing=True)
+        torch.cuda.synchronize()
+        what = "tiled" if tiled else "checkpoint order"
+        assert np.array_equal(gidx.cpu().numpy(), ridx), f"{what} decode routing"
+        np.testing.assert_allclose(gw.cpu().numpy(), rw, rtol=1e-5, equal_nan=True)
+        ref = oex.moe_combine(synth.bf16_to_f32(x_bits)[3:], ridx[3:] % 6, rw[3:],
+                              lambda e, xx: oex.mxfp4_expert_forward(xx, experts[e]))
+        assert_close_bf16(y[3:], ref, f"{what} decode, row without NaN")
+
+
 # ----------------------------------------------------------------------------- decode
 def _mx_setup(H, I, E, seed, bias=True):
     rng = np.random.default_rng(seed)

@@ -244,6 +244,27 @@ def test_routing_ties_go_to_lower_index():
     np.testing.assert_allclose(w, [[1 / 3] * 3], rtol=1e-6)
 
 
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+def test_routing_nan_and_inf_order_matches_torch_topk():
+    """NaN ranks above every number and +-inf keep their places, as torch.topk orders them
+    (rows without ties: torch leaves the order of equal values unspecified, and it varies
+    with the row length; the oracle resolves ties to the lower index)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        E = int(rng.integers(2, 300))
+        k = int(rng.integers(1, min(E, 16) + 1))
+        lg = rng.normal(size=(3, E)).astype(np.float32)
+        for r in range(3):
+            for val, p in ((np.nan, 0.5), (np.inf, 0.3), (-np.inf, 0.3)):
+                if rng.random() < p:
+                    lg[r, rng.integers(E)] = val
+        tv, ti = torch.topk(torch.from_numpy(lg), k, dim=-1)
+        idx, w = oex.route_topk_then_softmax(lg, k)
+        assert np.array_equal(idx, ti.numpy())
+        np.testing.assert_allclose(w, torch.softmax(tv.double(), dim=-1).float().numpy(), rtol=1e-6, equal_nan=True)
+
+
 # ----------------------------------------------------------------------------- activation / combine
 def test_gptoss_swiglu_closed_forms():
     sig = lambda v: 1.0 / (1.0 + np.exp(-v))  # noqa: E731

@@ -135,14 +135,15 @@ __device__ __forceinline__ float load_bias(const uint8_t* src, int dtype, int64_
     return dtype == TSA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
 
-// Orderable key of a logit: a larger float has a larger key, -0 and +0 share one key, and
-// NaN gets key 1, just above the key 0 of padding and of already selected entries (a
-// stable descending sort, as the reference's routing does, puts NaN last).
+// Orderable key of a logit: a larger float has a larger key, -0 and +0 share one key, NaN
+// gets the largest key (torch.topk, which the reference's routing calls, ranks NaN above
+// every number), and every logit's key is above the key 0 of padding and of entries
+// already selected.
 __device__ __forceinline__ uint32_t route_key(float v) {
     uint32_t u = __float_as_uint(v);
     u = u == 0x80000000u ? 0u : u;
     const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return v != v ? 1u : key;
+    return v != v ? 0xFFFFFFFFu : key;
 }
 __device__ __forceinline__ float route_key_value(uint32_t key) {
     return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
@@ -159,90 +160,53 @@ __device__ __forceinline__ float row16_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
 }
 
-// Number of set bits of m below this lane.
-__device__ __forceinline__ int bits_below(uint64_t m) {
-    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0x111, 0xF, 0xF>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x112, 0xF, 0xF>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x113, 0xF, 0xF>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x114, 0xF, 0xE>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x118, 0xF, 0xC>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x142, 0xA, 0xF>((int)v, 0));
+    v = max(v, (uint32_t)dpp_i<0x143, 0xC, 0xF>((int)v, 0));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// Top-k selection over NV logits per lane (expert e = lane + 64 j), k <= 16:
-//  1. the threshold: a bitwise search (most significant bit first) for the largest key t
-//     with at least k keys >= t, counted with ballots; it stops as soon as exactly k keys
-//     are >= t. Otherwise t is the k-th largest key and several keys equal it; those are
-//     taken in id order (the lowest ids first).
-//  2. each selected entry's rank among the k: the number of selected entries with a larger
-//     key, or an equal key and a lower id (one scalar read per selected entry).
-//  3. entry of rank r -> s_slot / s_w[t k + r] (id and key), read back by lane r, then the
-//     slot of the entry replaces the id.
-// Lane r < k ends with the key and id of the r-th selection.
+// Top-k selection over NV logits per lane (expert e = lane + 64 j), k <= 16, in k rounds:
+// each takes the largest remaining key with a DPP wave max, its lowest expert id among
+// equal keys with ballots, and removes it (key 0, below the key of every logit). The
+// selections come out in rank order: NaN first, then descending logit, ties to the lower id. Lane r < k ends with the key, id and slot (es) of the r-th selection.
 template <int NV, class P>
-__device__ void route_select(const P& p, int t, int lane, const float v[4], const int es[4], int* s_slot, float* s_w,
-                             uint32_t& myk, int& mysel) {
-    const int k = p.k;
+__device__ void route_select(const P& p, int lane, const float v[4], const int es[4], uint32_t& myk, int& mysel,
+                             int& myslot) {
     uint32_t key[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) key[j] = lane + 64 * j < p.E ? route_key(v[j]) : 0u;
-    uint32_t thr = 0;
-    int cnt = 64 * NV;
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t c = thr | (1u << bit);
-        int n = 0;
+    myk = 0u;
+    mysel = -1;
+    myslot = -1;
+    for (int r = 0; r < p.k; ++r) {
+        uint32_t m = key[0];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) n += __popcll(__ballot(key[j] >= c));
-        if (n >= k) {
-            thr = c;
-            cnt = n;
-            if (n == k) break;
-        }
-    }
-    bool sel[NV];
-    if (cnt == k) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) sel[j] = key[j] >= thr;
-    } else {  // ties at the k-th largest key
-        int need = k, before = 0;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) need -= __popcll(__ballot(key[j] > thr));
+        for (int j = 1; j < NV; ++j) m = max(m, key[j]);
+        const uint32_t top = wave_max_u32(m);
+        int id = -1, slot = -1;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const uint64_t eq = __ballot(key[j] == thr);
-            sel[j] = key[j] > thr || (key[j] == thr && before + bits_below(eq) < need);
-            before += __popcll(eq);
+            const uint64_t hit = __ballot(key[j] == top);
+            if (hit && id < 0) {
+                const int l = __ffsll((unsigned long long)hit) - 1;
+                id = 64 * j + l;
+                slot = __builtin_amdgcn_readlane(es[j], l);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) key[j] = lane + 64 * j == id ? 0u : key[j];
+        if (lane == r) {
+            myk = top;
+            mysel = id;
+            myslot = slot;
         }
     }
-    int rank[NV];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) rank[j] = 0;
-#pragma unroll
-    for (int jq = 0; jq < NV; ++jq) {
-        uint64_t m = __ballot(sel[jq]);
-        while (m) {
-            const int L = __ffsll((unsigned long long)m) - 1;
-            m &= m - 1;
-            const uint32_t kq = (uint32_t)__builtin_amdgcn_readlane((int)key[jq], L);
-            const int eq_id = 64 * jq + L;
-#pragma unroll
-            for (int j = 0; j < NV; ++j)
-                rank[j] += (kq > key[j] || (kq == key[j] && eq_id < 64 * j + lane)) ? 1 : 0;
-        }
-    }
-    uint32_t* s_key = reinterpret_cast<uint32_t*>(s_w) + t * k;
-#pragma unroll
-    for (int j = 0; j < NV; ++j)
-        if (sel[j]) {
-            s_slot[t * k + rank[j]] = 64 * j + lane;
-            s_key[rank[j]] = key[j];
-        }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    mysel = lane < k ? s_slot[t * k + lane] : -1;
-    myk = lane < k ? s_key[lane] : 0u;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll
-    for (int j = 0; j < NV; ++j)
-        if (sel[j]) s_slot[t * k + rank[j]] = es[j];
 }
 
 // One wave routes token t (E <= 256, k <= 16): slots of the selected experts into s_slot
@@ -251,19 +215,19 @@ __device__ void route_select(const P& p, int t, int lane, const float v[4], cons
 // id; the softmax is monotone, so this is also the top-k of the probabilities
 // (tinyserve/_model_hooks.py:456-473). Softmax over all experts, top-k and renormalisation
 // equals the softmax over the k selected logits, so that mode shares the top-k-softmax
-// path; only the unnormalised mode needs the sum over all experts.
+// path; only the unnormalised mode needs the sum over all experts. v[j] = logit lane + 64 j
+// of the token, loaded by the caller (as load4 gives them).
 template <class P>
-__device__ int route_token(const P& p, int t, int lane, const int es[4], int* s_slot, float* s_w) {
-    float v[4];
-    load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, v);
+__device__ int route_token_v(const P& p, int t, int lane, const float v[4], const int es[4], int* s_slot, float* s_w) {
     uint32_t myk;
-    int mysel;
+    int mysel, myslot;
     switch ((p.E + 63) >> 6) {
-        case 1: route_select<1>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
-        case 2: route_select<2>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
-        case 3: route_select<3>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
-        default: route_select<4>(p, t, lane, v, es, s_slot, s_w, myk, mysel); break;
+        case 1: route_select<1>(p, lane, v, es, myk, mysel, myslot); break;
+        case 2: route_select<2>(p, lane, v, es, myk, mysel, myslot); break;
+        case 3: route_select<3>(p, lane, v, es, myk, mysel, myslot); break;
+        default: route_select<4>(p, lane, v, es, myk, mysel, myslot); break;
     }
+    if (lane < p.k) s_slot[t * p.k + lane] = myslot;
     const float myval = route_key_value(myk);  // lane r < k: the r-th selected logit
     const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));  // the maximum
     float w;
@@ -280,6 +244,14 @@ __device__ int route_token(const P& p, int t, int lane, const int es[4], int* s_
     }
     if (lane < p.k) s_w[t * p.k + lane] = w;
     return mysel;
+}
+
+// route_token_v with the token's logits loaded here.
+template <class P>
+__device__ int route_token(const P& p, int t, int lane, const int es[4], int* s_slot, float* s_w) {
+    float v[4];
+    load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, v);
+    return route_token_v(p, t, lane, v, es, s_slot, s_w);
 }
 
 __device__ __forceinline__ float swiglu_oai(const tsa_expert_layout& L, float gate, float up) {

@@ -68,7 +68,9 @@ struct MxtParams {
     float h_scale, h_inv;
 };
 
-// A wave's 16-row tile: MM pieces of 1 KB and the scale words (byte m%4 of word m/4).
+// A wave's 16-row tile: MM pieces of 1 KB and the scale words (byte m%4 of word m/4) as
+// loaded; words >= w (past the row end) are masked where they are used (a select right
+// after the load would make the wave wait for the scales before it issues the pieces).
 // Buffer resources span exactly the tile, so pieces past a short row (K < 128 MM) read
 // zero without touching memory.
 template <int MM>
@@ -77,13 +79,13 @@ struct Tile {
     static constexpr int CHUNKS = (MS + 3) / 4;  // scale loads
     u32x4 q[MM];
     uint32_t sc[MS];
+    int w;
 };
 
-// The scale words (W per lane, W = stile_bytes / 256 <= MS) come in lane-major chunks of
+// The scale words (w per lane, w = stile_bytes / 256 <= MS) come in lane-major chunks of
 // up to 4 words: one 16-byte load per chunk, bounded to the tile's scale area. A load
-// wider than a lane's part of a chunk picks up the next lane's words; words >= W are
-// zeroed, so they can only meet the zero blocks of groups past the row end. Issues exactly
-// CHUNKS + MM buffer loads, in that order.
+// wider than a lane's part of a chunk picks up the next lane's words, which the mask at
+// use removes. Issues exactly CHUNKS + MM buffer loads, in that order.
 template <int MM>
 __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, int64_t tile_bytes,
                                           const uint8_t* scales, int64_t stile_bytes, int lane) {
@@ -92,12 +94,13 @@ __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, i
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(scales), (short)0, (int)stile_bytes, 0x00020000);
     const int W = (int)(stile_bytes >> 8);
+    tl.w = W;
 #pragma unroll
     for (int c = 0; c < Tile<MM>::CHUNKS; ++c) {
         const int wc = W - 4 * c < 4 ? (W - 4 * c > 0 ? W - 4 * c : 0) : 4;  // this chunk's words per lane
         const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * wc * lane, 1024 * c, 0));
 #pragma unroll
-        for (int d = 0; d < 4 && 4 * c + d < Tile<MM>::MS; ++d) tl.sc[4 * c + d] = 4 * c + d < W ? v[d] : 0u;
+        for (int d = 0; d < 4 && 4 * c + d < Tile<MM>::MS; ++d) tl.sc[4 * c + d] = v[d];
     }
     __builtin_amdgcn_sched_barrier(0);
     // Every piece is issued, in order, before any is used: left alone the scheduler sinks
@@ -110,78 +113,86 @@ __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, i
     }
 }
 
-// s[b] = word v of lane 16 b + (lane & 15): the scales of blocks 4m + b of the lane's
-// column, gathered from the four lane groups (v_permlane32_swap swaps the upper half of
-// its first operand with the lower half of its second, v_permlane16_swap likewise within
-// each 32-lane half).
-__device__ __forceinline__ void gather_groups(uint32_t v, uint32_t s[4]) {
-    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);        // groups g&1, (g&1)+2
-    const auto a = __builtin_amdgcn_permlane16_swap(h[0], h[0], false, false);  // groups 0, 1
-    const auto b = __builtin_amdgcn_permlane16_swap(h[1], h[1], false, false);  // groups 2, 3
-    s[0] = a[0];
-    s[1] = a[1];
-    s[2] = b[0];
-    s[3] = b[1];
+// The bias of row r as one dword load bounded to the n-element bias vector (n * element
+// size is a multiple of 4 here; a 2-byte element is the half of its dword that r & 1
+// selects). A zero-size bound (no bias) reads 0. One register, so no reuse of a pending
+// load's registers makes the wave wait for it early.
+__device__ __forceinline__ uint32_t bias_word(const uint8_t* src, int dtype, int64_t n, int64_t r) {
+    const int es = dtype == TSA_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), (short)0, (int)(n * es), 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b32(rb, (int)((r * es) & ~3ll), 0, 0);
+}
+__device__ __forceinline__ float bias_word_value(uint32_t w, int dtype, int64_t r) {
+    if (dtype == TSA_F32) return __uint_as_float(w);
+    const uint32_t h = (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+    return dtype == TSA_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
 }
 
-// One piece's scale bytes: byte e of word s[b] -> 2^(e - 127) as a float (e = 0 reads as 0).
-__device__ __forceinline__ void scale_fma(float (&acc)[4], const v4f& d, const uint32_t (&s)[4], int pp) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) acc[b] = fmaf(d[b], __uint_as_float(((s[b] >> (8 * pp)) & 255u) << 23), acc[b]);
+// One scaled MFMA: D = A * B (+ C) with A's blocks at scale 1 and B's block scales taken
+// per lane: lane 16q + i supplies the e8m0 scale of column i, K block q, as byte OPB of sb.
+template <int OPB>
+__device__ __forceinline__ v4f mfma_fp8_fp4(const v8i& A, const v8i& B, const v4f& C, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, C, 0, 4, 0, 0x7F7F7F7F, OPB, sb);
 }
 
-// sum over the tile's K of W[i][k] * term_g(k) in lane 16 g + i (g = 0, 1; lanes 32..63 hold
-// zero rows), W the lane's 16-row tile and term_g the g-th fp8 term of a vector in LDS. a_lo
-// and a_hi are the lane's A-operand sources (a_sources); four accumulators (one per block
-// position) keep the FMAs independent.
+// sum over the tile's K of W[i][k] * (term_0(k) + term_1(k)) in lane i < 16, W the wave's
+// 16-row tile and term_r the fp8 terms of a vector in LDS. Piece m is one
+// v_mfma_scale_f32_16x16x128_f8f6f4 (fp8 e4m3 A, cbsz 0; fp4 e2m1 B, blgp 4): A row r is
+// term r over the piece's 128 K (rows 2..15 zero), B is the piece as loaded, and the block
+// scales are applied by the instruction: lane 16q + i holds the scale word of (row i, blocks
+// 4m' + q), so byte m % 4 of its word m / 4 is exactly its B scale for piece m. The MFMA
+// accumulates across pieces. src: the lane's A-operand source (a_source). The A operands
+// of the next two pieces are read ahead of each MFMA (sched barriers keep them there: left
+// alone the scheduler moves the reads next to their use and the MFMAs wait for LDS, and
+// the reads are volatile so that no earlier pass hoists them all to the top).
+// 16 bytes from LDS (p points into LDS). Volatile: the read stays where it is written; the
+// explicit address space keeps it a ds_read with an immediate offset (through a generic
+// pointer the compiler precomputes a 64-bit flat address per read and runs out of registers).
+typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
+__device__ __forceinline__ u32x4 lds16(const uint8_t* p) {
+    return *(lds_u32x4*)(p);
+}
 template <int MM>
-__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* a_lo, const uint8_t* a_hi) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 lo = *reinterpret_cast<const u32x4*>(a_lo), hi = *reinterpret_cast<const u32x4*>(a_hi);
-    uint32_t s[4];
-    gather_groups(tl.sc[0], s);
-    v4f dp = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    // Software pipeline: piece m's MFMA is issued, piece m+1's A operand is read into the
-    // registers it has just consumed, and piece m-1's result is scaled and accumulated while
-    // the MFMA runs. The empty asm statement pins the accumulators at the end of each piece:
-    // without it the compiler sinks every piece's scaling to the end of the loop and keeps
-    // all MM results live (and spills).
+__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src) {
+    constexpr int PD = 2;
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 lo[PD + 1], hi[PD + 1];
+#pragma unroll
+    for (int i = 0; i <= PD && i < MM; ++i) {
+        lo[i] = lds16(src + 128 * i);
+        hi[i] = lds16(src + 128 * i + 64);
+    }
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        const v8i A = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        const int b = m % (PD + 1);
+        const v8i A = {(int)lo[b][0], (int)lo[b][1], (int)lo[b][2], (int)lo[b][3],
+                       (int)hi[b][0], (int)hi[b][1], (int)hi[b][2], (int)hi[b][3]};
         const v8i B = {(int)tl.q[m][0], (int)tl.q[m][1], (int)tl.q[m][2], (int)tl.q[m][3], 0, 0, 0, 0};
-        // fp8 e4m3 A (cbsz 0) x fp4 e2m1 B (blgp 4); zero scale operands select the unscaled
-        // instruction
-        const v4f d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 4, 0, 0,
-                                                                      0, 0);
-        if (m + 1 < MM) {
-            lo = *reinterpret_cast<const u32x4*>(a_lo + 128 * (m + 1));
-            hi = *reinterpret_cast<const u32x4*>(a_hi + 128 * (m + 1));
+        const int sb = m / 4 < tl.w ? (int)tl.sc[m / 4] : 0x7F7F7F7F;  // past the row end: any finite scale
+        switch (m & 3) {
+            case 0: acc = mfma_fp8_fp4<0>(A, B, acc, sb); break;
+            case 1: acc = mfma_fp8_fp4<1>(A, B, acc, sb); break;
+            case 2: acc = mfma_fp8_fp4<2>(A, B, acc, sb); break;
+            default: acc = mfma_fp8_fp4<3>(A, B, acc, sb); break;
         }
-        if (m > 0) {
-            scale_fma(acc, dp, s, (m - 1) % 4);
-            if (m % 4 == 0) gather_groups(tl.sc[m / 4], s);  // piece m's word, after piece m-1 used the last
+        asm volatile("" : "+v"(acc));  // piece m's MFMA stays ahead of the next reads
+        if (m + PD + 1 < MM) {
+            lo[b] = lds16(src + 128 * (m + PD + 1));
+            hi[b] = lds16(src + 128 * (m + PD + 1) + 64);
         }
-        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
-        dp = d;
         __builtin_amdgcn_sched_barrier(0);
     }
-    scale_fma(acc, dp, s, (MM - 1) % 4);
-    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    return acc[0] + acc[1];  // lanes 0..15: rows 0 and 1 of D, column = lane
 }
 
-// The lane's A-operand sources for a vector whose two terms start at `terms` (term r at
-// terms + r * kp, zero past the vector's end): row 4r+b of A, K slice kq = lane / 16. Bytes
-// 0..15 of the operand are K = 16 kq .. 16 kq + 15 (block kq / 2), bytes 16..31 are
-// K = 64 + 16 kq .. (block 2 + kq / 2); a lane whose row and slice do not meet reads a zero
-// area instead (rows 8..15 are all zero).
-__device__ __forceinline__ void a_sources(const uint8_t* terms, const uint8_t* zero, int kp, int lane,
-                                          const uint8_t*& lo, const uint8_t*& hi) {
-    const int row = lane & 15, r = row >> 2, b = row & 3, kq = lane >> 4;
-    const uint8_t* src = terms + r * kp + 32 * b + 16 * (kq & 1);
-    const bool live = r < 2;
-    lo = live && b < 2 && (kq >> 1) == b ? src : zero;
-    hi = live && b >= 2 && (kq >> 1) == b - 2 ? src : zero;
+// The lane's A-operand source for a vector whose two terms start at `terms` (term r at
+// terms + r * kp, zero past the vector's end): lane l holds row l % 16 of A, bytes 0..15 =
+// K 16 (l / 16) .. + 15 and bytes 16..31 = K 64 + 16 (l / 16) .. + 15 of each piece (read at
+// src + 128 m and src + 128 m + 64); rows 2..15 read a zero area of kp bytes instead.
+__device__ __forceinline__ const uint8_t* a_source(const uint8_t* terms, const uint8_t* zero, int kp, int lane) {
+    const int row = lane & 15, kq = lane >> 4;
+    return row < 2 ? terms + row * kp + 16 * kq : zero;
 }
 
 // 16 bytes per lane from buffer offset voff straight into LDS at lds + 16 lane (one 1 KB
@@ -205,116 +216,186 @@ __device__ __forceinline__ void lds_zero(uint8_t* a, int from, int to, int me, i
     for (int o = from + 16 * me; o < to; o += 16 * nthr) *reinterpret_cast<u32x4*>(a + o) = u32x4{0u, 0u, 0u, 0u};
 }
 
-constexpr int XCH = 3072 / 8 / (64 * (WAVES - 1));  // x chunks (8 values) per loading thread, H <= 3072
+constexpr int GU_WAVES = 2;        // waves per gate_up workgroup (one 16-row tile each)
+constexpr int XCH = 3072 / 8 / 64;  // x chunks (8 values) per lane when a wave loads all of x (H <= 3072)
+constexpr int GU_MISC = 512 * GU_WAVES;  // per wave: the routing scratch (64 composite keys)
+
+__device__ __forceinline__ void wave_lds_sync() {  // this wave's LDS writes before its later reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The token's top-k selection within one wave: lane r < k ends with the key, expert id and
+// slot of the r-th selection (rank order: NaN first, then descending logit, ties to the
+// lower id). lg / es: the token's logits and slot table as load4 lays them out. E <= 64:
+// lane e ranks expert e by counting the composite keys (route_key << 32 | ~id, unique) that
+// beat its own, read back from the wave's scratch kl (64 x 8 bytes), then the selection is
+// put in rank order through the same scratch; larger E: k rounds of route_select.
+template <class P>
+__device__ void select_topk(const P& p, int lane, const float lg[4], const int es[4], uint64_t* kl, uint32_t& myk,
+                            int& mysel, int& myslot) {
+    if (p.E > 64) {
+        switch ((p.E + 63) >> 6) {
+            case 2: route_select<2>(p, lane, lg, es, myk, mysel, myslot); break;
+            case 3: route_select<3>(p, lane, lg, es, myk, mysel, myslot); break;
+            default: route_select<4>(p, lane, lg, es, myk, mysel, myslot); break;
+        }
+        return;
+    }
+    const uint32_t key = lane < p.E ? route_key(lg[0]) : 0u;
+    const uint64_t mine = ((uint64_t)key << 32) | (uint32_t)~lane;
+    kl[lane] = lane < p.E ? mine : 0ull;  // padding never beats a logit's key
+    wave_lds_sync();
+    int rank = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (16 * g >= p.E) break;
+        uint64_t kk[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kk[i] = kl[16 * g + i];  // issued together, one wait
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rank += kk[i] > mine ? 1 : 0;
+    }
+    wave_lds_sync();
+    uint32_t* ks = reinterpret_cast<uint32_t*>(kl);  // [0, 16) keys, [16, 32) ids, [32, 48) slots
+    if (lane < p.E && rank < p.k) {
+        ks[rank] = key;
+        ks[16 + rank] = (uint32_t)lane;
+        ks[32 + rank] = (uint32_t)es[0];
+    }
+    wave_lds_sync();
+    myk = lane < p.k ? ks[lane] : 0u;
+    mysel = lane < p.k ? (int)ks[16 + lane] : -1;
+    myslot = lane < p.k ? (int)ks[32 + lane] : -1;
+}
 
 // ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h terms to the workspace.
-// Workgroup b: pair b % (T k), 64-row block b / (T k) (pair-major, so neighbouring
-// workgroups stream different experts).
+// Workgroup b: pair b % (T k), 32-row block b / (T k) (pair-major, so neighbouring
+// workgroups stream different experts). Two waves per workgroup: for GPT-OSS-20B shapes the
+// 720 workgroups spread over the 256 CUs more evenly than 360 four-wave ones would, which
+// shortens the weight stream (measured 6.2 against 6.8 us for the stream alone).
+//
+// The waves share nothing and never wait for each other: each selects the token's experts
+// itself, issues its tile's loads as soon as it knows the slot, and builds its own copy of
+// the x terms (max |x| over all of x, conversion, zero padding) in the shadow of those loads.
 template <int MM>
-__global__ void __launch_bounds__(256, 2) mxt_gate_up_kernel(MxtParams p) {
+__global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = 128 * MM;  // padded vector length
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int pairs = p.T * k;
-    const int kb = (int)blockIdx.x / pairs, pr = (int)blockIdx.x % pairs, t = pr / k;
-    int* s_slot = reinterpret_cast<int*>(smem);                     // [MAXT*MAXK]
-    float* s_w = reinterpret_cast<float*>(smem + 4 * MAXT * MAXK);  // [MAXT*MAXK]
-    float* s_xmax = reinterpret_cast<float*>(smem + 8 * MAXT * MAXK);  // [WAVES]
-    uint8_t* vec = smem + MISC_LDS;  // x terms [2][KP], then a zero area [KP]
+    const int kb = (int)blockIdx.x / pairs, pr = (int)blockIdx.x % pairs, t = pr / k, jj = pr % k;
+    uint64_t* kl = reinterpret_cast<uint64_t*>(smem + 512 * wave);  // this wave's routing scratch
+    uint8_t* vec = smem + GU_MISC + wave * 3 * KP;  // this wave's x terms [2][KP], then a zero area [KP]
     uint8_t* zero = vec + 2 * KP;
+    const bool routed = p.logits != nullptr;
 
-    // ---- prologue: waves 1..3 load x of token t into registers (every load issued before
-    // the first is used) and take its max |x|; wave 0 selects the token's experts and clears
-    // the terms' padding and the zero area.
+    // ---- loads, all issued before any is used: x of token t, then the routing inputs
     u32x4 xr[XCH];
-    if (wave > 0) {
-        const int me = tid - 64;
-        const uint16_t* xt = p.x + (int64_t)t * H;
+    const uint16_t* xt = p.x + (int64_t)t * H;
 #pragma unroll
-        for (int i = 0; i < XCH; ++i) {
-            const int c = me + 64 * (WAVES - 1) * i;
-            xr[i] = c < H / 8 ? *reinterpret_cast<const u32x4*>(xt + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-        }
-        float mx = 0.0f;
+    for (int i = 0; i < XCH; ++i) {
+        const int c = lane + 64 * i;
+        xr[i] = c < H / 8 ? *reinterpret_cast<const u32x4*>(xt + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float lg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int es[4] = {0, 0, 0, 0};
+    int64_t slot = -1;
+    uint32_t myk = 0u;
+    int mysel = -1, myslot = -1;
+    if (routed) {
 #pragma unroll
-        for (int i = 0; i < XCH; ++i)
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-                mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(xr[i][d] & 0xFFFFu)), fabsf(bf16_bits_to_f32(xr[i][d] >> 16))));
-        mx = wave_max_u(mx);
-        if (lane == 0) s_xmax[wave] = mx;
+        for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+        load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
+        select_topk(p, lane, lg, es, kl, myk, mysel, myslot);
+        slot = __builtin_amdgcn_readlane(myslot, jj);
     } else {
-        if (p.logits) {
-            int es[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
-            const int sel = route_token(p, t, lane, es, s_slot, s_w);
-            if (kb == 0 && pr % k == 0 && lane < k) {  // the token's first workgroup publishes the selection
-                p.sel_slot[t * k + lane] = s_slot[t * k + lane];
-                p.sel_w[t * k + lane] = s_w[t * k + lane];
-                if (p.idx_out) {
-                    p.idx_out[t * k + lane] = sel;
-                    p.w_out[t * k + lane] = s_w[t * k + lane];
-                }
-            }
-        } else if (lane == 0) {
-            s_slot[pr] = p.sel_slot[pr];
-        }
-        lds_zero(vec, H, KP, lane, 64);
-        lds_zero(vec + KP, H, KP, lane, 64);
-        lds_zero(zero, 0, KP, lane, 64);
+        slot = uniform(p.sel_slot[pr]);
     }
-    __syncthreads();
 
-    // ---- the wave's gate_up tile: rows row0 .. row0 + 15 of the pair's expert
-    const int64_t slot = uniform(s_slot[pr]);
+    // the token's first workgroup publishes the selection: softmax over the k selected
+    // logits, or (unnormalised mode) over all E
+    auto publish = [&]() {
+        const float myval = route_key_value(myk);
+        const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));
+        float w;
+        if (p.route_mode == TSA_ROUTE_SOFTMAX_TOPK) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (lane + 64 * j < p.E) sum += __expf(lg[j] - top);
+            const float z = wave_sum_u(sum);
+            w = lane < k ? __expf(myval - top) / z : 0.0f;
+        } else {
+            const float ex = lane < k ? __expf(myval - top) : 0.0f;
+            w = ex / row16_sum(ex);
+        }
+        if (lane < k) {
+            p.sel_slot[t * k + lane] = myslot;
+            p.sel_w[t * k + lane] = w;
+            if (p.idx_out) {
+                p.idx_out[t * k + lane] = mysel;
+                p.w_out[t * k + lane] = w;
+            }
+        }
+    };
+    const bool publisher = routed && kb == 0 && jj == 0 && wave == 0;
     const bool live = slot >= 0 && slot < p.n_slots;
-    const int64_t row0 = (int64_t)kb * 64 + 16 * wave;
-    const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
-    const bool hbias = L.gate_bias_off >= 0;
-    Tile<MM> tl;
-    u32x4 braw = u32x4{0u, 0u, 0u, 0u};
-    if (live) {
-        if (hbias) braw = bias_raw(base + L.gate_bias_off, L.bias_dtype, 2 * (int64_t)I, row0 + (lane & 15));
-        const int64_t tile = row0 / 16;
-        tile_load<MM>(tl, base + L.gate_off + tile * p.gu_tile, p.gu_tile, base + L.gate_scales_off + tile * p.gu_stile,
-                      p.gu_stile, lane);
+    if (!live) {  // a dead pair's h is never read
+        if (publisher) publish();
+        return;
     }
-    // x terms: scale 2^(7 - e), e = exponent of max |x| (scaled maximum in [128, 256))
-    const float mx = fmaxf(fmaxf(s_xmax[1], s_xmax[2]), s_xmax[3]);
+
+    // ---- the wave's gate_up tile: rows row0 .. row0 + 15 of the pair's expert, after its bias
+    const int64_t row0 = (int64_t)kb * 16 * GU_WAVES + 16 * wave;
+    const uint8_t* base = p.pool + slot * L.slot_bytes;
+    const bool hbias = L.gate_bias_off >= 0;
+    const int64_t brow = row0 + (lane & 15);
+    const uint32_t bw = bias_word(base + (hbias ? L.gate_bias_off : 0), L.bias_dtype, hbias ? 2 * (int64_t)I : 0, brow);
+    Tile<MM> tl;
+    tile_load<MM>(tl, base + L.gate_off + (row0 / 16) * p.gu_tile, p.gu_tile,
+                  base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
+    if (publisher) publish();  // while the tile streams in
+
+    // ---- x terms: scale 2^(7 - e), e = exponent of max |x| (scaled maximum in [128, 256))
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XCH; ++i)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(xr[i][d] & 0xFFFFu)), fabsf(bf16_bits_to_f32(xr[i][d] >> 16))));
+    mx = wave_max_u(mx);
     int e = (int)((__float_as_uint(mx) >> 23) & 255u) - 127;
     e = mx > 0.0f ? min(max(e, -100), 100) : 0;
-    if (wave > 0) {
-        const float sc = __uint_as_float((uint32_t)(127 + 7 - e) << 23);
+    const float sc = __uint_as_float((uint32_t)(127 + 7 - e) << 23);
 #pragma unroll
-        for (int i = 0; i < XCH; ++i) {
-            const int c = tid - 64 + 64 * (WAVES - 1) * i;
-            if (c < H / 8) {
-                uint32_t hw[4], lw[4];
+    for (int i = 0; i < XCH; ++i) {
+        const int c = lane + 64 * i;
+        if (c < H / 8) {
+            uint32_t hw[4], lw[4];
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    uint32_t h2, l2;
-                    fp8_terms(bf16_bits_to_f32(xr[i][d] & 0xFFFFu) * sc, bf16_bits_to_f32(xr[i][d] >> 16) * sc, h2, l2);
-                    hw[d] = h2;
-                    lw[d] = l2;
-                }
-                *reinterpret_cast<uint2*>(vec + 8 * c) = uint2{hw[0] | (hw[1] << 16), hw[2] | (hw[3] << 16)};
-                *reinterpret_cast<uint2*>(vec + KP + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
+            for (int d = 0; d < 4; ++d) {
+                uint32_t h2, l2;
+                fp8_terms(bf16_bits_to_f32(xr[i][d] & 0xFFFFu) * sc, bf16_bits_to_f32(xr[i][d] >> 16) * sc, h2, l2);
+                hw[d] = h2;
+                lw[d] = l2;
             }
+            *reinterpret_cast<uint2*>(vec + 8 * c) = uint2{hw[0] | (hw[1] << 16), hw[2] | (hw[3] << 16)};
+            *reinterpret_cast<uint2*>(vec + KP + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
         }
     }
-    __syncthreads();
-    if (!live) return;  // a dead pair's h is never read
+    lds_zero(vec, H, KP, lane, 64);
+    lds_zero(vec + KP, H, KP, lane, 64);
+    lds_zero(zero, 0, KP, lane, 64);
+    wave_lds_sync();
 
-    const uint8_t *a_lo, *a_hi;
-    a_sources(vec, zero, KP, lane, a_lo, a_hi);
-    const float a = tile_dot<MM>(tl, a_lo, a_hi);
-    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane));
     const float x_inv = __uint_as_float((uint32_t)(127 - 7 + e) << 23);
-    const float bias = hbias ? bias_value(braw, L.bias_dtype)[0] : 0.0f;
-    const float tot = (a + __uint_as_float(sw[1])) * x_inv + bias;  // lanes 0..15: row row0 + lane
+    const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
+    const float tot = a * x_inv + bias;  // lanes 0..15: row row0 + lane
     // rows alternate gate, up: lane 2r holds h[row0 / 2 + r]
     const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(tot), 0xB1, 0xF, 0xF, false));
     const float hv = bf16_bits_to_f32(f32_to_bf16_bits(swiglu_oai(L, tot, up))) * p.h_scale;
@@ -353,47 +434,43 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     const bool hbias = L.down_bias_off >= 0;
     const int rounds = (k + WAVES - 1) / WAVES;
 
+    lds_zero(zero, 0, KP, tid, 256);
+    __syncthreads();  // the only barrier before the weighted sum: the waves stream independently
     float yv = 0.0f;  // lanes 0..15: row n0 + lane, this wave's weighted experts
+#pragma unroll 1
     for (int rd = 0; rd < rounds; ++rd) {
         const int j = rd * WAVES + wave;
-        const int64_t slot = j < k ? uniform(p.sel_slot[t * k + j]) : -1;
-        const float w = j < k ? p.sel_w[t * k + j] : 0.0f;
-        const bool live = slot >= 0 && slot < p.n_slots;
-        const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
+        if (j >= k) break;
+        // h(t, j) first, straight into LDS (each term zero-filled to TPB by the buffer
+        // bound; its address needs no routing), then the selection, the bias and the tile:
+        // CHUNKS + MM + 1 buffer loads younger than the transfer
+        const uint8_t* src = p.h + (int64_t)(t * k + j) * 2 * I;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const __amdgpu_buffer_rsrc_t rh =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src + r * I), (short)0, I, 0x00020000);
+#pragma unroll
+            for (int i = 0; i < TPB / 1024; ++i)
+                lds_dma16(rh, (uint32_t)(1024 * i + 16 * lane), hs_lds + (uint32_t)(r * TPB + 1024 * i));
+        }
+        const int64_t slot = uniform(p.sel_slot[t * k + j]);
+        const float w = p.sel_w[t * k + j];
+        if (slot < 0 || slot >= p.n_slots) {  // contributes nothing; the transfer must land before reuse or exit
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            continue;
+        }
+        const uint8_t* base = p.pool + slot * L.slot_bytes;
         Tile<MM> tl;
-        u32x4 braw = u32x4{0u, 0u, 0u, 0u};
-        if (live) {
-            // h(t, j) first, straight into LDS (each term zero-filled to TPB by the buffer
-            // bound), then the bias and the tile: CHUNKS + MM + 1 loads younger than the DMA
-            const uint8_t* src = p.h + (int64_t)(t * k + j) * 2 * I;
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const __amdgpu_buffer_rsrc_t rh =
-                    __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src + r * I), (short)0, I, 0x00020000);
-#pragma unroll
-                for (int i = 0; i < TPB / 1024; ++i)
-                    lds_dma16(rh, (uint32_t)(1024 * i + 16 * lane), hs_lds + (uint32_t)(r * TPB + 1024 * i));
-            }
-            braw = bias_raw(base + (hbias ? L.down_bias_off : 0), L.bias_dtype, hbias ? (int64_t)H : 0,
-                            n0 + (lane & 15));
-            tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
-                          base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
-        }
-        if (rd == 0) {
-            lds_zero(zero, 0, KP, tid, 256);
-            __syncthreads();
-        }
-        if (live) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Tile<MM>::CHUNKS + MM + 1) : "memory");
-            const uint8_t *a_lo, *a_hi;
-            a_sources(hs, zero, TPB, lane, a_lo, a_hi);
-            const float a = tile_dot<MM>(tl, a_lo, a_hi);
-            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-            // used unconditionally (zero without a bias: the load's bound is 0), so the load
-            // stays and the count above holds
-            const float bias = bias_value(braw, L.bias_dtype)[0];
-            yv += w * ((a + __uint_as_float(sw[1])) * p.h_inv + bias);
-        }
+        const int64_t brow = n0 + (lane & 15);
+        const uint32_t bw = bias_word(base + (hbias ? L.down_bias_off : 0), L.bias_dtype, hbias ? (int64_t)H : 0, brow);
+        tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
+                      base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Tile<MM>::CHUNKS + MM + 1) : "memory");
+        const float a = tile_dot<MM>(tl, a_source(hs, zero, TPB, lane));
+        // used unconditionally (zero without a bias: the load's bound is 0), so the load
+        // stays and the count above holds
+        const float bias = bias_word_value(bw, L.bias_dtype, brow);
+        yv += w * (a * p.h_inv + bias);
     }
     if (lane < 16) s_y[wave * 16 + lane] = yv;
     __syncthreads();
@@ -504,11 +581,12 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     p.h_scale = ldexpf(1.0f, 7 - e);
     p.h_inv = ldexpf(1.0f, e - 7);
 
-    const size_t lds_a = MISC_LDS + 3 * 128 * (size_t)ma;
+    const size_t lds_a = GU_MISC + GU_WAVES * 3 * 128 * (size_t)ma;
     const size_t tpb = (128 * (size_t)mb + 1023) / 1024 * 1024;
     const size_t lds_b = MISC_LDS + WAVES * 2 * tpb + 128 * (size_t)mb;
     void* args[] = {&p};
-    TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / 32))), dim3(256), args, lds_a, st));
+    TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / (8 * GU_WAVES)))), dim3(64 * GU_WAVES), args,
+                                  lds_a, st));
     TSA_HIP_CHECK(hipLaunchKernel(kd, dim3((unsigned)(T * (L.hidden / 16))), dim3(256), args, lds_b, st));
     return TSA_OK;
 }

@@ -1,9 +1,10 @@
 // Router top-k: one wave64 per token; up to 16 logits per lane (E <= 1024).
 // Router logits (router_logits_kernel): the MoE block's linear gate ahead of it.
 //
-// Selection is by logit value, descending, ties to the lower expert id; the
-// softmax is monotone in the logits, so the selected set and order equal a top-k
-// over the softmax probabilities (tinyserve/_model_hooks.py:456-473).
+// Selection is by logit value, descending, ties to the lower expert id, NaN ranked
+// above every number (as torch.topk ranks it); the softmax is monotone in the logits, so
+// the selected set and order equal a top-k over the softmax probabilities
+// (tinyserve/_model_hooks.py:456-473) for logits without NaN.
 #include "fused_common.h"
 
 namespace tsa {
@@ -11,8 +12,9 @@ namespace {
 
 constexpr int MAX_PER_LANE = 16;
 
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+// (key, id) pairs: the larger key wins, equal keys go to the lower id.
+__device__ __forceinline__ void argmax_merge(uint32_t& key, int& i, uint32_t okey, int oi) {
+    if (okey > key || (okey == key && oi < i)) { key = okey; i = oi; }
 }
 
 __global__ void __launch_bounds__(256) route_topk_kernel(const void* __restrict__ logits, int ldt, int64_t T, int E,
@@ -42,25 +44,27 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const void* __restrict_
         zsum = wave_sum(s);
         vmax = gmax;
     }
+    // Selection by route_key (NaN first, then descending logit), ties to the lower id. Every
+    // logit's key is above the 0 a lane starts from, so with k <= E each round finds one.
     unsigned taken = 0;  // bit j: element lane + 64 j already selected
     float sel_v = 0.0f;  // lane j < k keeps the j-th selected logit
     int sel_i = 0;
     for (int r = 0; r < k; ++r) {
-        float bv = -INFINITY;
+        uint32_t bk = 0u;
         int bi = 0x7FFFFFFF;
 #pragma unroll
         for (int j = 0; j < MAX_PER_LANE; ++j) {
             const int e = lane + 64 * j;
-            if (e < E && !((taken >> j) & 1u)) argmax_merge(bv, bi, v[j], e);
+            if (e < E && !((taken >> j) & 1u)) argmax_merge(bk, bi, route_key(v[j]), e);
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
+            const uint32_t ok = (uint32_t)__shfl_xor((int)bk, off, 64);
             const int oi = __shfl_xor(bi, off, 64);
-            argmax_merge(bv, bi, ov, oi);
+            argmax_merge(bk, bi, ok, oi);
         }
         if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == r) { sel_v = bv; sel_i = bi; }
+        if (lane == r) { sel_v = route_key_value(bk); sel_i = bi; }
     }
     // weights
     float wgt;
