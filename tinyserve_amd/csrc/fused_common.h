@@ -171,20 +171,22 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// Top-k selection over NV logits per lane (expert e = lane + 64 j), k <= 16, in k rounds:
+// Top-k selection over NV logits per lane (expert e = lane + 64 j), k <= 16, in rounds:
 // each takes the largest remaining key with a DPP wave max, its lowest expert id among
 // equal keys with ballots, and removes it (key 0, below the key of every logit). The
-// selections come out in rank order: NaN first, then descending logit, ties to the lower id. Lane r < k ends with the key, id and slot (es) of the r-th selection.
+// selections come out in rank order: NaN first, then descending logit, ties to the lower id.
+// Lane r < nr ends with the key, id and slot (es) of the r-th selection; nr <= k rounds run
+// (a caller that needs only the r-th selection stops after round r).
 template <int NV, class P>
-__device__ void route_select(const P& p, int lane, const float v[4], const int es[4], uint32_t& myk, int& mysel,
-                             int& myslot) {
+__device__ void route_select(const P& p, int lane, const float v[4], const int es[4], int nr, uint32_t& myk,
+                             int& mysel, int& myslot) {
     uint32_t key[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) key[j] = lane + 64 * j < p.E ? route_key(v[j]) : 0u;
     myk = 0u;
     mysel = -1;
     myslot = -1;
-    for (int r = 0; r < p.k; ++r) {
+    for (int r = 0; r < nr; ++r) {
         uint32_t m = key[0];
 #pragma unroll
         for (int j = 1; j < NV; ++j) m = max(m, key[j]);
@@ -222,10 +224,10 @@ __device__ int route_token_v(const P& p, int t, int lane, const float v[4], cons
     uint32_t myk;
     int mysel, myslot;
     switch ((p.E + 63) >> 6) {
-        case 1: route_select<1>(p, lane, v, es, myk, mysel, myslot); break;
-        case 2: route_select<2>(p, lane, v, es, myk, mysel, myslot); break;
-        case 3: route_select<3>(p, lane, v, es, myk, mysel, myslot); break;
-        default: route_select<4>(p, lane, v, es, myk, mysel, myslot); break;
+        case 1: route_select<1>(p, lane, v, es, p.k, myk, mysel, myslot); break;
+        case 2: route_select<2>(p, lane, v, es, p.k, myk, mysel, myslot); break;
+        case 3: route_select<3>(p, lane, v, es, p.k, myk, mysel, myslot); break;
+        default: route_select<4>(p, lane, v, es, p.k, myk, mysel, myslot); break;
     }
     if (lane < p.k) s_slot[t * p.k + lane] = myslot;
     const float myval = route_key_value(myk);  // lane r < k: the r-th selected logit

@@ -47,6 +47,7 @@ constexpr int WAVES = 4;
 constexpr int MISC_LDS = 1024;  // slot/weight tables, per-wave maxima and rows
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 struct MxtParams {
     tsa_expert_layout L;
@@ -218,56 +219,20 @@ __device__ __forceinline__ void lds_zero(uint8_t* a, int from, int to, int me, i
 
 constexpr int GU_WAVES = 2;        // waves per gate_up workgroup (one 16-row tile each)
 constexpr int XCH = 3072 / 8 / 64;  // x chunks (8 values) per lane when a wave loads all of x (H <= 3072)
-constexpr int GU_MISC = 512 * GU_WAVES;  // per wave: the routing scratch (64 composite keys)
 
-__device__ __forceinline__ void wave_lds_sync() {  // this wave's LDS writes before its later reads
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// The token's top-k selection within one wave: lane r < k ends with the key, expert id and
-// slot of the r-th selection (rank order: NaN first, then descending logit, ties to the
-// lower id). lg / es: the token's logits and slot table as load4 lays them out. E <= 64:
-// lane e ranks expert e by counting the composite keys (route_key << 32 | ~id, unique) that
-// beat its own, read back from the wave's scratch kl (64 x 8 bytes), then the selection is
-// put in rank order through the same scratch; larger E: k rounds of route_select.
+// The token's first nr selections within one wave (route_select: rounds of a DPP wave max):
+// lane r < nr ends with the key, expert id and slot of the r-th selection (NaN first, then
+// descending logit, ties to the lower id). lg / es: the token's logits and slot table as
+// load4 lays them out.
 template <class P>
-__device__ void select_topk(const P& p, int lane, const float lg[4], const int es[4], uint64_t* kl, uint32_t& myk,
-                            int& mysel, int& myslot) {
-    if (p.E > 64) {
-        switch ((p.E + 63) >> 6) {
-            case 2: route_select<2>(p, lane, lg, es, myk, mysel, myslot); break;
-            case 3: route_select<3>(p, lane, lg, es, myk, mysel, myslot); break;
-            default: route_select<4>(p, lane, lg, es, myk, mysel, myslot); break;
-        }
-        return;
+__device__ __forceinline__ void select_topk(const P& p, int lane, const float lg[4], const int es[4], int nr,
+                                            uint32_t& myk, int& mysel, int& myslot) {
+    switch ((p.E + 63) >> 6) {
+        case 1: route_select<1>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        case 2: route_select<2>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        case 3: route_select<3>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        default: route_select<4>(p, lane, lg, es, nr, myk, mysel, myslot); break;
     }
-    const uint32_t key = lane < p.E ? route_key(lg[0]) : 0u;
-    const uint64_t mine = ((uint64_t)key << 32) | (uint32_t)~lane;
-    kl[lane] = lane < p.E ? mine : 0ull;  // padding never beats a logit's key
-    wave_lds_sync();
-    int rank = 0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        if (16 * g >= p.E) break;
-        uint64_t kk[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) kk[i] = kl[16 * g + i];  // issued together, one wait
-#pragma unroll
-        for (int i = 0; i < 16; ++i) rank += kk[i] > mine ? 1 : 0;
-    }
-    wave_lds_sync();
-    uint32_t* ks = reinterpret_cast<uint32_t*>(kl);  // [0, 16) keys, [16, 32) ids, [32, 48) slots
-    if (lane < p.E && rank < p.k) {
-        ks[rank] = key;
-        ks[16 + rank] = (uint32_t)lane;
-        ks[32 + rank] = (uint32_t)es[0];
-    }
-    wave_lds_sync();
-    myk = lane < p.k ? ks[lane] : 0u;
-    mysel = lane < p.k ? (int)ks[16 + lane] : -1;
-    myslot = lane < p.k ? (int)ks[32 + lane] : -1;
 }
 
 // ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h terms to the workspace.
@@ -276,9 +241,10 @@ __device__ void select_topk(const P& p, int lane, const float lg[4], const int e
 // 720 workgroups spread over the 256 CUs more evenly than 360 four-wave ones would, which
 // shortens the weight stream (measured 6.2 against 6.8 us for the stream alone).
 //
-// The waves share nothing and never wait for each other: each selects the token's experts
-// itself, issues its tile's loads as soon as it knows the slot, and builds its own copy of
-// the x terms (max |x| over all of x, conversion, zero padding) in the shadow of those loads.
+// Each wave selects the token's experts itself and issues its tile's loads as soon as it
+// knows the slot. Each wave also loads all of x (so its max needs no exchange); in the
+// shadow of the tile loads the two waves convert one half of x each into the shared terms
+// and meet at the workgroup's only barrier before the dot.
 template <int MM>
 __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -288,8 +254,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int pairs = p.T * k;
     const int kb = (int)blockIdx.x / pairs, pr = (int)blockIdx.x % pairs, t = pr / k, jj = pr % k;
-    uint64_t* kl = reinterpret_cast<uint64_t*>(smem + 512 * wave);  // this wave's routing scratch
-    uint8_t* vec = smem + GU_MISC + wave * 3 * KP;  // this wave's x terms [2][KP], then a zero area [KP]
+    uint8_t* vec = smem;  // x terms [2][KP], then a zero area [KP]
     uint8_t* zero = vec + 2 * KP;
     const bool routed = p.logits != nullptr;
 
@@ -310,15 +275,16 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
 #pragma unroll
         for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
         load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
-        select_topk(p, lane, lg, es, kl, myk, mysel, myslot);
+        select_topk(p, lane, lg, es, jj + 1, myk, mysel, myslot);  // the pair's selection is round jj
         slot = __builtin_amdgcn_readlane(myslot, jj);
     } else {
         slot = uniform(p.sel_slot[pr]);
     }
 
-    // the token's first workgroup publishes the selection: softmax over the k selected
-    // logits, or (unnormalised mode) over all E
+    // the token's first workgroup publishes the selection (all k rounds): softmax over the k
+    // selected logits, or (unnormalised mode) over all E
     auto publish = [&]() {
+        select_topk(p, lane, lg, es, k, myk, mysel, myslot);
         const float myval = route_key_value(myk);
         const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));
         float w;
@@ -360,21 +326,22 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
                   base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
     if (publisher) publish();  // while the tile streams in
 
-    // ---- x terms: scale 2^(7 - e), e = exponent of max |x| (scaled maximum in [128, 256))
-    float mx = 0.0f;
+    // ---- x terms: scale 2^(7 - e), e = exponent of max |x| (scaled maximum in [128, 256)).
+    // The max over magnitude bits: for non-negative floats the integer order is the float
+    // order (v_pk_max_u16, two values per instruction).
+    us2 mb = us2{0, 0};
 #pragma unroll
     for (int i = 0; i < XCH; ++i)
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-            mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(xr[i][d] & 0xFFFFu)), fabsf(bf16_bits_to_f32(xr[i][d] >> 16))));
-    mx = wave_max_u(mx);
+        for (int d = 0; d < 4; ++d) mb = __builtin_elementwise_max(mb, __builtin_bit_cast(us2, xr[i][d] & 0x7FFF7FFFu));
+    const float mx = wave_max_u(bf16_bits_to_f32(mb[0] > mb[1] ? mb[0] : mb[1]));
     int e = (int)((__float_as_uint(mx) >> 23) & 255u) - 127;
     e = mx > 0.0f ? min(max(e, -100), 100) : 0;
     const float sc = __uint_as_float((uint32_t)(127 + 7 - e) << 23);
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
         const int c = lane + 64 * i;
-        if (c < H / 8) {
+        if (i % GU_WAVES == wave && c < H / 8) {  // this wave's half
             uint32_t hw[4], lw[4];
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
@@ -387,10 +354,10 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
             *reinterpret_cast<uint2*>(vec + KP + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
         }
     }
-    lds_zero(vec, H, KP, lane, 64);
-    lds_zero(vec + KP, H, KP, lane, 64);
-    lds_zero(zero, 0, KP, lane, 64);
-    wave_lds_sync();
+    lds_zero(vec, H, KP, tid, 64 * GU_WAVES);
+    lds_zero(vec + KP, H, KP, tid, 64 * GU_WAVES);
+    lds_zero(zero, 0, KP, tid, 64 * GU_WAVES);
+    __syncthreads();  // every pair is live or dead for both waves: both get here or neither
 
     const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane));
     const float x_inv = __uint_as_float((uint32_t)(127 - 7 + e) << 23);
@@ -581,7 +548,7 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     p.h_scale = ldexpf(1.0f, 7 - e);
     p.h_inv = ldexpf(1.0f, e - 7);
 
-    const size_t lds_a = GU_MISC + GU_WAVES * 3 * 128 * (size_t)ma;
+    const size_t lds_a = 3 * 128 * (size_t)ma;
     const size_t tpb = (128 * (size_t)mb + 1023) / 1024 * 1024;
     const size_t lds_b = MISC_LDS + WAVES * 2 * tpb + 128 * (size_t)mb;
     void* args[] = {&p};
