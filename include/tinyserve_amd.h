@@ -148,8 +148,8 @@ int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, in
  *   y[t] = sum_j weights[t, j] * FFN(pool + slots[t, j] * slot_bytes, x[t]),
  * skipping slots < 0 (they contribute zero). slots [T, k] int32 and weights [T, k] f32
  * stay on the device (no host sync). y is overwritten. The workspace
- * (tsa_moe_decode_workspace_size bytes) must be zero-filled once before its first use;
- * calls leave it reusable. Calls that share a workspace must be ordered (one stream).
+ * (tsa_moe_decode_workspace_size bytes) needs no initialisation: no kernel keeps state in
+ * it from one call to the next. Calls that share a workspace must be ordered (one stream).
  * Replaces fast_expert_forward (tinyserve/csrc/expert_loop.cpp:41-123) and the per-expert
  * loops of ExpertPipeline._execute_layer_experts_native / _forward_cache_hits
  * (tinyserve/expert_pipeline.py:241-285,416-496) over GGMLExpertForward
@@ -163,8 +163,8 @@ int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool, int64_t n_
 /* Router + fused top-k expert FFN in one call: routes logits [T, E] (mode as in
  * tsa_route_topk), maps expert ids to slots through expert_slot [E] (-1: not resident,
  * contributes zero) and computes y as tsa_moe_decode does. idx_out [T, k] / w_out [T, k]
- * (optional, may be NULL) receive the routing. For MXFP4 experts with T <= 4 this is a
- * single kernel launch with no host sync.
+ * (optional, may be NULL) receive the routing. For MXFP4 experts with T <= 4 and E <= 256
+ * this is two kernel launches (routing inside both) with no host sync.
  * Replaces the route closure + execute_layer_experts pair of the MoE hook
  * (tinyserve/_model_hooks.py:524-564, tinyserve/expert_pipeline.py:140-164). */
 int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
