@@ -172,6 +172,18 @@ int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int
                           int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
                           int32_t* idx_out, float* w_out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* tsa_moe_decode_routed without the workspace argument: it allocates nothing (no hipMalloc,
+ * no allocating library call) and works in a device array of 8 MiB per GPU that the library
+ * holds until the process ends; calls whose workspace would exceed it (see
+ * tsa_moe_decode_workspace_size) return TSA_ERR_WORKSPACE. All calls on one GPU share that
+ * array, so calls that overlap on one GPU race: order them on one stream.
+ * No counterpart in the reference. For callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation. */
+int tsa_moe_decode_routed_noalloc(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                                  const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype,
+                                  int mode, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                                  int32_t* idx_out, float* w_out, void* stream);
+
 /* Expert-major grouping of the (token, j) assignments idx [T, k] (int32 expert ids in
  * [0, E), ids < 0 ignored): counts [E], offsets [E+1] (exclusive scan), perm [T*k]
  * holding t*k + j, token-major within each expert.

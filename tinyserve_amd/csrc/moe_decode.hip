@@ -13,6 +13,8 @@
 // (weighted top-k accumulation).
 #include "rowdot.h"
 
+#include <mutex>
+
 namespace tsa {
 namespace {
 
@@ -458,4 +460,54 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
         return tiled_decode(L, pl, n_slots, slots, w, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype, y,
                             y_dtype, ws, workspace_bytes, st);
     return two_launch_decode(L, pl, n_slots, slots, w, T, k, x, x_dtype, y, y_dtype, ws, st);
+}
+
+// ---- allocation-free routed decode: the workspace is a file-scope device array, one per
+// GPU (held until the process ends), whose address is looked up once per device with that
+// device current. Calls on one GPU share it, so calls that overlap on one GPU race (order
+// them on one stream); every call fully rewrites what it reads, so nothing needs clearing.
+static constexpr int64_t kNoAllocScratchBytes = 8ll << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's copy of `scratch` (device address).
+int scratch_for_current_device(uint8_t** out) {
+    int dev = -1;
+    TSA_HIP_CHECK(hipGetDevice(&dev));
+    TSA_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, TSA_ERR_INVALID_ARG, "device %d is beyond the scratch table", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        TSA_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        TSA_REQUIRE(ptr != nullptr, TSA_ERR_HIP, "no device address for the decode scratch");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+    return TSA_OK;
+}
+}  // namespace
+
+extern "C" int tsa_moe_decode_routed_noalloc(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                                             const int32_t* expert_slot, int64_t E, const void* logits,
+                                             int logits_dtype, int mode, int64_t T, int k, const void* x, int x_dtype,
+                                             void* y, int y_dtype, int32_t* idx_out, float* w_out, void* stream) {
+    clear_error();
+    int rc = validate_layout(layout);
+    if (rc) return rc;
+    TSA_REQUIRE(T >= 0 && k >= 1 && k <= 64, TSA_ERR_SHAPE, "bad T (%lld) / k (%d)", (long long)T, k);
+    if (T == 0) return TSA_OK;
+    const int64_t need = ws_bytes(*layout, T, k);
+    TSA_REQUIRE(need <= kNoAllocScratchBytes, TSA_ERR_WORKSPACE,
+                "the allocation-free decode has %lld scratch bytes per device; T %lld x top-%d needs %lld "
+                "(use tsa_moe_decode_routed with a workspace)",
+                (long long)kNoAllocScratchBytes, (long long)T, k, (long long)need);
+    uint8_t* ws = nullptr;
+    rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+    return tsa_moe_decode_routed(layout, pool, n_slots, expert_slot, E, logits, logits_dtype, mode, T, k, x, x_dtype, y,
+                                 y_dtype, idx_out, w_out, ws, kNoAllocScratchBytes, stream);
 }
