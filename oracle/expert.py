@@ -33,7 +33,8 @@ SWIGLU_ALPHA = 1.702
 
 
 def sigmoid(x: np.ndarray) -> np.ndarray:
-    return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+    with np.errstate(over="ignore"):  # exp(-x) -> inf for very negative x gives the exact limit 0
+        return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
 
 
 def gptoss_swiglu(gu: np.ndarray, limit: float = SWIGLU_LIMIT, alpha: float = SWIGLU_ALPHA) -> np.ndarray:

@@ -1,0 +1,208 @@
+"""``ExpertPipeline`` over an all-resident expert cache, and the MoE block hook.
+
+Keeps tinyserve/expert_pipeline.py's constructor, ``ExpertPipeline(store, template, device,
+staging_buffer_a, staging_buffer_b, transfer_stream, compute_stream, cache=None,
+shared_stream=None, ram_cache=None, cpu_expert=None, max_top_k=8)`` (:58-138), and its two
+entry points, ``execute_layer_experts(hidden_states, layer_idx, expert_indices,
+routing_weights)`` (decode, :140-164) and ``execute_layer_experts_batched(...)`` (prefill,
+:166-239), plus the attributes the reference's ExpertBatcher reads (``store``,
+``template``, ``cache``, ``staging_buffer_a``, ``_inline_fwd``, ``_param_refs``).
+
+What differs is the mechanism. The reference double-buffers PCIe transfers into an LRU pool
+sized for a small card and loops over experts in Python (with ``.tolist()`` host syncs).
+One MI355X holds every expert of the target models in its 288 GB, so the first time a
+layer runs all its experts are copied into the cache (``ensure_resident``); from then on a
+decode layer is one ``tsa_moe_decode`` call and a prefill layer one ``tsa_moe_prefill``
+call over the cache's slot pool, with the expert -> slot lookup done on the device.
+``execute_layer_logits`` goes from router logits to the weighted sum in one
+``tsa_moe_decode_routed`` call (the routing runs inside the decode kernels).
+
+``install_offloaded_forward`` replaces a MoE block's forward as the reference's hook does
+(tinyserve/_model_hooks.py:479-568): the block's router linear, then the experts through
+the pipeline, with the block's shared expert (if any) on ``pipeline.shared_stream`` joined
+by an event.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .expert_cache import ExpertCache
+from .expert_forward import (_build_cpp_layout_args, _build_gpu_int4_forward, _build_inline_forward,
+                             _build_mxfp4_inline_forward, _precompute_param_refs)
+
+
+class ExpertPipeline:
+    def __init__(self, store, template: nn.Module | None = None, device="cuda", staging_buffer_a=None,
+                 staging_buffer_b=None, transfer_stream=None, compute_stream=None, cache: ExpertCache | None = None,
+                 shared_stream=None, ram_cache=None, cpu_expert=None, max_top_k: int = 8):
+        self.store = store
+        self.template = template
+        self.device = torch.device(device)
+        self.staging_buffer_a = staging_buffer_a if staging_buffer_a is not None else store.allocate_buffer(self.device)
+        self.staging_buffer_b = staging_buffer_b
+        self.transfer_stream = transfer_stream
+        self.compute_stream = compute_stream
+        self.ram_cache = ram_cache
+        self.cpu_expert = cpu_expert
+        self.max_top_k = max_top_k
+        self.cache_bias = 0.0
+        self.profiler = None
+        if cache is None:  # room for every expert of every layer
+            n = store.num_layers * store.num_experts
+            cache = ExpertCache(n, store.expert_bytes, self.device, num_layers=max(self._layer_ids()) + 1,
+                                num_experts=store.num_experts)
+        self.cache = cache
+        self.shared_stream = shared_stream if shared_stream is not None else (
+            torch.cuda.Stream(self.device) if self.device.type == "cuda" else None)
+        self._native_quant = hasattr(store, "ggml_types")
+        if self._native_quant:
+            from .ggml_forward import GGMLExpertForward
+
+            self._act_fn = nn.SiLU()
+            self._nq_forward = GGMLExpertForward(store.layout, store.ggml_types, self._act_fn,
+                                                 getattr(store, "proj_shapes", {}))
+            self._param_refs = None
+            self._inline_fwd = None
+            self._cpp_layout_args = None
+        else:
+            self._act_fn = getattr(template, "_act_fn", None)
+            self._param_refs = _precompute_param_refs(template, store.layout) if template is not None else None
+            self._inline_fwd = (_build_inline_forward(store.layout, self._act_fn)
+                                or _build_mxfp4_inline_forward(store.layout, self._act_fn)
+                                or _build_gpu_int4_forward(store.layout, self._act_fn))
+            self._cpp_layout_args = _build_cpp_layout_args(store.layout, self._act_fn)
+        self._kernel_layouts: dict[int, object] = {}
+        self._decode_ws: dict[tuple, torch.Tensor] = {}
+
+    def _layer_ids(self) -> list[int]:
+        """The layer_idx values the store answers to: a GGUF store's block numbers, else
+        0 .. num_layers - 1 (ExpertStore indexes its layers by position)."""
+        layers = getattr(self.store, "layers", None)
+        return list(layers) if layers else list(range(self.store.num_layers))
+
+    # ---- residency and layouts
+    def kernel_layout(self, layer_idx: int):
+        """The kernels' tsa_expert_layout of this layer's slots (GGUF layers may differ in type)."""
+        L = self._kernel_layouts.get(layer_idx)
+        if L is None:
+            if self._native_quant:
+                L = self.store.expert_layout(layer_idx)
+            else:
+                L = self.store.expert_layout(self._act_fn)
+            self._kernel_layouts[layer_idx] = L
+        return L
+
+    def ensure_resident(self, layer_idx: int) -> None:
+        """Copy every expert of the layer that has no slot yet into the cache (host work on
+        the first call for a layer only; afterwards a check of the host slot map)."""
+        E = self.store.num_experts
+        cache = self.cache
+        if cache.layer_resident(layer_idx, E):
+            return
+        for e in range(E):
+            if not cache.contains(layer_idx, e):
+                slot = cache.allocate(layer_idx, e)
+                self.store.copy_to_buffer_slot(cache, slot, layer_idx, e)
+        cache.flush_slot_updates()
+
+    def _workspace(self, L, T: int, k: int) -> torch.Tensor:
+        key = (int(L.hidden), int(L.inter), int(L.format), T, k)
+        ws = self._decode_ws.get(key)
+        if ws is None:
+            ws = self._decode_ws[key] = ops.moe_decode_workspace(L, T, k, self.device)
+        return ws
+
+    # ---- the reference's entry points
+    def execute_layer_experts(self, hidden_states: torch.Tensor, layer_idx: int, expert_indices: torch.Tensor,
+                              routing_weights: torch.Tensor) -> torch.Tensor:
+        """sum_j w[t, j] * expert_{idx[t, j]}(h[t]) for every token; one fused decode call."""
+        self.ensure_resident(layer_idx)
+        L = self.kernel_layout(layer_idx)
+        h = hidden_states.reshape(-1, L.hidden)
+        T = h.shape[0]
+        idx = expert_indices.reshape(T, -1)
+        k = idx.shape[1]
+        slots = self.cache.lookup_slots(layer_idx, idx)
+        w = routing_weights.reshape(T, k).to(torch.float32)
+        y = ops.moe_decode(L, self.cache._packed, slots, w, h, workspace=self._workspace(L, T, k))
+        return y.view(hidden_states.shape)
+
+    def execute_layer_experts_batched(self, hidden_states: torch.Tensor, layer_idx: int,
+                                      expert_indices: torch.Tensor, routing_weights: torch.Tensor) -> torch.Tensor:
+        """The same sum for a prefill batch: one grouped tsa_moe_prefill call."""
+        self.ensure_resident(layer_idx)
+        L = self.kernel_layout(layer_idx)
+        h = hidden_states.reshape(-1, L.hidden)
+        T = h.shape[0]
+        if T == 0:
+            return hidden_states.clone()
+        idx = expert_indices.reshape(T, -1).to(torch.int32)
+        w = routing_weights.reshape(T, -1).to(torch.float32)
+        y = ops.moe_prefill(L, self.cache._packed, self.cache.expert_slot(layer_idx), idx, w, h)
+        return y.to(hidden_states.dtype).view(hidden_states.shape)
+
+    def execute_layer_logits(self, hidden_states: torch.Tensor, layer_idx: int, router_logits: torch.Tensor,
+                             top_k: int, mode: str = "topk_then_softmax", return_routing: bool = False):
+        """Router logits [T, E] -> the weighted expert sum in one routed decode call."""
+        self.ensure_resident(layer_idx)
+        L = self.kernel_layout(layer_idx)
+        h = hidden_states.reshape(-1, L.hidden)
+        T = h.shape[0]
+        res = ops.moe_decode_routed(L, self.cache._packed, self.cache.expert_slot(layer_idx),
+                                    router_logits.reshape(T, -1), h, top_k, mode,
+                                    workspace=self._workspace(L, T, top_k), return_routing=return_routing)
+        if return_routing:
+            y, idx, w = res
+            return y.view(hidden_states.shape), idx, w
+        return res.view(hidden_states.shape)
+
+
+_ROUTE_ORDERS = {"topk_then_softmax": "topk_then_softmax", "softmax_then_topk": "softmax_then_topk"}
+
+
+def install_offloaded_forward(moe_block: nn.Module, pipeline: ExpertPipeline, layer_idx: int, router_attr: str,
+                              top_k: int, returns_router_logits: bool = False,
+                              softmax_order: str = "topk_then_softmax", routed_decode_tokens: int = 4) -> None:
+    """Replace ``moe_block.forward`` (tinyserve/_model_hooks.py:479-568): router linear
+    (``getattr(moe_block, router_attr)``), then for up to ``routed_decode_tokens`` tokens one
+    routed decode call (routing inside the kernels), for longer inputs the device router
+    plus one batched prefill call; the block's ``shared_experts`` / ``shared_expert`` runs
+    on ``pipeline.shared_stream`` and is joined with an event. ``softmax_order``:
+    ``"topk_then_softmax"`` (GPT-OSS) or ``"softmax_then_topk"`` (renormalised, Qwen3-MoE)."""
+    if softmax_order not in _ROUTE_ORDERS:
+        raise ValueError(f"unsupported softmax_order {softmax_order!r}")
+    mode = _ROUTE_ORDERS[softmax_order]
+    router = getattr(moe_block, router_attr)
+    shared = getattr(moe_block, "shared_experts", None) or getattr(moe_block, "shared_expert", None)
+
+    def offloaded_forward(hidden_states: torch.Tensor, **_kwargs):
+        hidden = hidden_states.shape[-1]
+        flat = hidden_states.reshape(-1, hidden)
+        shared_out = shared_event = None
+        main = torch.cuda.current_stream(flat.device)
+        if shared is not None:
+            side = pipeline.shared_stream
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                shared_out = shared(flat)
+                shared_event = torch.cuda.Event()
+                shared_event.record(side)
+            # tensors crossing streams: keep their memory until both streams are done with it
+            flat.record_stream(side)
+            shared_out.record_stream(main)
+        logits = router(flat)
+        if flat.shape[0] <= routed_decode_tokens:
+            out = pipeline.execute_layer_logits(flat, layer_idx, logits, top_k, mode)
+        else:
+            idx, w = ops.route_topk(logits.float(), top_k, mode)
+            out = pipeline.execute_layer_experts_batched(flat, layer_idx, idx, w)
+        out = out.to(flat.dtype)
+        if shared_event is not None:
+            main.wait_event(shared_event)
+            out = out + shared_out
+        out = out.view(hidden_states.shape)
+        return (out, logits) if returns_router_logits else out
+
+    moe_block.forward = offloaded_forward
