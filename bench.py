@@ -73,35 +73,48 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
     return rows
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str, kernel_key: str, workload: int, command: str) -> dict:
-    """Calibrated HBM bytes per launch of the kernel whose name contains kernel_key."""
-    out = {"workload": workload, "kernel": kernel_key, "command": command}
+# The kernels of one step of each decode workload (name substrings; "3c" = workload 3 with
+# the experts in checkpoint order).
+STEP_KERNELS = {"1": ("gq_matvec_kernel",), "2": ("gq_phase_a", "gq_phase_b"),
+                "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
+                "4": ("gq_phase_a", "gq_phase_b")}
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str, key: str, command: str) -> dict:
+    """Calibrated HBM bytes per step: for every kernel of the step (each distinct kernel
+    name matching STEP_KERNELS[key]) the mean counter value per dispatch, summed."""
+    out = {"workload": key, "kernels": {}, "command": command}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _pmc_rows(d, counter)
         copy = [v for k, v in rows if "MulFunctor" in k]  # torch.mul's elementwise kernel
-        kern = [v for k, v in rows if kernel_key in k]
-        if not copy or not kern:
-            raise SystemExit(f"{counter}: no calibration copy ({len(copy)}) or {kernel_key} ({len(kern)}) dispatches in {d}")
+        names = sorted({k for k, _ in rows if any(s in k for s in STEP_KERNELS[key])})
+        if not copy or not names:
+            raise SystemExit(f"{counter}: no calibration copy ({len(copy)}) or step kernels ({names}) in {d}")
         copy_kib = max(copy)  # the 256 MiB copy is the largest elementwise dispatch
         factor = copy_kib * 1024.0 / (4.0 * COPY_ELEMS)
-        out[counter] = {"kib_per_dispatch": float(np.mean(kern)), "dispatches": len(kern),
-                        "copy_kib": copy_kib, "copy_factor": factor,
-                        "bytes_per_launch": float(np.mean(kern)) * 1024.0 / factor}
-    out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+        per = {}
+        for n in names:
+            vals = [v for k, v in rows if k == n]
+            per[n] = {"kib_per_dispatch": float(np.mean(vals)), "dispatches": len(vals),
+                      "bytes_per_dispatch": float(np.mean(vals)) * 1024.0 / factor}
+            out["kernels"].setdefault(n, {})[counter] = per[n]
+        out[counter] = {"copy_kib": copy_kib, "copy_factor": factor,
+                        "bytes_per_step": sum(v["bytes_per_dispatch"] for v in per.values())}
+    out["traffic_bytes_per_step"] = out["FETCH_SIZE"]["bytes_per_step"] + out["WRITE_SIZE"]["bytes_per_step"]
     return out
 
 
-def load_traffic(workload: int, kernel_key: str):
+def _read_traffic() -> dict:
     try:
-        import json as _json
-
         with open(TRAFFIC_FILE) as fh:
-            t = _json.load(fh)
-        if t.get("workload") == workload and t.get("kernel") == kernel_key:
-            return t
+            t = json.load(fh)
+        return t if isinstance(t, dict) and "workloads" in t else {"workloads": {}}
     except (OSError, ValueError):
-        pass
-    return None
+        return {"workloads": {}}
+
+
+def load_traffic(key: str):
+    return _read_traffic()["workloads"].get(key)
 
 
 def _bf16(bits: np.ndarray, dev) -> torch.Tensor:
@@ -238,36 +251,6 @@ class GgufWorkload:
                                           st))
 
 
-def cpu_baseline_gguf(wl_id: int, budget_s: float = 12.0) -> dict:
-    """The oracle's workload 1 / 2 path (numpy dequant of the whole matrix or expert, then
-    fp32 matvec: the CPU restatement of gguf_dequant_torch + F.linear) on this host."""
-    from threadpoolctl import threadpool_info
-
-    from oracle import expert as oex
-    from oracle import gguf as og
-
-    wl = synth.workload(wl_id)
-    if wl_id == 1:
-        x = wl["x"].reshape(1, -1)
-        fn = lambda: x @ og.dequant_tensor(wl["w"], 8, (wl["N"], wl["K"])).T  # noqa: E731
-        nbytes = wl["w"].size + 2 * 4 * wl["K"]
-    else:
-        x = synth.bf16_to_f32(wl["x_bits"]).reshape(1, -1)
-        fn = lambda: oex.gguf_expert_forward(x, wl["expert"])  # noqa: E731
-        nbytes = wl["layout"].total_bytes + 2 * 2 * wl["hidden"]
-    fn()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
-            "sample": f"{len(times)} calls of workload {wl_id} (median {med * 1e3:.1f} ms; numpy dequant + fp32 BLAS)"}
-
-
 class PrefillWorkload:
     """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
     2048-token prefill; one step = one layer's whole batched MoE."""
@@ -311,34 +294,6 @@ class PrefillWorkload:
             _lib.BF16, self.ws.data_ptr(), self.ws.numel(), st))
 
 
-def cpu_baseline_prefill(budget_s: float = 15.0) -> dict:
-    """The oracle's grouped prefill (per expert: numpy dequant of its weights, fp32 BLAS
-    matmuls over its tokens, weighted scatter) on a bounded sample of the workload's
-    tokens, as TFLOP/s."""
-    from threadpoolctl import threadpool_info
-
-    from oracle import expert as oex
-
-    wl = synth.workload(5)
-    idx, w = oex.route_topk_then_softmax(wl["logits"], wl["top_k"])
-    H, I = wl["hidden"], wl["inter"]
-    n_tok = 128
-    x = synth.bf16_to_f32(wl["x_bits"][:n_tok])
-    fwd = lambda e, xx: oex.mxfp4_expert_forward(xx, wl["experts"][e])  # noqa: E731
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 2:
-        t0 = time.perf_counter()
-        oex.moe_combine_grouped(x, idx[:n_tok], w[:n_tok], fwd)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    flops = 2 * n_tok * wl["top_k"] * 3 * H * I
-    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"{len(times)} grouped prefills of the first {n_tok} of the workload's tokens (median "
-                      f"{med * 1e3:.0f} ms; numpy dequant of each routed expert + fp32 BLAS matmuls)"}
-
-
 def run_prefill(args, dev) -> int:
     wl = PrefillWorkload(args.layers_prefill, dev)
     K, W = args.steps, args.warmup
@@ -377,42 +332,105 @@ def run_prefill(args, dev) -> int:
                      "note": "whole step (routing, grouping, both GEMMs, combine) per HIP-event time"},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_prefill()
+        line["cpu_baseline"] = cpu_baseline(5)
     print(json.dumps(line))
     return 0
 
 
-def cpu_baseline(wl_id: int, budget_s: float = 12.0) -> dict:
-    """The oracle (numpy restatement of the reference CPU path: full dequant of the
-    selected experts, then fp32 matmuls) timed on this host, one token of one layer."""
-    from threadpoolctl import threadpool_info
+def _cpu_host() -> tuple[int, str]:
+    """Threads for torch = the cores this process may run on; the CPU model name."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, model
 
+
+def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: float = 10.0) -> dict:
+    """The reference's CPU path restated in torch (oracle.torch_cpu: whole-tensor vectorised
+    dequant, then fp32 matmuls), timed on this host's cores: the median of >= min_runs runs
+    after `warmup`, dequant and matmul timed separately. Workloads 1-4 time one decode step
+    (router top-k, then the selected experts); workload 5 a grouped prefill of a token
+    sample. The routing itself (numpy top-k over the step's logits) is outside the timing."""
     from oracle import expert as oex
+    from oracle import torch_cpu as otc
 
+    cores, model = _cpu_host()
     wl = synth.workload(wl_id)
-    logits = wl["logits"][:1]
-    x = synth.bf16_to_f32(wl["x_bits"][:1])
-    if wl_id == 3:
-        idx, w = oex.route_topk_then_softmax(logits, wl["top_k"])
-        fwd = lambda e, xx: oex.mxfp4_expert_forward(xx, wl["experts"][e])  # noqa: E731
-        per_expert = wl["layout"].total_bytes
+    if wl_id == 1:
+        x = torch.from_numpy(wl["x"]).reshape(1, -1)
+        w = otc.as_u8(wl["w"])
+        dequant = lambda: otc.gguf_dequant(w, 8, (wl["N"], wl["K"]))  # noqa: E731
+        matmul = lambda W: x @ W.T  # noqa: E731
+        work, unit, what = wl["w"].size + 2 * 4 * wl["K"], "GB/s", "Q8_0 2880 x 2880 matvecs"
+    elif wl_id == 2:
+        x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"])).reshape(1, -1)
+        e = otc.torch_expert(wl["expert"])
+        dequant = lambda: otc.gguf_expert_weights(e)  # noqa: E731
+        matmul = lambda W: otc.gguf_expert_ffn(x, *W)  # noqa: E731
+        work, unit, what = wl["layout"].total_bytes + 2 * 2 * wl["hidden"], "GB/s", "single-expert FFNs"
+    elif wl_id in (3, 4):
+        x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"][:1]))
+        route = oex.route_topk_then_softmax if wl_id == 3 else oex.route_softmax_then_topk
+        idx, wts = route(wl["logits"][:1], wl["top_k"])
+        sel = [otc.torch_expert(wl["experts"][int(e)]) for e in idx[0]]
+        if wl_id == 3:
+            dequant = lambda: [otc.mxfp4_expert_weights(e) for e in sel]  # noqa: E731
+            ffn = lambda W, e: otc.mxfp4_expert_ffn(x, *W, e["gate_up_bias"], e["down_bias"])  # noqa: E731
+        else:
+            dequant = lambda: [otc.gguf_expert_weights(e) for e in sel]  # noqa: E731
+            ffn = lambda W, e: otc.gguf_expert_ffn(x, *W)  # noqa: E731
+        matmul = lambda Ws: sum(float(c) * ffn(W, e) for c, W, e in zip(wts[0], Ws, sel))  # noqa: E731
+        work = wl["top_k"] * wl["layout"].total_bytes + 2 * wl["hidden"] * 2 + wl["E"] * 4
+        unit, what = "GB/s", f"single-token MoE-layer decodes (top-{wl['top_k']} of {wl['E']} experts)"
     else:
-        idx, w = oex.route_softmax_then_topk(logits, wl["top_k"])
-        fwd = lambda e, xx: oex.gguf_expert_forward(xx, wl["experts"][e])  # noqa: E731
-        per_expert = wl["layout"].total_bytes
-    nbytes = wl["top_k"] * per_expert + 2 * wl["hidden"] * 2 + wl["E"] * 4
-    oex.moe_combine(x, idx, w, fwd)  # warm-up
-    times = []
+        n_tok = 64
+        idx, wts = oex.route_topk_then_softmax(wl["logits"][:n_tok], wl["top_k"])
+        x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"][:n_tok]))
+        groups = oex.group_tokens_by_expert(idx)
+        sel = {e: otc.torch_expert(wl["experts"][e]) for e in groups}
+        dequant = lambda: {e: otc.mxfp4_expert_weights(t) for e, t in sel.items()}  # noqa: E731
+
+        def matmul(Ws):
+            out = torch.zeros_like(x)
+            for e, pairs in groups.items():
+                toks = torch.tensor([p[0] for p in pairs])
+                c = torch.tensor([float(wts[t, j]) for t, j in pairs]).unsqueeze(1)
+                out.index_add_(0, toks, c * otc.mxfp4_expert_ffn(x[toks], *Ws[e], sel[e]["gate_up_bias"],
+                                                                 sel[e]["down_bias"]))
+            return out
+
+        work = 2 * n_tok * wl["top_k"] * 3 * wl["hidden"] * wl["inter"]
+        unit, what = "TFLOP/s", f"grouped prefills of the first {n_tok} tokens ({len(groups)} routed experts)"
+    for _ in range(warmup):
+        matmul(dequant())
+    td, tm, tt = [], [], []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while len(tt) < min_runs or time.perf_counter() < t_end and len(tt) < 200:
         t0 = time.perf_counter()
-        oex.moe_combine(x, idx, w, fwd)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
-            "sample": f"{len(times)} single-token decodes of workload {wl_id} layer 0 (median {med * 1e3:.1f} ms; "
-                      f"numpy dequant of the top-{wl['top_k']} experts + fp32 BLAS matmuls)"}
+        W = dequant()
+        t1 = time.perf_counter()
+        matmul(W)
+        t2 = time.perf_counter()
+        td.append(t1 - t0)
+        tm.append(t2 - t1)
+        tt.append(t2 - t0)
+        if len(tt) >= min_runs and time.perf_counter() >= t_end:
+            break
+    med = float(np.median(tt))
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": round(work / med / scale, 5), "unit": unit, "cores": cores, "kind": "port",
+            "cpu_model": model, "total_ms": round(med * 1e3, 3), "dequant_ms": round(float(np.median(td)) * 1e3, 3),
+            "matmul_ms": round(float(np.median(tm)) * 1e3, 3), "runs": len(tt),
+            "sample": f"{len(tt)} {what} of workload {wl_id} after {warmup} warmups; torch on the CPU "
+                      f"(torch.set_num_threads({cores})): whole-tensor dequant, then fp32 matmuls; medians"}
 
 
 def main() -> int:
@@ -433,13 +451,14 @@ def main() -> int:
                     help="write profiles/traffic.json from two rocprofv3 --pmc csv runs (no GPU work)")
     ap.add_argument("--pmc-command", default="", help="the profiled command, recorded with --summarize-pmc")
     args = ap.parse_args()
-    kernel_key = "mxt_decode_kernel" if args.workload == 3 and not args.checkpoint_order else (
-        "mx_decode_kernel" if args.workload == 3 else "gq_matvec_kernel" if args.workload == 1 else "gq_phase")
+    traffic_key = "3c" if args.workload == 3 and args.checkpoint_order else str(args.workload)
     if args.summarize_pmc:
-        t = summarize_pmc(*args.summarize_pmc, kernel_key, args.workload, args.pmc_command)
+        t = summarize_pmc(*args.summarize_pmc, traffic_key, args.pmc_command)
+        allt = _read_traffic()
+        allt["workloads"][traffic_key] = t
         os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
         with open(TRAFFIC_FILE, "w") as fh:
-            json.dump(t, fh, indent=1)
+            json.dump(allt, fh, indent=1)
         print(json.dumps(t))
         return 0
     if args.gpus != 1:
@@ -531,20 +550,21 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "note": "achieved = algorithmic bytes per step / HIP-event time per step over the timed graph replay "
-                    "(one fused launch per step: routing + gate_up + SwiGLU + down + weighted sum; inter-launch gaps "
-                    "included)",
+            "note": "achieved = algorithmic bytes per step / HIP-event time per step over the timed graph replay, "
+                    "on the stream the kernels run on; a step is the launches of "
+                    f"{' + '.join(STEP_KERNELS[traffic_key])} (gaps between them included)",
         },
     }
-    tr = load_traffic(args.workload, kernel_key)
+    tr = load_traffic(traffic_key)
     if tr:
-        line["roofline"]["traffic"] = round(tr["traffic_bytes_per_launch"])
+        line["roofline"]["traffic"] = round(tr["traffic_bytes_per_step"])
         line["roofline"]["traffic_note"] = (
-            f"HBM bytes per launch of {kernel_key} from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the "
-            f"counter's reading for a {4 * COPY_ELEMS >> 20} MiB copy (factors {tr['FETCH_SIZE']['copy_factor']:.3f}, "
-            f"{tr['WRITE_SIZE']['copy_factor']:.3f}); algorithmic bytes {nbytes}")
+            f"HBM bytes per step ({' + '.join(STEP_KERNELS[traffic_key])}) from rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+            f"each scaled by the counter's reading for a {4 * COPY_ELEMS >> 20} MiB copy (factors "
+            f"{tr['FETCH_SIZE']['copy_factor']:.3f}, {tr['WRITE_SIZE']['copy_factor']:.3f}); algorithmic bytes "
+            f"{nbytes}")
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.workload) if args.workload > 2 else cpu_baseline_gguf(args.workload)
+        line["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(line))
     return 0
 
