@@ -43,7 +43,11 @@ from tinyserve_amd import _lib, ops, synth  # noqa: E402
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (the prefill GEMMs run bf16 MFMA)
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (the prefill GEMMs' bf16 form)
+# The fp6 form runs v_mfma_scale_f32_32x32x64_f8f6f4 on fp4 weights x fp6 activation terms
+# (MI355X dense fp6/fp4: 10.1 PFLOP/s), two products (hi and lo term) per multiply-add of
+# the GEMM: an algorithmic ceiling of 5.05 PFLOP/s (the int8 / fp8 dense peak is 5.0).
+MFMA_F6F4_ALGO_PEAK_TFLOPS = 10100.0 / 2
 COPY_ELEMS = 64 << 20  # calibration copy: 64 Mi float32 read + written (256 MiB each way)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -255,11 +259,11 @@ class PrefillWorkload:
     """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
     2048-token prefill; one step = one layer's whole batched MoE."""
 
-    def __init__(self, n_layers: int, dev: torch.device):
+    def __init__(self, n_layers: int, dev: torch.device, prefill_mfma: int = _lib.PREFILL_FP6):
         base = synth.workload(5)
         self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
         lay = synth.mxfp4_tiled_layout(self.H, self.I)
-        self.L = mxfp4_expert_layout(lay, tiled=True)
+        self.L = mxfp4_expert_layout(lay, tiled=True, prefill_mfma=prefill_mfma)
         pool0 = np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in base["experts"]])
         g = torch.Generator(device=dev)
         g.manual_seed(20261205)
@@ -295,7 +299,9 @@ class PrefillWorkload:
 
 
 def run_prefill(args, dev) -> int:
-    wl = PrefillWorkload(args.layers_prefill, dev)
+    fp6 = args.prefill_mfma == "fp6"
+    wl = PrefillWorkload(args.layers_prefill, dev, _lib.PREFILL_FP6 if fp6 else _lib.PREFILL_BF16)
+    peak = MFMA_F6F4_ALGO_PEAK_TFLOPS if fp6 else MFMA_BF16_PEAK_TFLOPS
     K, W = args.steps, args.warmup
     for s in range(W):
         wl.step(s)
@@ -323,13 +329,19 @@ def run_prefill(args, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4 weights expanded exactly to bf16, bf16 activations, bf16 MFMA, fp32 accumulate",
+        "dtype": ("mxfp4 weights x activations as two fp6 (e2m3) terms with per-32 e8m0 scales (from bf16), "
+                  "scaled fp4 x fp6 MFMA, fp32 accumulate" if fp6 else
+                  "mxfp4 weights expanded exactly to bf16, bf16 activations, bf16 MFMA, fp32 accumulate"),
         "data": f"synthetic: seeded workload-5 layer + {args.layers_prefill - 1} random layers rotated per step",
         "config": {"workload": "gpt-oss-20b-shaped mxfp4 moe layer prefill (2048 tokens, hidden 2880, 32 experts, "
-                               "zipf top-4)", "flops_per_step": wl.flops_per_step(), "tokens": wl.T},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "note": "whole step (routing, grouping, both GEMMs, combine) per HIP-event time"},
+                               "zipf top-4)", "flops_per_step": wl.flops_per_step(), "tokens": wl.T,
+                   "prefill_mfma": args.prefill_mfma},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None,
+                     "note": "whole step (routing, grouping, activation terms, both GEMMs, combine) per HIP-event "
+                             "time; " + ("peak = the dense fp6/fp4 MFMA rate (10.1 PFLOP/s) / 2 products per "
+                                         "multiply-add (hi and lo activation terms)" if fp6 else
+                                         "peak = dense bf16 MFMA")},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(5)
@@ -440,6 +452,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--layers-prefill", type=int, default=3, help="workload 5: distinct layers rotated per step")
+    ap.add_argument("--prefill-mfma", choices=["fp6", "bf16"], default="fp6",
+                    help="workload 5: the GEMMs' MFMA form (fp4 x fp6 terms, or weights expanded to bf16)")
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")

@@ -57,7 +57,11 @@ typedef enum tsa_expert_format { TSA_EXPERT_MXFP4 = 1, TSA_EXPERT_GGUF = 2 } tsa
  *  GGUF: gate [I x H] of gate_type at gate_off, up [I x H] of up_type at up_off,
  *    down [H x I] of down_type at down_off (GGUF has no biases; set them to -1).
  *  act: TSA_ACT_SWIGLU_OAI = (up+1)*g*sigmoid(alpha*g), g = min(gate, limit),
- *    up = clamp(up, -limit, limit); TSA_ACT_SILU = silu(gate)*up. */
+ *    up = clamp(up, -limit, limit); TSA_ACT_SILU = silu(gate)*up.
+ *  prefill_mfma (tiled MXFP4 prefill GEMMs): TSA_PREFILL_FP6 (0, the default) multiplies the
+ *    fp4 weights with activations carried as two fp6 (e2m3) terms per value with
+ *    per-32-block scales, on the scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4);
+ *    TSA_PREFILL_BF16 (1) expands the weights to bf16 for v_mfma_f32_32x32x16_bf16. */
 typedef struct tsa_expert_layout {
     int32_t format;
     int32_t act;
@@ -70,8 +74,10 @@ typedef struct tsa_expert_layout {
     int64_t gate_bias_off, down_bias_off;
     float swiglu_limit, swiglu_alpha;
     int32_t mx_tiled;
-    int32_t reserved;
+    int32_t prefill_mfma;
 } tsa_expert_layout;
+
+typedef enum tsa_prefill_mfma { TSA_PREFILL_FP6 = 0, TSA_PREFILL_BF16 = 1 } tsa_prefill_mfma;
 
 /* ---- library info / errors (no reference counterpart) ---- */
 int tsa_version(void);

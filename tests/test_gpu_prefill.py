@@ -8,13 +8,13 @@ import torch
 
 from oracle import expert as oex
 from tests.helpers import assert_close_bf16, bf16_dev, to_f32
-from tinyserve_amd import ops, synth
+from tinyserve_amd import _lib, ops, synth
 from tinyserve_amd.expert_forward import mxfp4_expert_layout
 
 pytestmark = pytest.mark.gpu
 
 
-def _pool(H, I, E, seed, bias=True, tiled=True):
+def _pool(H, I, E, seed, bias=True, tiled=True, mfma=_lib.PREFILL_FP6):
     rng = np.random.default_rng(seed)
     experts = [synth.make_mxfp4_expert(rng, H, I, bias=bias) for _ in range(E)]
     if tiled:
@@ -23,7 +23,7 @@ def _pool(H, I, E, seed, bias=True, tiled=True):
     else:
         lay = synth.mxfp4_layout(H, I, bias=bias)
         pool = np.stack([synth.pack_mxfp4_expert(e, lay) for e in experts])
-    return rng, mxfp4_expert_layout(lay, tiled=tiled), experts, torch.from_numpy(pool).cuda()
+    return rng, mxfp4_expert_layout(lay, tiled=tiled, prefill_mfma=mfma), experts, torch.from_numpy(pool).cuda()
 
 
 def _ref(experts, xf, idx, w):
@@ -38,14 +38,16 @@ def _ref(experts, xf, idx, w):
     (1024, 256, 33, 1, 97),    # more experts than the tile table's first rows; k = 1
     (256, 128, 256, 8, 300),   # over 128 partial row tiles spread over the 8 XCD groups
 ])
-def test_prefill_tiled_vs_oracle(H, I, E, k, T):
-    rng, L, experts, pool = _pool(H, I, E, seed=H + I + E + k + T)
+@pytest.mark.parametrize("mfma", [_lib.PREFILL_FP6, _lib.PREFILL_BF16], ids=["fp6", "bf16"])
+def test_prefill_tiled_vs_oracle(H, I, E, k, T, mfma):
+    rng, L, experts, pool = _pool(H, I, E, seed=H + I + E + k + T, mfma=mfma)
     x_bits = synth.bf16_normal(rng, (T, H))
     idx, w = oex.route_topk_then_softmax(synth.zipf_logits(rng, T, E), k)
     y = ops.moe_prefill(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
                         torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(), bf16_dev(x_bits))
     assert y.dtype == torch.bfloat16 and y.shape == (T, H)
-    assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w), f"prefill H={H} I={I} E={E} k={k} T={T}")
+    assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w),
+                      f"prefill H={H} I={I} E={E} k={k} T={T} mfma={mfma}")
 
 
 def test_prefill_only_full_row_tiles():
@@ -137,3 +139,30 @@ def test_prefill_workload5_sampled_tokens():
         for r, j, v in zip(rows, js, ye):
             ref[r] += np.float32(w[toks[r], j]) * v
     assert_close_bf16(yf[toks], ref, "workload 5 sample")
+
+
+def test_prefill_fp6_and_bf16_forms_agree_and_zero_blocks():
+    """The fp6-term and bf16 GEMMs agree with each other and the oracle on activations with
+    all-zero tokens, all-zero 32-blocks, tiny and large blocks (the fp6 scales span them)."""
+    H, I, E, k, T = 512, 384, 6, 2, 96
+    rng, L6, experts, pool = _pool(H, I, E, seed=77)
+    Lb = mxfp4_expert_layout(synth.mxfp4_tiled_layout(H, I), tiled=True, prefill_mfma=_lib.PREFILL_BF16)
+    x = synth.bf16_to_f32(synth.bf16_normal(rng, (T, H)))
+    x[3] = 0.0                      # a zero token
+    x[5, 64:96] = 0.0               # a zero block
+    x[6, :32] *= 2.0 ** -60         # a tiny block
+    x[7, 32:64] *= 2.0 ** 20        # a huge block
+    x_bits = (x.view(np.uint32) >> 16).astype(np.uint16)  # exact: scaling by powers of two
+    idx, w = oex.route_topk_then_softmax(synth.zipf_logits(rng, T, E), k)
+    args = (torch.arange(E, dtype=torch.int32, device="cuda"), torch.from_numpy(idx.astype(np.int32)).cuda(),
+            torch.from_numpy(w).cuda(), bf16_dev(x_bits))
+    y6 = ops.moe_prefill(L6, pool, *args, out_dtype=torch.float32)
+    yb = ops.moe_prefill(Lb, pool, *args, out_dtype=torch.float32)
+    ref = _ref(experts, synth.bf16_to_f32(x_bits), idx, w)
+    rows = [r for r in range(T) if r != 7]  # row 7 (its outputs are far larger) is checked on its own
+    for y, form in ((y6, "fp6"), (yb, "bf16")):
+        yf = to_f32(y)
+        assert np.isfinite(yf).all()
+        assert_close_bf16(yf[rows], ref[rows], f"{form} form")
+        assert_close_bf16(yf[7:8], ref[7:8], f"{form} form, huge block")
+        assert_close_bf16(yf[3:4], ref[3:4], f"{form} form, zero token")

@@ -30,6 +30,7 @@ _TORCH_TO_TSA = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 ROUTE_TOPK_SOFTMAX, ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM = 0, 1, 2
 ACT_SILU, ACT_SWIGLU_OAI = 0, 1
 EXPERT_MXFP4, EXPERT_GGUF = 1, 2
+PREFILL_FP6, PREFILL_BF16 = 0, 1
 
 
 class ExpertLayout(ctypes.Structure):
@@ -55,7 +56,7 @@ class ExpertLayout(ctypes.Structure):
         ("swiglu_limit", ctypes.c_float),
         ("swiglu_alpha", ctypes.c_float),
         ("mx_tiled", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("prefill_mfma", ctypes.c_int32),
     ]
 
 

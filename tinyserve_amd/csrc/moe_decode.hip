@@ -239,6 +239,8 @@ int validate_layout(const tsa_expert_layout* L) {
                 (long long)L->inter);
     TSA_REQUIRE(L->hidden * 4 <= 64 * 1024 && L->inter * 4 <= 64 * 1024, TSA_ERR_SHAPE,
                 "hidden/intermediate sizes above 16384 are not supported");
+    TSA_REQUIRE(L->prefill_mfma == TSA_PREFILL_FP6 || L->prefill_mfma == TSA_PREFILL_BF16, TSA_ERR_INVALID_ARG,
+                "layout.prefill_mfma %d unknown", L->prefill_mfma);
     TSA_REQUIRE(L->mx_tiled == 0 || (L->mx_tiled == 1 && L->format == TSA_EXPERT_MXFP4), TSA_ERR_INVALID_ARG,
                 "layout.mx_tiled must be 0, or 1 for MXFP4 experts (got %d)", L->mx_tiled);
     if (L->mx_tiled) {

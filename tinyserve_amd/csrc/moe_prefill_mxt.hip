@@ -34,6 +34,7 @@
 
 #include "fused_common.h"
 #include "mfma_tile.h"
+#include "fp6_terms.h"
 
 namespace tsa {
 
@@ -61,6 +62,17 @@ constexpr int PF_HS_GU = 272;   // LDS row stride (bytes) of the staged gate_up 
 constexpr int PF_HS_DN = 528;   // ... of the staged down outputs: 256 values + 16 B
 static_assert(PF_BM * PF_HS_DN <= PF_LDS, "the staged outputs fit in the stages");
 constexpr int PF_COST0 = 96;  // a tile's estimated cost is PF_COST0 + rows (measured: 16 rows ~0.5 x 128 rows)
+// fp6 form of the activations (TSA_PREFILL_FP6): a row is a run of records, one per 128-wide
+// piece of K: 4 blocks of 32 values, each 24 bytes of hi codes then 24 of lo codes
+// (fp6_terms.h), then the 4 hi scale bytes, then 12 bytes of padding (208 = 13 x 16 bytes:
+// whole DMA chunks, and a record stride of 52 dwords keeps the operand reads of 8
+// consecutive tokens on distinct LDS banks).
+constexpr int PF_QREC = 208;
+constexpr int PF_QSCALE = 192;
+constexpr int PF_QCHUNKS = PF_QREC / 16;
+static_assert(PF_BM * PF_QREC <= PF_XBYTES, "a piece of fp6 records fits an activation stage");
+constexpr int PF_HS_Q = 528;  // LDS row stride (bytes) of gate_up's fp32 outputs in the fp6 form: 128 h + 16 B
+static_assert(PF_BM * PF_HS_Q <= PF_LDS, "the staged fp32 outputs fit in the stages");
 
 struct PfEntry {
     int slot, row0, rows, expert;
@@ -71,12 +83,15 @@ struct PfGemm {
     const uint8_t* pool;
     const int* n_entries;     // device: [0] all table entries, [1 + x] .. [2 + x] XCD x's group
     const PfEntry* table;
-    const uint16_t* src;      // gate_up: x [T, K] rows gathered through perm; down: h [n, K] sorted
+    const void* src;          // gate_up: x rows gathered through perm; down: h rows in sorted order
     int64_t src_rows;         // rows of src (bounds of its buffer resource)
+    int64_t src_stride;       // bytes per src row (bf16: 2 K; fp6 records: 208 MP)
     const int32_t* perm;      // sorted position -> assignment id (token * k + j)
     int* ctr;                 // 8 per-XCD tile counters (stride PF_CTR_STRIDE), zero at launch
     int k;
-    uint16_t* out;            // gate_up: h [n, N / 2]; down: yk [T k, N]
+    uint16_t* out;            // gate_up: h [n, N / 2] (bf16 form); down: yk [T k, N]
+    uint8_t* qout;            // gate_up in the fp6 form: h as fp6 records, rows of out_stride bytes
+    int64_t out_stride;
     int N, K, NT, MP;         // weight rows, reduction length, tiles along N, pieces along K
     int64_t w_off, s_off, b_off;        // slot offsets of the tiled blocks, tiled scales, bias (< 0: none)
     int64_t tile_bytes, stile_bytes;    // per 16-row tile
@@ -180,6 +195,85 @@ __device__ __forceinline__ void pf_piece(v16f (&acc)[2][2], const uint8_t* xs, c
     }
 }
 
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// acc += A (fp4 weights, e8m0 scale sa) x B (fp6 e2m3 activations, scale byte OPB of sb).
+template <int OPB>
+__device__ __forceinline__ v16f mfma_f4f6(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 2, 0, sa, OPB, sb);
+}
+
+// One 128-wide piece of a wave's 64-row x 64-token block on the scaled MFMA
+// v_mfma_scale_f32_32x32x64_f8f6f4 (fp4 weights as A, fp6 activation terms as B; 2 x 2
+// blocks of 32 x 32, two K-steps of 64, each a hi and a lo product). Lane (q, r) = (lane /
+// 32, lane % 32) supplies, for K-step ks, block 2 ks + q of weight row r: the 16 bytes of
+// its 16-row tile's lane 16 (2 ks + q) + r % 16 and that lane's scale byte for the piece;
+// and of token column r: the block's 24 bytes of hi (or lo) codes and its scale, which the
+// instruction takes from byte 2 ks of the scale word shifted down by q bytes. Blocks at
+// or past K get a zero weight operand with a unit scale (their activation records are
+// zero, but the weight bytes and scales there belong to the next tile).
+template <int NB>
+__device__ __forceinline__ void pf_piece_q6(v16f (&acc)[2][2], const uint8_t* xs, const uint8_t* ws,
+                                            const uint8_t* ss, int mp, int K, int wn, int wt, int lane) {
+    const int q = lane >> 5, rr = lane & 31;
+    v8i A[2][2];
+    int sa[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int rt = 4 * wn + 2 * rb + (rr >> 4);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int lt = 16 * (2 * ks + q) + (rr & 15);
+            const u32x4 w = *reinterpret_cast<const u32x4*>(ws + rt * 1024 + 16 * lt);
+            A[rb][ks] = v8i{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+            sa[rb][ks] = ss[rt * 256 + 4 * lt + (mp & 3)];
+        }
+    }
+    if (128 * (mp + 1) > K) {  // the row's last, partial piece
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                if (128 * mp + 32 * (2 * ks + q) >= K) {
+                    A[rb][ks] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    sa[rb][ks] = 127;
+                }
+    }
+    v8i Bh[2][NB], Bl[2][NB];
+    int sh[NB], sl[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint8_t* rec = xs + (64 * wt + 32 * b + rr) * PF_QREC;
+        sh[b] = (int)(*reinterpret_cast<const uint32_t*>(rec + PF_QSCALE) >> (8 * q));
+        sl[b] = sh[b] - 0x05050505;  // lo scale = hi scale - 5 (every scale byte is >= 5)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const uint8_t* blk = rec + 48 * (2 * ks + q);
+            const u32x4 d0 = *reinterpret_cast<const u32x4*>(blk);
+            const u32x4 d1 = *reinterpret_cast<const u32x4*>(blk + 16);
+            const u32x4 d2 = *reinterpret_cast<const u32x4*>(blk + 32);
+            Bh[ks][b] = v8i{(int)d0[0], (int)d0[1], (int)d0[2], (int)d0[3], (int)d1[0], (int)d1[1], 0, 0};
+            Bl[ks][b] = v8i{(int)d1[2], (int)d1[3], (int)d2[0], (int)d2[1], (int)d2[2], (int)d2[3], 0, 0};
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[rb][b] = mfma_f4f6<0>(A[rb][0], Bh[0][b], acc[rb][b], sa[rb][0], sh[b]);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[rb][b] = mfma_f4f6<0>(A[rb][0], Bl[0][b], acc[rb][b], sa[rb][0], sl[b]);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[rb][b] = mfma_f4f6<2>(A[rb][1], Bh[1][b], acc[rb][b], sa[rb][1], sh[b]);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[rb][b] = mfma_f4f6<2>(A[rb][1], Bl[1][b], acc[rb][b], sa[rb][1], sl[b]);
+}
+
 // The K loop of one tile, as a stream of steps s = -PF_WAHEAD .. MP - 1: step s waits for
 // and multiplies piece s (s >= 0), then issues the activations of piece s + PF_XAHEAD and
 // the weights of piece s + PF_WAHEAD, in that order. The weights of piece i therefore go
@@ -187,7 +281,7 @@ __device__ __forceinline__ void pf_piece(v16f (&acc)[2][2], const uint8_t* xs, c
 // complete, W(s) and its scale word are too; the loads newer than X(s) are counted
 // exactly (never fewer than issued: a wait for fewer outstanding is only stricter). NB = 0:
 // the wave has no live block in this tile and only takes part in the loads and barriers.
-template <int NB, class IX, class IW, class WL>
+template <int NB, bool Q6, class IX, class IW, class WL>
 __device__ __forceinline__ void pf_kloop(v16f (&acc)[2][2], IX& issue_x, IW& issue_w, WL& w_loads, int MP, int K,
                                          int wn, int wt, int lane) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -205,12 +299,13 @@ __device__ __forceinline__ void pf_kloop(v16f (&acc)[2][2], IX& issue_x, IW& iss
             const uint8_t* xs = smem + (st % PF_XST) * PF_XBYTES;
             const uint8_t* ws = smem + PF_WOFF + (st % PF_WST) * PF_WBYTES;
             const uint8_t* ss = smem + PF_SOFF + ((st >> 2) & 1) * PF_SBYTES;
-            pf_piece<NB ? NB : 1>(acc, xs, ws, ss, st, K, wn, wt, lane);
+            if constexpr (Q6) pf_piece_q6<NB ? NB : 1>(acc, xs, ws, ss, st, K, wn, wt, lane);
+            else pf_piece<NB ? NB : 1>(acc, xs, ws, ss, st, K, wn, wt, lane);
         }
     }
 }
 
-template <bool GATE_UP>
+template <bool GATE_UP, bool Q6>
 __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
@@ -224,7 +319,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
     __shared__ int s_next;
     const int W = (int)(p.stile_bytes >> 8);  // scale words per lane
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
-    const v4i xr = buf_desc(p.src, (uint32_t)(p.src_rows * K * 2));
+    const v4i xr = buf_desc(p.src, (uint32_t)(p.src_rows * p.src_stride));
 
     // The first tile of workgroup b is b / 8; later ones come from the counter (offset by R,
     // so the first R are never handed out twice).
@@ -241,13 +336,24 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         // s = lane % 16 the row's 16-byte chunk s ^ (token % 16). The swizzle keeps the B
         // fragment reads (one chunk of 32 tokens per lane group) free of bank conflicts.
         // Tokens past the tile's rows re-read token 0's row (their columns are dropped).
+        // fp6 form: the piece's 128 records are 13 x 128 chunks of 16 bytes, chunk i at LDS
+        // offset 16 i; instruction c of wave w carries chunks 64 (4 w + c) + lane (those past
+        // the tile's rows, and the 384 past 128 records, re-read token 0's and land in the
+        // unused end of the stage).
         uint32_t xoff[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            int tok = 16 * wave + 4 * c + (lane >> 4);
+            int tok, ch = 0;
+            if constexpr (Q6) {
+                const int ci = 64 * (4 * wave + c) + lane;
+                tok = ci / PF_QCHUNKS;
+                ch = ci - PF_QCHUNKS * tok;
+            } else {
+                tok = 16 * wave + 4 * c + (lane >> 4);
+            }
             if (tok >= rows) tok = 0;
             const int64_t srow = GATE_UP ? p.perm[row0 + tok] / p.k : row0 + tok;
-            xoff[c] = (uint32_t)(srow * K * 2);
+            xoff[c] = (uint32_t)(srow * p.src_stride + 16 * ch);
         }
         // Weight DMA: wave w fills row tiles 2w, 2w+1 of the workgroup's 16; one resource
         // spans the workgroup's live tiles (tiles past N read zero).
@@ -263,6 +369,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         const uint32_t sb = (uint32_t)p.stile_bytes;
         auto issue_x = [&](int mp) {
             const uint32_t st = lds0 + (uint32_t)((mp % PF_XST) * PF_XBYTES) + 16 * wave * 256;
+            if constexpr (Q6) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) pf_dma(xr, xoff[c] + PF_QREC * mp, st + c * 1024);
+                return;
+            }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int tok = 16 * wave + 4 * c + (lane >> 4);
@@ -318,9 +429,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
                 for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
         // One K loop per live-subtile count, so the accumulators keep one register home
         // (a per-piece branch made the compiler copy them after every piece).
-        if (!active) pf_kloop<0>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
-        else if (nsub == 2) pf_kloop<2>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
-        else pf_kloop<1>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        if (!active) pf_kloop<0, Q6>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        else if (nsub == 2) pf_kloop<2, Q6>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
+        else pf_kloop<1, Q6>(acc, issue_x, issue_w, w_loads, MP, K, wn, wt, lane);
         if (tid == 0) s_next = grabbed;
         __syncthreads();  // every wave is done with the last stages before the next tile refills them
         tl = uniform(s_next);  // rewritten only after the next tile's K loop, which has a barrier per piece
@@ -329,7 +440,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         // per token (the stages are free: every wave is past the K loop's last LDS read).
         // acc[rb][b][4u + r] is row 32 rb + 8u + 4g + r of the wave's 64 (r = 0..3), token
         // column 64 wt + 32 b + (lane % 32).
-        constexpr int HS = GATE_UP ? PF_HS_GU : PF_HS_DN;
+        constexpr int HS = GATE_UP ? (Q6 ? PF_HS_Q : PF_HS_GU) : PF_HS_DN;
         if (active) {
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -343,7 +454,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
                         const int tk = 64 * wt + 32 * b + rr;
                         if (b >= nsub || tk >= rows) continue;
                         const v4f v = v4f{acc[rb][b][4 * u], acc[rb][b][4 * u + 1], acc[rb][b][4 * u + 2], acc[rb][b][4 * u + 3]} + bias;
-                        if (GATE_UP)
+                        if (GATE_UP && Q6)
+                            *reinterpret_cast<float2*>(smem + tk * HS + 2 * c) =
+                                make_float2(swiglu_oai_fast(p.L, v[0], v[1]), swiglu_oai_fast(p.L, v[2], v[3]));
+                        else if (GATE_UP)
                             *reinterpret_cast<uint32_t*>(smem + tk * HS + c) =
                                 pack_bf16x2(swiglu_oai_fast(p.L, v[0], v[1]), swiglu_oai_fast(p.L, v[2], v[3]));
                         else
@@ -353,9 +467,38 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
             }
         }
         __syncthreads();
-        // 2: whole rows out, 16 bytes (8 values) per lane, consecutive lanes along a row:
-        // gate_up h[row0 + tk, 128 nt ..] (256 B a row), down yk[perm[row0 + tk], 256 nt ..] (512 B).
-        {
+        // 2, fp6 form of gate_up: thread (token tk, block bq) turns h[row0 + tk, 128 nt + 32 bq ..]
+        // into its fp6 terms, written to record nt of the row (blocks past the row's end as
+        // zero codes with a unit scale: the down GEMM multiplies them by zero weights).
+        if constexpr (GATE_UP && Q6) {
+            const int tk = tid & (PF_BM - 1), bq = tid >> 7;
+            if (tk < rows) {
+                uint32_t hi[6], lo[6], sc = 127u;
+                const int c0 = 128 * nt + 32 * bq;
+                if (c0 < N / 2) {
+                    float v[32];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const v4f f = *reinterpret_cast<const v4f*>(smem + tk * HS + 128 * bq + 16 * i);
+                        v[4 * i] = f[0];
+                        v[4 * i + 1] = f[1];
+                        v[4 * i + 2] = f[2];
+                        v[4 * i + 3] = f[3];
+                    }
+                    sc = fp6_terms(v, hi, lo);
+                } else {
+#pragma unroll
+                    for (int d = 0; d < 6; ++d) hi[d] = lo[d] = 0u;
+                }
+                uint8_t* rec = p.qout + (int64_t)(row0 + tk) * p.out_stride + (int64_t)nt * PF_QREC;
+                *reinterpret_cast<uint4*>(rec + 48 * bq) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<uint4*>(rec + 48 * bq + 16) = make_uint4(hi[4], hi[5], lo[0], lo[1]);
+                *reinterpret_cast<uint4*>(rec + 48 * bq + 32) = make_uint4(lo[2], lo[3], lo[4], lo[5]);
+                rec[PF_QSCALE + bq] = (uint8_t)sc;
+            }
+        } else {
+            // 2: whole rows out, 16 bytes (8 values) per lane, consecutive lanes along a row:
+            // gate_up h[row0 + tk, 128 nt ..] (256 B a row), down yk[perm[row0 + tk], 256 nt ..] (512 B).
             constexpr int CPR = GATE_UP ? 16 : 32;  // 16-byte chunks per row
             const int ncol = GATE_UP ? N / 2 - 128 * nt : N - 256 * nt;  // live values in the row (multiple of 8)
 #pragma unroll
@@ -482,6 +625,44 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
     }
 }
 
+// x [rows, K] bf16 -> fp6 records (rows of MP records; blocks at or past K as zero codes with a
+// unit scale). One thread per (row, 32-value block).
+__global__ void __launch_bounds__(256) pf_quant_kernel(const uint16_t* __restrict__ x, int64_t rows, int K, int MP,
+                                                       uint8_t* __restrict__ out) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nb = 4 * MP;
+    if (g >= rows * nb) return;
+    const int64_t r = g / nb;
+    const int b = (int)(g - r * nb);
+    uint32_t hi[6], lo[6], sc = 127u;
+    if (32 * b < K) {
+        // a bounded buffer resource over x: no alignment assumption beyond the element's
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(x), (short)0, (int)(rows * K * 2), 0x00020000);
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 w = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)((r * K + 32 * b + 8 * i) * 2), 0, 0));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * i + 2 * j] = bf16_bits_to_f32(w[j] & 0xFFFFu);
+                v[8 * i + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+            }
+        }
+        sc = fp6_terms(v, hi, lo);
+    } else {
+#pragma unroll
+        for (int d = 0; d < 6; ++d) hi[d] = lo[d] = 0u;
+    }
+    uint8_t* rec = out + r * (int64_t)MP * PF_QREC + (int64_t)(b >> 2) * PF_QREC;
+    const int bq = b & 3;
+    *reinterpret_cast<uint4*>(rec + 48 * bq) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(rec + 48 * bq + 16) = make_uint4(hi[4], hi[5], lo[0], lo[1]);
+    *reinterpret_cast<uint4*>(rec + 48 * bq + 32) = make_uint4(lo[2], lo[3], lo[4], lo[5]);
+    rec[PF_QSCALE + bq] = (uint8_t)sc;
+}
+
 // y[t] = sum_j w[t, j] yk[t k + j] over the live assignments, j in order; 8 columns per thread.
 __global__ void __launch_bounds__(256) pf_combine_kernel(const uint16_t* __restrict__ yk,
                                                          const int32_t* __restrict__ idx,
@@ -545,16 +726,21 @@ __global__ void __launch_bounds__(256) pf_combine_kernel(const uint16_t* __restr
 
 // Whether the tiled MXFP4 grouped-GEMM path covers this call (else the caller uses the
 // fused decode kernel token chunk by token chunk).
+static int64_t q6_row_bytes(int64_t K) { return (K + 127) / 128 * PF_QREC; }
+
 bool pf_mxt_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k) {
-    const int64_t n = T * k;
+    const int64_t n = T * k, lim = (int64_t)1 << 32;
+    const bool bf16_ok = T * L.hidden * 2 < lim && n * L.inter * 2 < lim;
+    const bool q6_ok = L.prefill_mfma != TSA_PREFILL_FP6 || (T * q6_row_bytes(L.hidden) < lim &&
+                                                            n * q6_row_bytes(L.inter) < lim);
     return L.format == TSA_EXPERT_MXFP4 && L.mx_tiled && x_dtype == TSA_BF16 && L.hidden % 16 == 0 &&
-           L.inter % 16 == 0 && T * L.hidden * 2 < ((int64_t)1 << 32) && n * L.inter * 2 < ((int64_t)1 << 32);
+           L.inter % 16 == 0 && bf16_ok && q6_ok;
 }
 
 static int64_t al256(int64_t v) { return (v + 255) / 256 * 256; }
 
 struct PfWs {
-    int64_t counts, offsets, perm, nent, ctr, table, h, yk, total;
+    int64_t counts, offsets, perm, nent, ctr, table, h, xq, yk, total;
 };
 
 static PfWs pf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
@@ -567,7 +753,9 @@ static PfWs pf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E
     w.nent = o; o += 256;
     w.ctr = o; o += al256(4 * PF_CTR_INTS);
     w.table = o; o += al256((int64_t)sizeof(PfEntry) * (n / PF_BM + E + 1));
-    w.h = o; o += al256(2 * n * L.inter);
+    const bool q6 = L.prefill_mfma == TSA_PREFILL_FP6;
+    w.h = o; o += al256(q6 ? n * q6_row_bytes(L.inter) : 2 * n * L.inter);  // h: fp6 records or bf16
+    w.xq = o; o += q6 ? al256(T * q6_row_bytes(L.hidden)) : 0;              // x as fp6 records
     w.yk = o; o += al256(2 * n * L.hidden);
     w.total = o;
     return w;
@@ -603,11 +791,13 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     static std::once_flag lds_once;
     static hipError_t lds_err = hipSuccess;
     std::call_once(lds_once, [] {
-        lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gemm_kernel<true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
-        if (lds_err == hipSuccess)
-            lds_err = hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gemm_kernel<false>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+        const void* kernels[4] = {reinterpret_cast<const void*>(pf_gemm_kernel<true, false>),
+                                  reinterpret_cast<const void*>(pf_gemm_kernel<false, false>),
+                                  reinterpret_cast<const void*>(pf_gemm_kernel<true, true>),
+                                  reinterpret_cast<const void*>(pf_gemm_kernel<false, true>)};
+        for (const void* f : kernels)
+            if (lds_err == hipSuccess)
+                lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
     });
     TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", PF_LDS, hipGetErrorString(lds_err));
     const int grid = (num_cus() / 8) * 8;
@@ -619,10 +809,21 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     g.perm = perm;
     g.ctr = ctr;
     g.k = k;
+    const bool q6 = L.prefill_mfma == TSA_PREFILL_FP6;
+    uint8_t* xq = ws + w.xq;
+    if (q6) {  // x as fp6 records
+        const int64_t threads = T * 4 * ((H + 127) / 128);
+        hipLaunchKernelGGL(pf_quant_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, x, T, H,
+                           (H + 127) / 128, xq);
+        TSA_LAUNCH_CHECK();
+    }
     // gate_up: [2I, H] -> h
-    g.src = x;
+    g.src = q6 ? static_cast<const void*>(xq) : static_cast<const void*>(x);
     g.src_rows = T;
+    g.src_stride = q6 ? q6_row_bytes(H) : 2 * (int64_t)H;
     g.out = h;
+    g.qout = ws + w.h;
+    g.out_stride = q6_row_bytes(I);
     g.N = 2 * I;
     g.K = H;
     g.NT = (2 * I + PF_BN - 1) / PF_BN;
@@ -632,11 +833,13 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     g.b_off = L.gate_bias_off;
     g.tile_bytes = 16 * (int64_t)H / 2;
     g.stile_bytes = mx_tile_scale_bytes(H);
-    hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    if (q6) hipLaunchKernelGGL((pf_gemm_kernel<true, true>), dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    else hipLaunchKernelGGL((pf_gemm_kernel<true, false>), dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
     TSA_LAUNCH_CHECK();
     // down: [H, I] -> yk
-    g.src = h;
+    g.src = ws + w.h;
     g.src_rows = T * k;
+    g.src_stride = q6 ? q6_row_bytes(I) : 2 * (int64_t)I;
     g.ctr = ctr + 8 * PF_CTR_STRIDE;
     g.out = yk;
     g.N = H;
@@ -648,7 +851,8 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     g.b_off = L.down_bias_off;
     g.tile_bytes = 16 * (int64_t)I / 2;
     g.stile_bytes = mx_tile_scale_bytes(I);
-    hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    if (q6) hipLaunchKernelGGL((pf_gemm_kernel<false, true>), dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
+    else hipLaunchKernelGGL((pf_gemm_kernel<false, false>), dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
     TSA_LAUNCH_CHECK();
 
     const int64_t threads = T * (H / 8);

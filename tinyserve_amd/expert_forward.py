@@ -68,10 +68,12 @@ def _mx_tiled_specs(layout: TensorLayout) -> bool:
 
 def mxfp4_expert_layout(layout: TensorLayout, act_fn=None, slot_bytes: int | None = None,
                         swiglu_limit: float = _SWIGLU_LIMIT, swiglu_alpha: float = _QUICK_GELU_COEFF,
-                        tiled: bool = False) -> _lib.ExpertLayout:
+                        tiled: bool = False, prefill_mfma: int = 0) -> _lib.ExpertLayout:
     """tsa_expert_layout of a GPT-OSS MXFP4 slot (gate_up_proj[_scales/_bias], down_proj[...]);
     ``tiled`` marks matrices stored in the 16-row MFMA tile order (synth.mxfp4_tiled_layout);
-    a layout whose scale tensors have the tiled shape is taken as tiled in any case."""
+    a layout whose scale tensors have the tiled shape is taken as tiled in any case.
+    ``prefill_mfma``: _lib.PREFILL_FP6 (fp4 weights x two fp6 activation terms on the scaled
+    MFMA, the default) or _lib.PREFILL_BF16 (weights expanded to bf16) for the prefill GEMMs."""
     specs = layout.specs
     tiled = tiled or _mx_tiled_specs(layout)
     gu_shape = tuple(specs["gate_up_proj"][0])
@@ -102,6 +104,9 @@ def mxfp4_expert_layout(layout: TensorLayout, act_fn=None, slot_bytes: int | Non
     L.bias_dtype = _BIAS_DTYPES[bias_dt]
     L.swiglu_limit, L.swiglu_alpha = float(swiglu_limit), float(swiglu_alpha)
     L.mx_tiled = int(bool(tiled))
+    if prefill_mfma not in (_lib.PREFILL_FP6, _lib.PREFILL_BF16):
+        raise ValueError(f"prefill_mfma must be PREFILL_FP6 or PREFILL_BF16, got {prefill_mfma}")
+    L.prefill_mfma = int(prefill_mfma)
     return L
 
 
