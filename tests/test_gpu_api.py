@@ -12,7 +12,8 @@ from oracle import mxfp4 as omx
 from tests.helpers import assert_close_bf16, bf16_dev, to_f32
 from tinyserve_amd import ggml_ops, mxfp4, synth
 from tinyserve_amd.expert_batcher import BatchItem, ExpertBatcher
-from tinyserve_amd.expert_forward import mxfp4_expert_layout
+from tinyserve_amd.expert_pipeline import ExpertPipeline
+from tinyserve_amd.expert_store import ExpertStore
 from tinyserve_amd.ggml_forward import GGMLExpertForward
 from tinyserve_amd.ggml_linear import GGMLLinear, replace_linear_with_ggml
 
@@ -115,22 +116,13 @@ def test_mxfp4_functions():
     assert_close_bf16(y, ref.reshape(1, -1), "mxfp4_linear")
 
 
-class _Pipeline:
-    def __init__(self, layout, pool, E):
-        self.layout, self.pool = layout, pool
-        self._es = torch.arange(E, dtype=torch.int32, device="cuda")
-
-    def expert_slot(self, layer_idx):
-        return self._es
-
-
 def test_expert_batcher():
     H, I, E, k = 256, 128, 6, 2
     rng = np.random.default_rng(9)
     lay = synth.mxfp4_layout(H, I)
     experts = [synth.make_mxfp4_expert(rng, H, I) for _ in range(E)]
-    pool = torch.from_numpy(np.stack([synth.pack_mxfp4_expert(e, lay) for e in experts])).cuda()
-    batcher = ExpertBatcher(_Pipeline(mxfp4_expert_layout(lay), pool, E))
+    data = torch.from_numpy(np.stack([synth.pack_mxfp4_expert(e, lay) for e in experts])).reshape(1, E, -1)
+    batcher = ExpertBatcher(ExpertPipeline(ExpertStore(data, lay, 1, E), None, "cuda"))
     items, refs = [], []
     for r in range(5):
         x_bits = synth.bf16_normal(rng, (1, H))

@@ -113,3 +113,69 @@ def test_gguf_matvec_token_limit(T, gtype, x_dtype):
     cos, rel = metrics(to_f32(y), ref)
     bar = 1e-4 if x_dtype != torch.bfloat16 else 1e-5  # hi/lo staging keeps fp32-level accuracy
     assert cos > 0.999999 and rel < bar, (cos, rel)
+
+
+def test_gguf_decode_routed_workload4_full_size():
+    """Workload 4 at its real shape: 128 Q5_K/Q6_K experts of hidden 2048, inter 768, top-8
+    of softmax-renormalised logits, one token (the benchmark's configuration)."""
+    wl = synth.workload(4)
+    H, I, E, k = wl["hidden"], wl["inter"], wl["E"], wl["top_k"]
+    pool = torch.from_numpy(wl["pool"]).cuda()
+    L = gguf_expert_layout(wl["layout"], {"gate": 13, "up": 13, "down": 14}, {"gate": (H, I), "up": (H, I), "down": (I, H)})
+    y, idx, w = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                      torch.from_numpy(wl["logits"]).cuda(), bf16_dev(wl["x_bits"]), k,
+                                      "softmax_then_topk", return_routing=True)
+    ridx, rw = oex.route_softmax_then_topk(wl["logits"], k)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    assert_close_bf16(y, _ref(wl["experts"], synth.bf16_to_f32(wl["x_bits"]), ridx, rw), "workload 4")
+
+
+def test_gguf_prefill_workload4_shapes():
+    """tsa_moe_prefill over GGUF slots at workload-4 shapes, 64 tokens (the GGUF prefill
+    runs the super-block decode over all the tokens' assignments at once)."""
+    rng = np.random.default_rng(64)
+    H, I, E, k, T = 2048, 768, 128, 8, 64
+    L, experts, pool = _pool(rng, H, I, (13, 13, 14), E)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    idx, w = oex.route_softmax_then_topk(synth.zipf_logits(rng, T, E), k)
+    y = ops.moe_prefill(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                        torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(), bf16_dev(x_bits))
+    ref = oex.moe_combine_grouped(synth.bf16_to_f32(x_bits), idx, w,
+                                  lambda e, xx: oex.gguf_expert_forward(xx, experts[e]))
+    assert_close_bf16(y, ref, "GGUF prefill, workload-4 shapes")
+
+
+def test_gguf_decode_more_assignments_than_grid_rows():
+    """T k above 65535 (one launch grid row per assignment): the decode runs token chunks."""
+    rng = np.random.default_rng(65)
+    H, I, E, k, T = 256, 256, 8, 8, 8200
+    L, experts, pool = _pool(rng, H, I, (8, 8, 8), E)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    idx = np.argsort(rng.random((T, E)), axis=1)[:, :k].astype(np.int32)  # k distinct experts per token
+    w = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
+    y = ops.moe_decode(L, pool, torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), bf16_dev(x_bits))
+    ref = oex.moe_combine_grouped(synth.bf16_to_f32(x_bits), idx, w,
+                                  lambda e, xx: oex.gguf_expert_forward(xx, experts[e]))
+    assert_close_bf16(y, ref, "GGUF decode, T k = 65600")
+
+
+def test_ggml_expert_forward_other_activation():
+    """GGMLExpertForward with a non-SiLU act_fn (here GELU) runs act_fn(gate) * up between the
+    GGUF matvecs, as the reference passes any act_fn."""
+    from tinyserve_amd.ggml_forward import GGMLExpertForward
+
+    rng = np.random.default_rng(66)
+    H, I = 512, 256
+    types = {"gate": 12, "up": 12, "down": 14}
+    lay = synth.gguf_layout(H, I, 12, 12, 14)
+    e = synth.make_gguf_expert(rng, H, I, 12, 12, 14)
+    packed = torch.from_numpy(synth.pack_gguf_expert(e, lay)).cuda()
+    fwd = GGMLExpertForward(lay, types, torch.nn.GELU(), {"gate": (H, I), "up": (H, I), "down": (I, H)})
+    x_bits = synth.bf16_normal(rng, (3, H))
+    y = fwd.forward(packed, bf16_dev(x_bits))
+    wg, wu, wd = oex.gguf_expert_weights(e)
+    xf = synth.bf16_to_f32(x_bits)
+    g = torch.nn.functional.gelu(torch.from_numpy(xf @ wg.T)).numpy()
+    ref = (g * (xf @ wu.T)) @ wd.T
+    assert_close_bf16(y, ref, "GELU-gated GGUF expert")

@@ -200,9 +200,11 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
 
 // GGUF experts with 2-byte aligned tensors, one gate/up type and k <= 16 run on the
 // super-block streaming kernels of moe_decode_gq.hip; the row kernels below cover the rest.
-static bool use_gq(const tsa_expert_layout& L, const uint8_t* pl, int k) {
+// The super-block GGUF decode covers 2-byte aligned slots, k <= 16 and T k <= 65535 (one
+// grid row per assignment); other calls take the per-row kernels.
+static bool use_gq(const tsa_expert_layout& L, const uint8_t* pl, int64_t T, int k) {
     const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
-    return L.format == TSA_EXPERT_GGUF && a2 && k <= 16 && !*gq_unsupported(L);
+    return L.format == TSA_EXPERT_GGUF && a2 && k <= 16 && T * k <= 65535 && !*gq_unsupported(L);
 }
 int mx_fused_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
                     const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot,
@@ -359,6 +361,18 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
     if (L.mx_tiled)
         return tiled_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x,
                             x_dtype, y, y_dtype, ws, workspace_bytes, st);
+    if (T * k > 65535) {  // the other paths launch one grid row per assignment: token chunks
+        const int64_t tc = 65535 / k;
+        for (int64_t t0 = 0; t0 < T; t0 += tc) {
+            const int64_t n = T - t0 < tc ? T - t0 : tc;
+            rc = tsa_moe_decode(layout, pool, n_slots, slots + t0 * k, weights + t0 * k, n, k,
+                                static_cast<const uint8_t*>(x) + t0 * L.hidden * dtype_size(x_dtype), x_dtype,
+                                static_cast<uint8_t*>(y) + t0 * L.hidden * dtype_size(y_dtype), y_dtype, workspace,
+                                workspace_bytes, stream);
+            if (rc) return rc;
+        }
+        return TSA_OK;
+    }
     rc = mx_fused_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
                          y, y_dtype, ws, workspace_bytes, st);
     if (rc <= 0) return rc;
@@ -385,7 +399,7 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
         TSA_LAUNCH_CHECK();
         return TSA_OK;
     }
-    if (use_gq(L, pl, k))
+    if (use_gq(L, pl, T, k))
         return gq_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
                          y, y_dtype, ws, h_region(L, T, k), st);
     const bool a2 = ((reinterpret_cast<uintptr_t>(pl) | L.slot_bytes | L.gate_off | L.up_off | L.down_off) & 1) == 0;
@@ -444,7 +458,7 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
                              w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
         if (rc <= 0) return rc;
     }
-    if (use_gq(L, pl, k) && E <= 256 && T <= 4)
+    if (use_gq(L, pl, T, k) && E <= 256 && T <= 4)
         return gq_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
                          T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
     // separate routing, slot mapping and the two-launch decode

@@ -41,6 +41,13 @@ __global__ void __launch_bounds__(256) mx_tile_kernel(const uint8_t* __restrict_
     ts[r * 256 * W + 1024 * ch + 4 * width * lanepos + 4 * (w % 4) + (b / 4) % 4] = scales[c];
 }
 
+// Zero n bytes (the tiled scale area's padding words must read zero). A kernel, not
+// hipMemsetAsync, so that the call can be captured into a HIP graph.
+__global__ void __launch_bounds__(256) mx_zero_kernel(uint8_t* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
 }  // namespace
 }  // namespace tsa
 
@@ -65,7 +72,9 @@ extern "C" int tsa_mxfp4_tile(const void* blocks, const void* scales, int64_t N,
     TSA_REQUIRE(((reinterpret_cast<uintptr_t>(blocks) | reinterpret_cast<uintptr_t>(tiled_blocks)) & 15) == 0,
                 TSA_ERR_INVALID_ARG, "blocks and tiled_blocks must be 16-byte aligned");
     hipStream_t st = as_stream(stream);
-    TSA_HIP_CHECK(hipMemsetAsync(tiled_scales, 0, (size_t)sb, st));
+    hipLaunchKernelGGL(mx_zero_kernel, dim3((unsigned)((sb + 255) / 256 < 1024 ? (sb + 255) / 256 : 1024)), dim3(256),
+                       0, st, static_cast<uint8_t*>(tiled_scales), sb);
+    TSA_LAUNCH_CHECK();
     const int64_t G = K / 32, n = N * G;
     hipLaunchKernelGGL(mx_tile_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        static_cast<const uint8_t*>(blocks), static_cast<const uint8_t*>(scales), N, G,

@@ -3,10 +3,15 @@
 ``TensorLayout`` keeps the contract of the reference's class of the same name
 (tinyserve/expert_store.py:57-77): offsets are assigned in the insertion order of
 ``tensor_specs``; ``sizes`` are element count times element size; ``total_bytes`` is
-the slot size. The resident slot pool (``ExpertCache``) stores experts in exactly
-this layout, in the weights' native formats (no repacking).
+the slot size. The resident slot pool (``ExpertCache``) stores experts in exactly this
+layout. MXFP4 checkpoints can be kept in their checkpoint order or repacked once, at
+load time, into the 16-row MFMA tile order the fast decode and prefill kernels read
+(``ExpertStore.from_safetensors(..., tiled=True)``); GGUF experts keep their ggml bytes.
 """
 from __future__ import annotations
+
+import itertools
+import math
 
 import torch
 
@@ -16,26 +21,24 @@ def _element_size(dtype: torch.dtype) -> int:
 
 
 class TensorLayout:
-    """Describes how named tensors are packed into a flat byte buffer."""
+    """Byte map of one packed expert slot: each named tensor's (offset, size) in the slot,
+    tensors placed back to back in the order of ``tensor_specs``."""
 
     def __init__(self, tensor_specs: dict[str, tuple[tuple[int, ...], torch.dtype]]):
         self.specs = tensor_specs
-        self.offsets: dict[str, int] = {}
-        self.sizes: dict[str, int] = {}
-        offset = 0
-        for name, (shape, dtype) in tensor_specs.items():
-            n = 1
-            for d in shape:
-                n *= int(d)
-            nbytes = n * _element_size(dtype)
-            self.offsets[name] = offset
-            self.sizes[name] = nbytes
-            offset += nbytes
-        self.total_bytes = offset
+        names = list(tensor_specs)
+        sizes = [math.prod(int(d) for d in shape) * _element_size(dtype) for shape, dtype in tensor_specs.values()]
+        self.sizes: dict[str, int] = dict(zip(names, sizes))
+        self.offsets: dict[str, int] = dict(zip(names, itertools.accumulate([0] + sizes[:-1])))
+        self.total_bytes = sum(sizes)
 
     @staticmethod
     def from_tensors(tensors: dict[str, torch.Tensor]) -> "TensorLayout":
-        return TensorLayout({name: (tuple(t.shape), t.dtype) for name, t in tensors.items()})
+        """The layout that packs these tensors (their shapes and dtypes, in dict order)."""
+        specs = {}
+        for name, t in tensors.items():
+            specs[name] = (tuple(t.shape), t.dtype)
+        return TensorLayout(specs)
 
 
 def pack_tensors(dest: torch.Tensor, layout: TensorLayout, tensors: dict[str, torch.Tensor]) -> None:

@@ -65,11 +65,11 @@ class GGMLExpertForward:
         types = self._ggml_types
         if layer_idx >= 0 and layer_idx in getattr(self, "_layer_ggml_types", {}):
             types = self._layer_ggml_types[layer_idx]
-        if not self._silu:
-            raise NotImplementedError(f"GGUF experts use a SiLU gate; got {self._act_fn!r}")
         H = self._proj_shapes["gate"][0]
         h2 = h.reshape(-1, H)
-        if types["gate"] == types["up"]:
+        # a SiLU gate with equal gate/up types is the fused decode kernel; any other act_fn
+        # (or mixed gate/up types) runs the three GGUF matvecs with act_fn(gate) * up between
+        if self._silu and types["gate"] == types["up"]:
             L = self._layout(types, packed.numel())
             T = h2.shape[0]
             key = (h.device, T)
@@ -84,5 +84,6 @@ class GGMLExpertForward:
         d = packed[self._down_off : self._down_off + self._actual_bytes(ds, types["down"])]
         go = ops.gguf_matvec(h2, g, types["gate"], gs[1], gs[0], out_dtype=torch.float32)
         uo = ops.gguf_matvec(h2, u, types["up"], us[1], us[0], out_dtype=torch.float32)
-        hid = (torch.nn.functional.silu(go) * uo).to(h.dtype)
+        act = torch.nn.functional.silu if self._silu or self._act_fn is None else self._act_fn
+        hid = (act(go) * uo).to(h.dtype)
         return ops.gguf_matvec(hid, d, types["down"], ds[1], ds[0], out_dtype=h.dtype).reshape(h.shape)

@@ -35,19 +35,17 @@ def _check_ggml() -> bool:
 
 
 class GGMLLinear(nn.Module):
-    """Linear layer backed by raw Q8_0 / Q4_K / Q5_K / Q6_K bytes resident on the GPU."""
+    """An ``nn.Linear`` stand-in whose weight stays in its GGUF encoding (Q8_0 / Q4_K / Q5_K /
+    Q6_K bytes) on the GPU; every forward runs the HIP GGUF matvec on it."""
 
     def __init__(self, raw_bytes: bytes | torch.Tensor, ggml_type: int, out_features: int, in_features: int,
                  bias: torch.Tensor | None = None, device: torch.device | str = "cuda"):
         super().__init__()
-        if isinstance(raw_bytes, bytes):
-            self._qweight = torch.frombuffer(bytearray(raw_bytes), dtype=torch.uint8).to(device)
-        else:
-            self._qweight = raw_bytes.to(device)
-        self._ggml_type = ggml_type
-        self.out_features = out_features
-        self.in_features = in_features
-        self.bias = nn.Parameter(bias.to(device)) if bias is not None else None
+        data = raw_bytes if isinstance(raw_bytes, torch.Tensor) else torch.tensor(bytearray(raw_bytes), dtype=torch.uint8)
+        self._qweight = data.reshape(-1).to(device=device)
+        self._ggml_type = int(ggml_type)
+        self.out_features, self.in_features = int(out_features), int(in_features)
+        self.bias = None if bias is None else nn.Parameter(bias.to(device))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not _check_ggml():
@@ -89,5 +87,5 @@ def replace_linear_with_ggml(model: nn.Module, raw_weights: dict[str, tuple[byte
             bias = None
         setattr(parent, attr, GGMLLinear(raw, ggml_type, shape[0], shape[1], bias=bias, device=device))
         replaced += 1
-    logger.info("Replaced %d nn.Linear modules with GGMLLinear", replaced)
+    logger.info("GGMLLinear now backs %d linear layer(s)", replaced)
     return replaced
