@@ -3,19 +3,19 @@
 // weight stream. Every weight byte is read by contiguous 1 KB wave loads and fed to the
 // matrix cores as it arrives, still in fp4.
 //
-// Arithmetic. One 1 KB piece m of a 16-row tile is the B operand of one
-// v_mfma_f32_16x16x128_f8f6f4 (fp4 e2m1, no conversion): lane 16q+i holds block 4m+q of
-// row i, which is exactly that instruction's fp4 operand layout (column i, K = 32q..32q+31).
-// The A operand carries the activation vector v (x for gate_up, h for down) in fp8 e4m3,
-// block-diagonally: A row 4r+b holds term r of v restricted to block b of the piece (zero
-// elsewhere), so D[4r+b][i] = sum over block b of e2m1(i, k) * term_r(k), one partial dot per
-// (row, block) with the block scale not yet applied. The lane holding D[4r+b][i] multiplies
-// it by the e8m0 scale of (row i, block 4m+b) and accumulates. The activation is split into
-// two e4m3 terms, v*s = hi + lo, with hi = e4m3(v*s) and lo = e4m3(v*s - hi): for a bf16 v
-// the pair is exact (hi keeps 4 significant bits, lo the remaining 4) unless v is more than
-// 2^10 below the scaled maximum, so the products are those of the reference's bf16
-// arithmetic. The scale s is a power of two: per token for x (from max |x|), fixed for h
-// (|h| <= (limit + 1) * limit after the clamped SwiGLU).
+// Arithmetic. One 1 KB piece m of a 16-row tile is the fp4 (e2m1) B operand of one
+// v_mfma_scale_f32_16x16x128_f8f6f4, as loaded: lane 16q+i holds block 4m+q of row i, which
+// is exactly that instruction's fp4 operand layout (column i, K = 32q..32q+31), and byte m%4
+// of the lane's scale word m/4 is the e8m0 scale of that block, which the instruction takes
+// as the lane's B scale: the block scales are applied by the matrix core. The A operand
+// carries the activation vector v (x for gate_up, h for down) as two fp8 e4m3 terms in
+// rows 0 and 1 (rows 2..15 zero), so D[r][i] accumulates sum_k W[i][k] term_r(k) over the
+// pieces and lane i adds rows 0 and 1 at the end. The two terms are v*s = hi + lo with
+// hi = e4m3(v*s) and lo = e4m3(v*s - hi): for a bf16 v the pair is exact (hi keeps 4
+// significant bits, lo the remaining 4) unless v is more than 2^10 below the scaled
+// maximum, so the products are those of the reference's bf16 arithmetic. The scale s is a
+// power of two: per token for x (from max |x|), fixed for h (|h| <= (limit + 1) * limit
+// after the clamped SwiGLU).
 //
 // Launch 1 (gate_up): workgroup (kb, pair) multiplies 64 gate_up rows of the pair's expert
 //   (one 16-row tile per wave) by x of the pair's token; bias, clamped SwiGLU, h rounded to
