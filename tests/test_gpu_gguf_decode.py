@@ -100,7 +100,7 @@ def test_gguf_decode_wide_activations(x_dtype):
 @pytest.mark.parametrize("T", [8, 9])
 @pytest.mark.parametrize("gtype,x_dtype", [(8, torch.float32), (13, torch.float16), (14, torch.bfloat16)])
 def test_gguf_matvec_token_limit(T, gtype, x_dtype):
-    """T = 8 is the last count on the super-block matvec, T = 9 runs the row kernel: both
+    """T = 8 is the last count on the streaming matvec, T = 9 runs the row kernel: both
     match the fp32 oracle, in every activation dtype."""
     rng = np.random.default_rng(T * 100 + gtype)
     K, N = 1024, 96
@@ -111,8 +111,9 @@ def test_gguf_matvec_token_limit(T, gtype, x_dtype):
     y = ops.gguf_matvec(xt.cuda(), dev_u8(data), gtype, N, K, out_dtype=torch.float32)
     assert y.shape == (T, N)
     cos, rel = metrics(to_f32(y), ref)
-    bar = 1e-4 if x_dtype != torch.bfloat16 else 1e-5  # hi/lo staging keeps fp32-level accuracy
-    assert cos > 0.999999 and rel < bar, (cos, rel)
+    # the activations enter the dot products as two int8 terms per 32-value block (about 16
+    # significant bits relative to the block maximum): fp32-level accuracy, not bit-exact bf16
+    assert cos > 0.999999 and rel < 1e-4, (cos, rel)
 
 
 def test_gguf_decode_routed_workload4_full_size():

@@ -1,0 +1,439 @@
+// GGUF matvec (y = deq(W) x for up to 8 tokens, Q8_0 / Q4_K / Q5_K / Q6_K) as a weight
+// stream of 32-value sub-blocks.
+//
+// Work unit: one lane, one 32-value sub-block of a row (a Q8_0 block, or one eighth of a
+// K-quant super-block). A row of K values has C = K / 32 sub-blocks and no sub-block
+// straddles two rows, so a lane's work is always (row, column c). Lanes keep their columns
+// for the whole launch: lane l takes column l (and l + 64 when C > 64), or, when C < 64,
+// column l % C of every (64 / C)-th row, so the activations of a lane's columns sit in its
+// registers for the whole stream.
+//
+// Activations: every workgroup quantises its token's vector once, per 32-value block, as two
+// int8 terms, x ~= s (hi + lo / 254) with s = max|x| / 127: hi = rint(x / s), lo =
+// rint((x / s - hi) 254). |x - s (hi + lo / 254)| <= max|x| / (127 * 508) = 1.6e-5 max|x|:
+// about 16 significant bits relative to the block's largest value. The exact sums of the
+// block (and of its 16-value halves, for Q6_K) come along in fp32.
+// Dot products: a sub-block's codes become 32 bytes (4 per dword; Q8_0 codes are already
+// int8, the K-quants' 4..6-bit codes are unpacked to 0..63), v_dot4_i32_i8 sums codes x hi
+// and codes x lo in int32 (exact), and the scales are applied once per sub-block:
+//   Q4_K / Q5_K: d sc s (ihi + ilo / 254) - dmin m sum32(x)
+//   Q6_K: d sum_h sc_h (s (ihi_h + ilo_h / 254) - 32 sum16_h(x))   (codes q + 32)
+//   Q8_0: d s (ihi + ilo / 254)
+// Loads: the token's activations (each wave a quarter) and then the wave's rows of
+// super-blocks are copied into LDS with contiguous buffer-to-LDS transfers; the wave waits
+// for its activations with the weights still in flight, and starts on a row as soon as the
+// transfers that hold it are complete (an exact vmcnt per row).
+//
+// Workgroup = 4 waves of one token, wave = RM rows.
+//
+// Semantics: tinyserve/gguf_dequant_torch.py:101-249 (formats), tinyserve/csrc/ggml_ops.cu:
+// 461-569 (y = deq(W) x in fp32).
+#include "fused_common.h"
+#include "mfma_tile.h"
+#include "gguf_dot.h"
+
+namespace tsa {
+namespace {
+
+constexpr int GS_RD = 8;        // rows per wave, at most
+constexpr int GS_ITEMS = 4;     // activation quarters (8 values) a thread quantises, at most
+constexpr int XQ_BYTES = 80;    // a quantised block in LDS: hi[8], lo[8] dwords, s, sum32, sum16 x 2
+
+// A lane's quantised activation block.
+struct XQ {
+    uint32_t h[8], l[8];
+    float s, s32, s16a, s16b;
+};
+
+__device__ __forceinline__ XQ xq_read(const uint8_t* p) {
+    XQ x;
+    const u32x4 a = ld16u(p), b = ld16u(p + 16), c = ld16u(p + 32), d = ld16u(p + 48), e = ld16u(p + 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x.h[i] = a[i];
+        x.h[4 + i] = b[i];
+        x.l[i] = c[i];
+        x.l[4 + i] = d[i];
+    }
+    x.s = __uint_as_float(e[0]);
+    x.s32 = __uint_as_float(e[1]);
+    x.s16a = __uint_as_float(e[2]);
+    x.s16b = __uint_as_float(e[3]);
+    return x;
+}
+
+// 8 raw activation values of one quarter-block, as loaded (bf16 / fp16: 4 dwords; fp32: 8).
+struct XRaw {
+    uint32_t w[8];
+};
+__device__ __forceinline__ void xraw_values(const XRaw& r, int dtype, float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (dtype == TSA_F32) {
+            f[i] = __uint_as_float(r.w[i]);
+        } else {
+            const uint32_t b = (r.w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            f[i] = dtype == TSA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+        }
+    }
+}
+
+// The activation items of one workgroup: nvec vectors of C blocks, item i = (vector i /
+// (4C), block (i % 4C) / 4, quarter i % 4) for i = tid + nthr m, quantised by gs_quant.
+struct XItems {
+    XRaw r[GS_ITEMS];
+};
+// The items, read from a raw copy of the vectors in LDS (vectors back to back).
+__device__ __forceinline__ void gs_items_lds(XItems& it, const uint8_t* raw, int dtype, int nvec, int C, int tid,
+                                             int nthr) {
+    const int total = nvec * 4 * C, es = dtype == TSA_F32 ? 4 : 2;
+#pragma unroll
+    for (int m = 0; m < GS_ITEMS; ++m) {
+        const int i = tid + nthr * m;
+        const int ii = i < total ? i : 0;
+        const uint8_t* q = raw + 8 * es * ii;  // vectors back to back: item ii starts at value 8 ii
+        const u32x4 a = ld16u(q);
+        const u32x4 b = es == 4 ? ld16u(q + 16) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            it.r[m].w[e] = a[e];
+            it.r[m].w[4 + e] = b[e];
+        }
+    }
+}
+
+// Quantises the loaded items into dst (block b = v C + c at dst + XQ_BYTES b). The four
+// threads of a block are four consecutive lanes (4C items per vector): their maximum and
+// sums come from DPP quad exchanges.
+__device__ __forceinline__ void gs_quant(const XItems& it, uint8_t* dst, int dtype, int nvec, int C, int tid,
+                                         int nthr) {
+    const int total = nvec * 4 * C;
+#pragma unroll
+    for (int m = 0; m < GS_ITEMS; ++m) {
+        const int i = tid + nthr * m;
+        if (nthr * m >= total) break;  // workgroup-uniform: no thread has this item
+        float f[8];
+        xraw_values(it.r[m], dtype, f);
+        float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(f[e]));
+            sum += f[e];
+        }
+        amax = __builtin_fmaxf(amax, dpp_f<0xB1, 0xF, 0xF>(amax, 0.0f));  // quad_perm [1,0,3,2]
+        amax = __builtin_fmaxf(amax, dpp_f<0x4E, 0xF, 0xF>(amax, 0.0f));  // quad_perm [2,3,0,1]
+        const float s16 = sum + dpp_f<0xB1, 0xF, 0xF>(sum, 0.0f);
+        const float s32 = s16 + dpp_f<0x4E, 0xF, 0xF>(s16, 0.0f);
+        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float u = f[e] * inv;
+            const float hi = __builtin_rintf(u);
+            const float lo = __builtin_rintf((u - hi) * 254.0f);
+            hw[e >> 2] |= ((uint32_t)(int)hi & 0xFFu) << (8 * (e & 3));
+            lw[e >> 2] |= ((uint32_t)(int)lo & 0xFFu) << (8 * (e & 3));
+        }
+        if (i < total) {
+            const int b = i >> 2, q = i & 3;
+            uint8_t* p = dst + XQ_BYTES * b;
+            *reinterpret_cast<uint2*>(p + 8 * q) = make_uint2(hw[0], hw[1]);
+            *reinterpret_cast<uint2*>(p + 32 + 8 * q) = make_uint2(lw[0], lw[1]);
+            if (q == 0) *reinterpret_cast<float2*>(p + 64) = make_float2(amax * (1.0f / 127.0f), s32);
+            if ((q & 1) == 0) *reinterpret_cast<float*>(p + 72 + 2 * q) = s16;  // q 0: first half, q 2: second
+        }
+    }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// sum over the block of code x activation, as s (hi + lo / 254), for the 8 code words q
+// (dwords i0 .. i1 - 1).
+template <int I0, int I1>
+__device__ __forceinline__ float qdot(const uint32_t (&q)[8], const XQ& x) {
+    int ih = 0, il = 0;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+        ih = sdot4(q[i], x.h[i], ih);
+        il = sdot4(q[i], x.l[i], il);
+    }
+    return x.s * ((float)ih + (float)il * (1.0f / 254.0f));
+}
+
+// k_scale_min for a sub-block index j that differs between lanes: both forms from the same
+// three bytes, then a select (no divergent branch).
+__device__ __forceinline__ void k_scale_min_lanes(const uint32_t s[3], int j, uint32_t& sc, uint32_t& m) {
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t b0 = __builtin_amdgcn_ubfe(s[0], sh, 8), b1 = __builtin_amdgcn_ubfe(s[1], sh, 8);
+    const uint32_t b2 = __builtin_amdgcn_ubfe(s[2], sh, 8);
+    const bool lo = j < 4;
+    sc = lo ? (b0 & 63u) : ((b2 & 15u) | ((b0 >> 6) << 4));
+    m = lo ? (b1 & 63u) : ((b2 >> 4) | ((b1 >> 6) << 4));
+}
+
+// Sub-block j (0..7; 0 for Q8_0) of the super-block (block) at p in LDS, dotted with x.
+template <int TY>
+__device__ __forceinline__ float sb_dot(const uint8_t* p, int j, const XQ& x) {
+    uint32_t q[8];
+    if constexpr (TY == 8) {
+        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+        const u32x4 a = ld16u(p + 2), b = ld16u(p + 18);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = a[i];
+            q[4 + i] = b[i];
+        }
+        return d * qdot<0, 8>(q, x);
+    } else if constexpr (TY == 12 || TY == 13) {
+        constexpr int QS = TY == 12 ? 16 : 48;
+        const u32x4 hdr = ld16u(p);
+        const u32x4 a = ld16u(p + QS + 32 * (j >> 1)), b = ld16u(p + QS + 32 * (j >> 1) + 16);
+        const int sh = 4 * (j & 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = (a[i] >> sh) & 0x0F0F0F0Fu;
+            q[4 + i] = (b[i] >> sh) & 0x0F0F0F0Fu;
+        }
+        if constexpr (TY == 13) {
+            const u32x4 ha = ld16u(p + 16), hb = ld16u(p + 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                q[i] |= ((ha[i] >> j) & 0x01010101u) << 4;
+                q[4 + i] |= ((hb[i] >> j) & 0x01010101u) << 4;
+            }
+        }
+        const float d = f16_bits_to_f32(hdr[0] & 0xFFFFu), dmin = f16_bits_to_f32(hdr[0] >> 16);
+        const uint32_t s[3] = {hdr[1], hdr[2], hdr[3]};
+        uint32_t sc, m;
+        k_scale_min_lanes(s, j, sc, m);
+        return d * (float)sc * qdot<0, 8>(q, x) - dmin * (float)m * x.s32;
+    } else {  // Q6_K: half h = j / 4, quarter t = j % 4 of it
+        const int h = j >> 2, t = j & 3;
+        const u32x4 la = ld16u(p + 64 * h + 32 * (t & 1)), lb = ld16u(p + 64 * h + 32 * (t & 1) + 16);
+        const u32x4 ha = ld16u(p + 128 + 32 * h), hb = ld16u(p + 144 + 32 * h);
+        const int shl = 4 * (t >> 1), shh = 2 * t;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = ((la[i] >> shl) & 0x0F0F0F0Fu) | (((ha[i] >> shh) & 0x03030303u) << 4);
+            q[4 + i] = ((lb[i] >> shl) & 0x0F0F0F0Fu) | (((hb[i] >> shh) & 0x03030303u) << 4);
+        }
+        const uint32_t scw = *reinterpret_cast<const uint16_t*>(p + 192 + 2 * j);
+        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 208));
+        const float sc0 = (float)(int8_t)(scw & 0xFFu), sc1 = (float)(int8_t)(scw >> 8);
+        return d * (sc0 * (qdot<0, 4>(q, x) - 32.0f * x.s16a) + sc1 * (qdot<4, 8>(q, x) - 32.0f * x.s16b));
+    }
+}
+
+template <int TY> struct GsType;
+template <> struct GsType<8>  { static constexpr uint32_t SB = 34,  SPB = 1; };
+template <> struct GsType<12> { static constexpr uint32_t SB = 144, SPB = 8; };
+template <> struct GsType<13> { static constexpr uint32_t SB = 176, SPB = 8; };
+template <> struct GsType<14> { static constexpr uint32_t SB = 210, SPB = 8; };
+
+// A wave's staged range of one matrix: the super-blocks holding sub-blocks [f0, f1).
+struct Range {
+    uint32_t s0;     // first super-block
+    uint32_t shift;  // the first super-block's offset in the LDS area (its address % 16)
+    uint32_t bytes;  // bytes transferred (whole 16-byte chunks)
+};
+template <int TY>
+__device__ __forceinline__ Range range_of(uint32_t off, uint32_t f0, uint32_t f1) {
+    using G = GsType<TY>;
+    Range r;
+    r.s0 = f0 / G::SPB;
+    const uint32_t s1 = (f1 + G::SPB - 1) / G::SPB;
+    const uint32_t first = off + r.s0 * G::SB;
+    r.shift = first & 15u;
+    r.bytes = ((s1 - r.s0) * G::SB + r.shift + 15u) / 16u * 16u;
+    return r;
+}
+// 1 KB transfers of the range that hold the sub-blocks before f_end.
+template <int TY>
+__device__ __forceinline__ uint32_t chunks_until(const Range& r, uint32_t f_end) {
+    using G = GsType<TY>;
+    const uint32_t s_end = (f_end + G::SPB - 1) / G::SPB;
+    return ((s_end - r.s0) * G::SB + r.shift + 1023u) / 1024u;
+}
+__device__ __forceinline__ uint32_t chunks(const Range& r) { return (r.bytes + 1023u) / 1024u; }
+
+// Waits until at most n of this wave's loads are outstanding (n above 31: 31, stricter).
+#define GS_WAIT_CASE(n) \
+    case n: asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); break;
+__device__ __forceinline__ void gs_wait(int n) {
+    switch (n) {
+        GS_WAIT_CASE(0) GS_WAIT_CASE(1) GS_WAIT_CASE(2) GS_WAIT_CASE(3) GS_WAIT_CASE(4) GS_WAIT_CASE(5)
+        GS_WAIT_CASE(6) GS_WAIT_CASE(7) GS_WAIT_CASE(8) GS_WAIT_CASE(9) GS_WAIT_CASE(10) GS_WAIT_CASE(11)
+        GS_WAIT_CASE(12) GS_WAIT_CASE(13) GS_WAIT_CASE(14) GS_WAIT_CASE(15) GS_WAIT_CASE(16) GS_WAIT_CASE(17)
+        GS_WAIT_CASE(18) GS_WAIT_CASE(19) GS_WAIT_CASE(20) GS_WAIT_CASE(21) GS_WAIT_CASE(22) GS_WAIT_CASE(23)
+        GS_WAIT_CASE(24) GS_WAIT_CASE(25) GS_WAIT_CASE(26) GS_WAIT_CASE(27) GS_WAIT_CASE(28) GS_WAIT_CASE(29)
+        GS_WAIT_CASE(30)
+        default: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+#undef GS_WAIT_CASE
+
+// A lane's place in a stream of rows of C sub-blocks: its columns c0 (and c0 + 64 when
+// two), its row group g of G (rows g, g + G, ...), and whether it has any column.
+struct Lanes {
+    int c0, ncol, g, G;
+};
+__device__ __forceinline__ Lanes lanes_of(int C, int lane) {
+    Lanes m;
+    if (C >= 64) {
+        m.c0 = lane;
+        m.ncol = lane + 64 < C ? 2 : 1;
+        m.g = 0;
+        m.G = 1;
+    } else {
+        m.G = 64 / C;
+        m.g = lane / C;
+        m.c0 = lane - m.g * C;
+        m.ncol = m.g < m.G ? 1 : 0;
+    }
+    return m;
+}
+
+template <int N>
+__device__ __forceinline__ void acc_put(float (&acc)[N], int r, float v) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (r == i) acc[i] += v;
+}
+
+struct GsMvParams {
+    const uint8_t* w;
+    uint32_t w_records;
+    const void* x;
+    uint32_t x_records;  // bytes of x
+    int x_dtype;
+    void* y;
+    int y_dtype;
+    int N, K, rm;
+    int xq_off, xraw_off, raw_off, raw_stride;
+};
+
+template <int TY>
+__global__ void __launch_bounds__(256) gs_matvec_kernel(GsMvParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    using G = GsType<TY>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const int K = p.K, N = p.N, C = K / 32, t = blockIdx.y;
+    const int n0 = ((int)blockIdx.x * 4 + wave) * p.rm;
+    const int nr = n0 >= N ? 0 : (N - n0 < p.rm ? N - n0 : p.rm);
+    uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
+    const uint32_t f0 = (uint32_t)n0 * C, f1 = (uint32_t)(n0 + nr) * C;
+    const Range rw = range_of<TY>(0u, f0, f1);
+    // the token's activations (each wave a quarter) and then the weight rows, all as
+    // buffer-to-LDS copies, so the activations can be waited for with the weights still out
+    const uint32_t xbytes = (uint32_t)K * (p.x_dtype == TSA_F32 ? 4u : 2u), xq4 = xbytes / 4;  // multiple of 16
+    gq_stage_raw(static_cast<const uint8_t*>(p.x), p.x_records, (uint32_t)t * xbytes + wave * xq4, xq4,
+                 (uint32_t)reinterpret_cast<uintptr_t>(smem + p.xraw_off) + wave * xq4, lane);
+    if (nr > 0)
+        gq_stage_raw(p.w, p.w_records, rw.s0 * G::SB - rw.shift, rw.bytes, (uint32_t)reinterpret_cast<uintptr_t>(rbuf),
+                     lane);
+    const int total = nr > 0 ? (int)chunks(rw) : 0;
+    gs_wait(total);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave's quarter of the activations is in LDS
+    XItems xi;
+    gs_items_lds(xi, smem + p.xraw_off, p.x_dtype, 1, C, tid, 256);
+    gs_quant(xi, smem + p.xq_off, p.x_dtype, 1, C, tid, 256);
+    __syncthreads();
+    if (nr == 0) return;
+    const Lanes ln = lanes_of(C, lane);
+    XQ x0 = xq_read(smem + p.xq_off + XQ_BYTES * ln.c0), x1 = x0;
+    if (ln.ncol > 1) x1 = xq_read(smem + p.xq_off + XQ_BYTES * (ln.c0 + 64));
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    for (int r0 = 0; r0 < nr; r0 += ln.G) {
+        const int rmax = r0 + ln.G - 1 < nr ? r0 + ln.G - 1 : nr - 1;
+        gs_wait(total - (int)chunks_until<TY>(rw, f0 + (uint32_t)(rmax + 1) * C));
+        const int r = r0 + ln.g;
+        if (ln.ncol == 0 || r >= nr) continue;
+        const uint8_t* area = rbuf + rw.shift;
+        float part = 0.0f;
+        {
+            const uint32_t f = f0 + (uint32_t)r * C + ln.c0;
+            part += sb_dot<TY>(area + (f / G::SPB - rw.s0) * G::SB, (int)(f % G::SPB), x0);
+        }
+        if (ln.ncol > 1) {
+            const uint32_t f = f0 + (uint32_t)r * C + ln.c0 + 64;
+            part += sb_dot<TY>(area + (f / G::SPB - rw.s0) * G::SB, (int)(f % G::SPB), x1);
+        }
+        acc_put(acc, r, part);
+    }
+    const float tot = wave_sum_rows<8>(acc, lane);
+    const int r = lane >> 3;
+    if ((lane & 7) == 0 && r < nr) store_out(p.y, p.y_dtype, (int64_t)t * N + n0 + r, tot);
+}
+
+const void* gs_pick(int t) {
+    switch (t) {
+        case 8: return reinterpret_cast<const void*>(&gs_matvec_kernel<8>);
+        case 12: return reinterpret_cast<const void*>(&gs_matvec_kernel<12>);
+        case 13: return reinterpret_cast<const void*>(&gs_matvec_kernel<13>);
+        case 14: return reinterpret_cast<const void*>(&gs_matvec_kernel<14>);
+    }
+    return nullptr;
+}
+
+uint32_t gs_sb(int t) { return t == 8 ? 34u : t == 12 ? 144u : t == 13 ? 176u : 210u; }
+uint32_t gs_spb(int t) { return t == 8 ? 1u : 8u; }
+
+// LDS bytes of a staged range of `rows` rows of C sub-blocks (any alignment of the first
+// row): the super-blocks they can touch, plus the 16-byte alignment slack.
+size_t gs_raw_bytes(int t, int rows, int C) {
+    const uint32_t spb = gs_spb(t);
+    const uint32_t nsb = ((uint32_t)rows * C + spb - 1) / spb + 1;
+    return ((size_t)nsb * gs_sb(t) + 15 + 15) / 16 * 16;
+}
+
+}  // namespace
+
+// Whether the sub-block stream matvec covers a matrix: "" if it does.
+const char* gs_unsupported(int type, int64_t K) {
+    if (!gs_pick(type)) return "unsupported ggml type";
+    if (K % 32) return "K must be a multiple of 32";
+    if (K > 4096) return "K above 4096";
+    return "";
+}
+
+int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T, int64_t K, void* y,
+              int y_dtype, int64_t N, hipStream_t st) {
+    GsMvParams p{};
+    p.w = w;
+    p.w_records = (uint32_t)(w_bytes < 0xFFFFFFF0ll ? w_bytes : 0xFFFFFFF0ll);
+    p.x = x;
+    p.x_dtype = x_dtype;
+    p.y = y;
+    p.y_dtype = y_dtype;
+    p.N = (int)N;
+    p.K = (int)K;
+    const int C = (int)(K / 32), GM = C >= 64 ? 1 : 64 / C, cus = num_cus();
+    p.rm = GS_RD / GM * GM;
+    if (p.rm == 0) p.rm = GM;
+    if (p.rm > GS_RD) p.rm = GS_RD;
+    while (p.rm > GM && (double)((N + p.rm - 1) / p.rm) * T < 8.0 * cus) p.rm -= GM;
+    const size_t xq = (size_t)XQ_BYTES * C, xraw = (size_t)K * (x_dtype == TSA_F32 ? 4 : 2);
+    const size_t raw = gs_raw_bytes(type, p.rm, C);
+    const size_t lds = xq + xraw + 4 * raw;
+    TSA_REQUIRE(lds <= 160 * 1024, TSA_ERR_SHAPE, "GGUF matvec: LDS %zu bytes", lds);
+    const int64_t xb = T * (int64_t)xraw;
+    p.x_records = (uint32_t)(xb < 0xFFFFFFF0ll ? xb : 0xFFFFFFF0ll);
+    p.xq_off = 0;
+    p.xraw_off = (int)xq;
+    p.raw_off = (int)(xq + xraw);
+    p.raw_stride = (int)raw;
+    const void* fn = gs_pick(type);
+    if (lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    void* args[] = {&p};
+    const dim3 grid((unsigned)((N + 4 * p.rm - 1) / (4 * p.rm)), (unsigned)T);
+    TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(256), args, lds, st));
+    return TSA_OK;
+}
+
+}  // namespace tsa

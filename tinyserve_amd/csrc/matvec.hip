@@ -142,6 +142,9 @@ namespace tsa {
 const char* gq_matvec_unsupported(int type, const void* w, int64_t T, int64_t K, int64_t N, int x_dtype);
 int gq_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T, int64_t K, void* y,
               int y_dtype, int64_t N, hipStream_t st);
+const char* gs_unsupported(int type, int64_t K);
+int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T, int64_t K, void* y,
+              int y_dtype, int64_t N, hipStream_t st);
 }  // namespace tsa
 
 using namespace tsa;
@@ -173,6 +176,11 @@ extern "C" int tsa_gguf_matvec(int ggml_type, const void* w, int64_t w_bytes, co
     TSA_REQUIRE(w && x && y, TSA_ERR_INVALID_ARG, "null pointer");
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     hipStream_t st = as_stream(stream);
+    // the sub-block stream (moe_decode_gs.hip) first, then the super-block matvec
+    if (T <= GQ_MATVEC_MAX_T && !*gs_unsupported(ggml_type, K) && (reinterpret_cast<uintptr_t>(w) & 1) == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15) == 0 && N * K < ((int64_t)1 << 31) &&
+        T * K * (x_dtype == TSA_F32 ? 4 : 2) < ((int64_t)1 << 32) - 16)
+        return gs_matvec(ggml_type, wb, w_bytes, x, x_dtype, T, K, y, y_dtype, N, st);
     if (T <= GQ_MATVEC_MAX_T && !*gq_matvec_unsupported(ggml_type, w, T, K, N, x_dtype))
         return gq_matvec(ggml_type, wb, w_bytes, x, x_dtype, T, K, y, y_dtype, N, st);
     const bool a16 = (reinterpret_cast<uintptr_t>(w) & 15) == 0, a2 = (reinterpret_cast<uintptr_t>(w) & 1) == 0;
