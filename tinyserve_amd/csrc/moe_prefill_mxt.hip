@@ -55,7 +55,8 @@ constexpr int PF_WBYTES = (PF_BN / 16) * 1024;    // a piece of MXFP4 weights: 1
 constexpr int PF_SBYTES = (PF_BN / 16) * 256;     // one scale word per lane of every row tile: 4 KB
 constexpr int PF_WOFF = PF_XST * PF_XBYTES;
 constexpr int PF_SOFF = PF_WOFF + PF_WST * PF_WBYTES;
-constexpr int PF_LDS = PF_SOFF + 2 * PF_SBYTES;   // 152 KB
+constexpr int PF_BIAS_OFF = PF_SOFF + 2 * PF_SBYTES;  // the tile's 256 bias values (up to 1 KB)
+constexpr int PF_LDS = PF_BIAS_OFF + 1024;            // 153 KB
 constexpr int PF_CTR_STRIDE = 32;                 // ints between per-XCD tile counters (one 128-byte line each)
 constexpr int PF_CTR_INTS = 2 * 8 * PF_CTR_STRIDE;  // gate_up's 8 counters, then down's
 constexpr int PF_HS_GU = 272;   // LDS row stride (bytes) of the staged gate_up outputs: 128 h + 16 B
@@ -405,19 +406,14 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
         nsub = nsub < 0 ? 0 : (nsub > 2 ? 2 : nsub);
         const bool active = rows_live && nsub > 0;
 
-        // The epilogue's bias, loaded now so its latency is hidden by the K loop (rows past N
-        // read zero: the buffer range check).
-        u32x4 braw[2][4];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int u = 0; u < 4; ++u) braw[rb][u] = u32x4{0u, 0u, 0u, 0u};
-        if (active && p.b_off >= 0) {
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    braw[rb][u] = bias_raw(base + p.b_off, p.L.bias_dtype, N, 16 * rt0 + 32 * rb + 8 * u + 4 * g);
+        // The tile's bias, copied into LDS now (wave 0, before the K loop's loads, so that every
+        // later wait covers it) and read by the epilogue; rows past N read zero (the buffer
+        // range check).
+        const int bes = p.L.bias_dtype == TSA_F32 ? 4 : 2;
+        if (wave == 0 && p.b_off >= 0) {
+            const int64_t brows = N - 16 * rtw;
+            const v4i br = buf_desc(base + p.b_off + (int64_t)16 * rtw * bes, (uint32_t)(brows > 0 ? brows * bes : 0));
+            for (int i = 0; i < bes; ++i) pf_dma4(br, 256 * i + 4 * lane, lds0 + PF_BIAS_OFF + 256 * i);
         }
 
         v16f acc[2][2];
@@ -448,7 +444,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1) pf_gemm_kernel(PfGemm p) {
                 for (int u = 0; u < 4; ++u) {
                     const int c = 64 * wn + 32 * rb + 8 * u + 4 * g;  // weight row within the workgroup tile
                     if (16 * rtw + c >= N) continue;  // N % 32 == 16: the block's second row tile is past N
-                    const v4f bias = p.b_off >= 0 ? bias_value(braw[rb][u], p.L.bias_dtype) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                    const v4f bias = p.b_off >= 0 ? bias_value(*reinterpret_cast<const u32x4*>(smem + PF_BIAS_OFF + c * bes),
+                                                               p.L.bias_dtype)
+                                                  : v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int b = 0; b < 2; ++b) {
                         const int tk = 64 * wt + 32 * b + rr;
