@@ -79,7 +79,7 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 
 # The kernels of one step of each decode workload (name substrings; "3c" = workload 3 with
 # the experts in checkpoint order).
-STEP_KERNELS = {"1": ("gq_matvec_kernel",), "2": ("gq_phase_a", "gq_phase_b"),
+STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gq_phase_a", "gq_phase_b"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
                 "4": ("gq_phase_a", "gq_phase_b")}
 
@@ -542,7 +542,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {1: "gguf q8_0 weights, fp32 activations (bf16 hi/lo pairs), fp32 accumulate",
+        "dtype": {1: "gguf q8_0 weights, fp32 activations (int8 hi/lo terms per 32 values), int32 dots, fp32 accumulate",
                   2: "gguf q4_k/q6_k weights, bf16 activations, fp32 accumulate",
                   3: "mxfp4 weights (e2m1 x e8m0), bf16 activations, fp32 accumulate",
                   4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate"}[args.workload],

@@ -9,7 +9,7 @@
 // registers for the whole stream.
 //
 // Activations: every workgroup quantises its token's vector once, per 32-value block, as two
-// int8 terms, x ~= s (hi + lo / 254) with s = max|x| / 127: hi = rint(x / s), lo =
+// int8 terms, x ~= s (hi + lo / 254) with s = max|x| / 127 (at least 2^-126): hi = rint(x / s), lo =
 // rint((x / s - hi) 254). |x - s (hi + lo / 254)| <= max|x| / (127 * 508) = 1.6e-5 max|x|:
 // about 16 significant bits relative to the block's largest value. The exact sums of the
 // block (and of its 16-value halves, for Q6_K) come along in fp32.
@@ -19,12 +19,12 @@
 //   Q4_K / Q5_K: d sc s (ihi + ilo / 254) - dmin m sum32(x)
 //   Q6_K: d sum_h sc_h (s (ihi_h + ilo_h / 254) - 32 sum16_h(x))   (codes q + 32)
 //   Q8_0: d s (ihi + ilo / 254)
-// Loads: the token's activations (each wave a quarter) and then the wave's rows of
+// Loads: the token's activations (1 KB pieces dealt round the waves) and then the wave's rows of
 // super-blocks are copied into LDS with contiguous buffer-to-LDS transfers; the wave waits
 // for its activations with the weights still in flight, and starts on a row as soon as the
 // transfers that hold it are complete (an exact vmcnt per row).
 //
-// Workgroup = 4 waves of one token, wave = RM rows.
+// Workgroup = 4..16 waves of one token (about one workgroup per CU), wave = RM rows.
 //
 // Semantics: tinyserve/gguf_dequant_torch.py:101-249 (formats), tinyserve/csrc/ggml_ops.cu:
 // 461-569 (y = deq(W) x in fp32).
@@ -36,7 +36,9 @@ namespace tsa {
 namespace {
 
 constexpr int GS_RD = 8;        // rows per wave, at most
-constexpr int GS_ITEMS = 4;     // activation quarters (8 values) a thread quantises, at most
+constexpr int GS_MIN_WAVES = 4;  // waves per workgroup, at least (4 K / 32 <= 2 * 64 * 4 items)
+constexpr int GS_MAX_WAVES = 16;
+constexpr int GS_ITEMS = 2;     // activation quarters (8 values) a thread quantises, at most
 constexpr int XQ_BYTES = 80;    // a quantised block in LDS: hi[8], lo[8] dwords, s, sum32, sum16 x 2
 
 // A lane's quantised activation block.
@@ -124,22 +126,35 @@ __device__ __forceinline__ void gs_quant(const XItems& it, uint8_t* dst, int dty
         amax = __builtin_fmaxf(amax, dpp_f<0x4E, 0xF, 0xF>(amax, 0.0f));  // quad_perm [2,3,0,1]
         const float s16 = sum + dpp_f<0xB1, 0xF, 0xF>(sum, 0.0f);
         const float s32 = s16 + dpp_f<0x4E, 0xF, 0xF>(s16, 0.0f);
-        const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-        uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+        // s = amax / 127 (at least 2^-126, so 1/s stays finite; an all-zero block then codes
+        // as zeros); u = f / s in [-127, 127]. Adding 1.5 * 2^23 rounds u to the nearest
+        // integer (ties to even) in the low mantissa bits, whose low byte is the two's
+        // complement code; the remainder u - hi in [-1/2, 1/2] gives lo = rint(254 (u - hi)).
+        const float s = __builtin_fmaxf(amax * (1.0f / 127.0f), 0x1p-126f);
+        const float inv = __builtin_amdgcn_rcpf(s);
+        constexpr float RND = 0x1.8p23f;
+        uint32_t hb[8], lb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float u = f[e] * inv;
-            const float hi = __builtin_rintf(u);
-            const float lo = __builtin_rintf((u - hi) * 254.0f);
-            hw[e >> 2] |= ((uint32_t)(int)hi & 0xFFu) << (8 * (e & 3));
-            lw[e >> 2] |= ((uint32_t)(int)lo & 0xFFu) << (8 * (e & 3));
+            const float th = __builtin_fmaf(f[e], inv, RND);
+            const float r = __builtin_fmaf(f[e], inv, -(th - RND));
+            hb[e] = __float_as_uint(th);
+            lb[e] = __float_as_uint(__builtin_fmaf(r, 254.0f, RND));
+        }
+        uint32_t hw[2], lw[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // low bytes of four words -> one word (v_perm_b32)
+            hw[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(hb[4 * h + 3], hb[4 * h + 2], 0x0C0C0400u),
+                                          __builtin_amdgcn_perm(hb[4 * h + 1], hb[4 * h], 0x0C0C0400u), 0x05040100u);
+            lw[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(lb[4 * h + 3], lb[4 * h + 2], 0x0C0C0400u),
+                                          __builtin_amdgcn_perm(lb[4 * h + 1], lb[4 * h], 0x0C0C0400u), 0x05040100u);
         }
         if (i < total) {
             const int b = i >> 2, q = i & 3;
             uint8_t* p = dst + XQ_BYTES * b;
             *reinterpret_cast<uint2*>(p + 8 * q) = make_uint2(hw[0], hw[1]);
             *reinterpret_cast<uint2*>(p + 32 + 8 * q) = make_uint2(lw[0], lw[1]);
-            if (q == 0) *reinterpret_cast<float2*>(p + 64) = make_float2(amax * (1.0f / 127.0f), s32);
+            if (q == 0) *reinterpret_cast<float2*>(p + 64) = make_float2(s, s32);
             if ((q & 1) == 0) *reinterpret_cast<float*>(p + 72 + 2 * q) = s16;  // q 0: first half, q 2: second
         }
     }
@@ -316,31 +331,35 @@ struct GsMvParams {
 };
 
 template <int TY>
-__global__ void __launch_bounds__(256) gs_matvec_kernel(GsMvParams p) {
+__global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_matvec_kernel(GsMvParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     using G = GsType<TY>;
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const int K = p.K, N = p.N, C = K / 32, t = blockIdx.y;
-    const int n0 = ((int)blockIdx.x * 4 + wave) * p.rm;
+    const int nw = (int)(blockDim.x >> 6);
+    const int n0 = ((int)blockIdx.x * nw + wave) * p.rm;
     const int nr = n0 >= N ? 0 : (N - n0 < p.rm ? N - n0 : p.rm);
     uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
     const uint32_t f0 = (uint32_t)n0 * C, f1 = (uint32_t)(n0 + nr) * C;
     const Range rw = range_of<TY>(0u, f0, f1);
-    // the token's activations (each wave a quarter) and then the weight rows, all as
-    // buffer-to-LDS copies, so the activations can be waited for with the weights still out
-    const uint32_t xbytes = (uint32_t)K * (p.x_dtype == TSA_F32 ? 4u : 2u), xq4 = xbytes / 4;  // multiple of 16
-    gq_stage_raw(static_cast<const uint8_t*>(p.x), p.x_records, (uint32_t)t * xbytes + wave * xq4, xq4,
-                 (uint32_t)reinterpret_cast<uintptr_t>(smem + p.xraw_off) + wave * xq4, lane);
+    // the token's activations (1 KB pieces dealt round the waves) and then the weight rows,
+    // all as buffer-to-LDS copies, so the activations can be waited for with the weights
+    // still out
+    const uint32_t xbytes = (uint32_t)K * (p.x_dtype == TSA_F32 ? 4u : 2u);  // a multiple of 64
+    for (uint32_t c = 1024u * wave; c < xbytes; c += 1024u * nw)
+        gq_stage_raw(static_cast<const uint8_t*>(p.x), p.x_records, (uint32_t)t * xbytes + c,
+                     xbytes - c < 1024u ? xbytes - c : 1024u,
+                     (uint32_t)reinterpret_cast<uintptr_t>(smem + p.xraw_off) + c, lane);
     if (nr > 0)
         gq_stage_raw(p.w, p.w_records, rw.s0 * G::SB - rw.shift, rw.bytes, (uint32_t)reinterpret_cast<uintptr_t>(rbuf),
                      lane);
     const int total = nr > 0 ? (int)chunks(rw) : 0;
     gs_wait(total);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __syncthreads();  // every wave's quarter of the activations is in LDS
+    __syncthreads();  // every wave's pieces of the activations are in LDS
     XItems xi;
-    gs_items_lds(xi, smem + p.xraw_off, p.x_dtype, 1, C, tid, 256);
-    gs_quant(xi, smem + p.xq_off, p.x_dtype, 1, C, tid, 256);
+    gs_items_lds(xi, smem + p.xraw_off, p.x_dtype, 1, C, tid, 64 * nw);
+    gs_quant(xi, smem + p.xq_off, p.x_dtype, 1, C, tid, 64 * nw);
     __syncthreads();
     if (nr == 0) return;
     const Lanes ln = lanes_of(C, lane);
@@ -417,10 +436,16 @@ int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_
     p.rm = GS_RD / GM * GM;
     if (p.rm == 0) p.rm = GM;
     if (p.rm > GS_RD) p.rm = GS_RD;
-    while (p.rm > GM && (double)((N + p.rm - 1) / p.rm) * T < 8.0 * cus) p.rm -= GM;
+    while (p.rm > GM && (double)((N + p.rm - 1) / p.rm) * T < 4.0 * cus) p.rm -= GM;
     const size_t xq = (size_t)XQ_BYTES * C, xraw = (size_t)K * (x_dtype == TSA_F32 ? 4 : 2);
     const size_t raw = gs_raw_bytes(type, p.rm, C);
-    const size_t lds = xq + xraw + 4 * raw;
+    // about one workgroup per CU (every workgroup stages and quantises the activations once),
+    // 4 to 16 waves, as LDS allows
+    const double waves = (double)((N + p.rm - 1) / p.rm) * T;
+    int nw = (int)((waves + cus - 1) / cus);
+    nw = nw < GS_MIN_WAVES ? GS_MIN_WAVES : nw > GS_MAX_WAVES ? GS_MAX_WAVES : nw;
+    while (nw > GS_MIN_WAVES && xq + xraw + (size_t)nw * raw > 160 * 1024) --nw;
+    const size_t lds = xq + xraw + (size_t)nw * raw;
     TSA_REQUIRE(lds <= 160 * 1024, TSA_ERR_SHAPE, "GGUF matvec: LDS %zu bytes", lds);
     const int64_t xb = T * (int64_t)xraw;
     p.x_records = (uint32_t)(xb < 0xFFFFFFF0ll ? xb : 0xFFFFFFF0ll);
@@ -431,8 +456,8 @@ int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_
     const void* fn = gs_pick(type);
     if (lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     void* args[] = {&p};
-    const dim3 grid((unsigned)((N + 4 * p.rm - 1) / (4 * p.rm)), (unsigned)T);
-    TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(256), args, lds, st));
+    const dim3 grid((unsigned)((N + (int64_t)nw * p.rm - 1) / ((int64_t)nw * p.rm)), (unsigned)T);
+    TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(64 * nw), args, lds, st));
     return TSA_OK;
 }
 

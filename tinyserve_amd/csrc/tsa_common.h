@@ -55,15 +55,10 @@ int num_cus();  // compute units of the current device (cached per device)
 
 
 // ---------------------------------------------------------------- device helpers
-// IEEE binary16 bits -> float, exact (subnormals kept) without relying on FP modes.
+// IEEE binary16 bits -> float by v_cvt_f32_f16: exact for every half, subnormals included
+// (HIP kernels run with f16/f64 denormals preserved; a signalling NaN comes back quiet).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-    const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
-    if (e == 0) {
-        const float v = (float)m * 0x1p-24f;
-        return s ? -v : v;
-    }
-    if (e == 31) return __uint_as_float(s | 0x7F800000u | (m << 13));
-    return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
