@@ -52,6 +52,21 @@ def test_gguf_matvec_bf16_in_out_unaligned(gtype):
     assert_close_bf16(y, ref)
 
 
+@pytest.mark.parametrize("gtype,K,N", [(8, 512, 96), (12, 512, 96), (13, 2048, 64), (14, 768, 80)])
+@pytest.mark.parametrize("offset", [2, 6, 10])
+@pytest.mark.parametrize("T", [1, 3])
+def test_gguf_matvec_2byte_aligned_weights(gtype, K, N, offset, T):
+    """Weights 2 (not 16) bytes aligned: the stream matvec's buffer-to-LDS copies start at the
+    16-byte boundary below each row range, so every row reads its own bytes."""
+    rng = np.random.default_rng(300 + gtype + offset + T)
+    data = synth.make_gguf(rng, gtype, N * K)
+    xf, xd = _x(rng, T, K, torch.float32)
+    ref = xf @ og.dequant_tensor(data, gtype, (N, K)).T
+    y = ops.gguf_matvec(xd, dev_u8(data, offset=offset), gtype, N, K)
+    cos, rel = metrics(to_f32(y), ref)
+    assert rel < 1e-4, rel
+
+
 def test_gguf_matvec_linear_in_x():
     """Size-independent property at workload-2 size: W(a x1 + b x2) = a W x1 + b W x2."""
     rng = np.random.default_rng(11)

@@ -143,8 +143,16 @@ __device__ __forceinline__ u32x4 ld16u(const uint8_t* p) { return *reinterpret_c
 
 typedef int gq_v4i __attribute__((ext_vector_type(4)));
 
-// Copies bytes [a0, a0 + n) of the buffer (base, records) into LDS at dst (all 16-byte
-// aligned; a0 may be "negative" as an unsigned wrap: those chunks read zero), 16 bytes per
+// Records of a buffer that starts mis bytes below n bytes of data: whole 16-byte chunks, so
+// the copy that holds the data's last bytes is not cut off by the range check (the rest of
+// that chunk lies on the same page).
+__device__ __forceinline__ uint32_t gq_records(uint64_t n, uint32_t mis) {
+    const uint64_t r = (n + mis + 15) & ~(uint64_t)15;
+    return r > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)r;
+}
+
+// Copies bytes [a0, a0 + n) of the buffer (base, records) into LDS at dst (base + a0 and dst
+// 16-byte aligned: an unaligned address would not be read as given), 16 bytes per
 // lane per instruction, one wave. Issued as inline assembly (the compiler would otherwise
 // wait for every load before any later LDS read); the caller waits with gq_wait_dma.
 __device__ __forceinline__ void gq_stage_raw(const uint8_t* base, uint32_t records, uint32_t a0, uint32_t n,

@@ -64,8 +64,11 @@ __global__ void __launch_bounds__(64 * MV_MAX_WAVES) gq_matvec_kernel(MvParams p
     const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
     const uint32_t s0 = lo / VS, raw = gq_raw_bytes(gq_sb_count<TY>(lo, hi), SB);
     uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
-    const uint32_t first = s0 * SB, shift = first & 15u;
-    if (n0 < N) gq_stage_raw(p.w, p.w_records, first - shift, raw, (uint32_t)reinterpret_cast<uintptr_t>(rbuf), lane);
+    // copies read 16-byte-aligned memory: the buffer starts at the boundary at or below w
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(p.w) & 15u;
+    const uint32_t first = mis + s0 * SB, shift = first & 15u;
+    if (n0 < N)
+        gq_stage_raw(p.w - mis, gq_records(p.w_records, mis), first - shift, raw, (uint32_t)reinterpret_cast<uintptr_t>(rbuf), lane);
     gq_stage(smem, p.x, p.x_dtype, (int64_t)t * K, K, tid, blockDim.x);
     gq_wait_dma();
     __syncthreads();

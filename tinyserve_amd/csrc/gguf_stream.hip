@@ -341,7 +341,9 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_matvec_kernel(GsMvParams
     const int nr = n0 >= N ? 0 : (N - n0 < p.rm ? N - n0 : p.rm);
     uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
     const uint32_t f0 = (uint32_t)n0 * C, f1 = (uint32_t)(n0 + nr) * C;
-    const Range rw = range_of<TY>(0u, f0, f1);
+    // copies read 16-byte-aligned memory: the buffer starts at the boundary at or below w
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(p.w) & 15u;
+    const Range rw = range_of<TY>(mis, f0, f1);
     // the token's activations (1 KB pieces dealt round the waves) and then the weight rows,
     // all as buffer-to-LDS copies, so the activations can be waited for with the weights
     // still out
@@ -351,8 +353,8 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_matvec_kernel(GsMvParams
                      xbytes - c < 1024u ? xbytes - c : 1024u,
                      (uint32_t)reinterpret_cast<uintptr_t>(smem + p.xraw_off) + c, lane);
     if (nr > 0)
-        gq_stage_raw(p.w, p.w_records, rw.s0 * G::SB - rw.shift, rw.bytes, (uint32_t)reinterpret_cast<uintptr_t>(rbuf),
-                     lane);
+        gq_stage_raw(p.w - mis, gq_records(p.w_records, mis), mis + rw.s0 * G::SB - rw.shift, rw.bytes,
+                     (uint32_t)reinterpret_cast<uintptr_t>(rbuf), lane);
     const int total = nr > 0 ? (int)chunks(rw) : 0;
     gs_wait(total);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

@@ -159,12 +159,14 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     const uint32_t raw = gq_raw_bytes(nsb, SB);
     uint8_t* rbuf = smem + p.raw_off_a + wave * p.raw_stride_a;
     const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
+    // copies read 16-byte-aligned memory: the buffer starts at the boundary at or below the slot
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(base) & 15u;
     uint32_t shift[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-        const uint32_t first = (uint32_t)(m ? L.up_off : L.gate_off) + s0 * SB;  // slot-relative byte
+        const uint32_t first = mis + (uint32_t)(m ? L.up_off : L.gate_off) + s0 * SB;  // byte in the buffer
         shift[m] = first & 15u;
-        gq_stage_raw(base, (uint32_t)L.slot_bytes, first - shift[m], raw, lds_r + m * raw, lane);
+        gq_stage_raw(base - mis, gq_records((uint64_t)L.slot_bytes, mis), first - shift[m], raw, lds_r + m * raw, lane);
     }
     gq_wait_dma();
     float acc[2][GQ_RW];
@@ -228,8 +230,10 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
         const int j = j0 + jw, nj = k - j0 < kk ? k - j0 : kk;
         const int64_t slot = j < k ? uniform(s_slot[gq_sel(p, t) + j]) : -1;
         const bool live = mine && j < k && slot >= 0 && slot < p.n_slots;
-        const uint32_t first = (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
-        if (live) gq_stage_raw(p.pool + slot * L.slot_bytes, (uint32_t)L.slot_bytes, first - shift, raw, lds_r, lane);
+        const uint8_t* sbase = p.pool + (live ? slot : 0) * L.slot_bytes;
+        const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(sbase) & 15u;  // as in phase A
+        const uint32_t first = mis + (uint32_t)L.down_off + s0 * SB, shift = first & 15u;
+        if (live) gq_stage_raw(sbase - mis, gq_records((uint64_t)L.slot_bytes, mis), first - shift, raw, lds_r, lane);
         // the round's h vectors (bf16 from phase A) into LDS once for the workgroup: vector jj
         // at smem + GQ_MISC + jj * vec_stride_b, staged by all threads together
         gq_stage_vecs(smem + GQ_MISC, p.vec_stride_b, p.h, TSA_BF16, (int64_t)(t * k + j0) * I, I, I, nj, tid,

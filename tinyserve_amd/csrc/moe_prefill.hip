@@ -9,6 +9,11 @@ int64_t pf_mxt_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int
 int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot,
                    int64_t E, const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y,
                    int y_dtype, uint8_t* ws, hipStream_t stream);
+bool gf_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k);
+int64_t gf_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int64_t E);
+int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot, int64_t E,
+               const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y, int y_dtype,
+               uint8_t* ws, hipStream_t stream);
 
 namespace {
 
@@ -165,12 +170,15 @@ static int64_t chunked_ws(const tsa_expert_layout& L, int64_t T, int k) {
     return ((T * k * 4 + 255) / 256) * 256 + dec;
 }
 
-// MXFP4 tiled pools with bf16 activations take the grouped MFMA GEMMs; every other
-// layout runs the fused decode kernel over chunks of tokens.
+// MXFP4 tiled pools with bf16 activations take the grouped MFMA GEMMs, and so do GGUF pools
+// (gf_supported: bf16 activations, dimensions multiples of 256, enough assignments); every
+// other call runs the decode kernels over chunks of tokens. The workspace covers the
+// largest form the layout can take (the x dtype is not known here).
 static int64_t prefill_ws(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
     const int64_t c = chunked_ws(L, T, k);
-    if (L.format != TSA_EXPERT_MXFP4 || !L.mx_tiled) return c;
-    const int64_t g = pf_mxt_workspace_bytes(L, T, k, E);
+    int64_t g = 0;
+    if (L.format == TSA_EXPERT_MXFP4 && L.mx_tiled) g = pf_mxt_workspace_bytes(L, T, k, E);
+    if (gf_supported(L, TSA_BF16, T, k)) g = gf_workspace_bytes(L, T, k, E);
     return g > c ? g : c;
 }
 
@@ -203,6 +211,13 @@ extern "C" int tsa_moe_prefill(const tsa_expert_layout* layout, const void* pool
         return pf_mxt_prefill(*layout, static_cast<const uint8_t*>(pool), n_slots, expert_slot, E, idx, weights, T, k,
                               static_cast<const uint16_t*>(x), y, y_dtype, static_cast<uint8_t*>(workspace),
                               as_stream(stream));
+    }
+    if (gf_supported(*layout, x_dtype, T, k) && (reinterpret_cast<uintptr_t>(pool) & 15u) == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        TSA_REQUIRE(x && y, TSA_ERR_INVALID_ARG, "null pointer");
+        return gf_prefill(*layout, static_cast<const uint8_t*>(pool), n_slots, expert_slot, E, idx, weights, T, k,
+                          static_cast<const uint16_t*>(x), y, y_dtype, static_cast<uint8_t*>(workspace),
+                          as_stream(stream));
     }
     int32_t* slots = static_cast<int32_t*>(workspace);
     const int64_t off = ((T * k * 4 + 255) / 256) * 256;

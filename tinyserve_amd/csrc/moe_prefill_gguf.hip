@@ -1,0 +1,414 @@
+// Batched (prefill) MoE over GGUF experts (Q8_0 / Q4_K / Q5_K / Q6_K slots in checkpoint
+// order): grouped expert GEMMs on the bf16 matrix cores, the weights decoded on the fly.
+//
+// The reference's batched GGUF expert (tinyserve/ggml_forward.py:117-151,
+// _fallback_forward) decodes each projection to fp32, casts it to the activations' dtype
+// (bf16) and runs F.linear; here the same bf16 weights (decode_unit's bit-exact fp32 values,
+// rounded to nearest even) are formed in LDS piece by piece from the native blocks and never
+// reach HBM.
+//
+// After group_kernel has sorted the (token, j) assignments expert-major, each resident
+// expert's run of sorted rows is cut into tiles of up to 64 rows (gf_table_kernel). Two
+// launches then cover every (row tile, weight tile) pair, and a combine pass sums:
+//   gate_up: h[i, n] = act(x[token(i)] . W_g[n], x[token(i)] . W_u[n]), bf16, sorted order;
+//   down:    yk[a, n] = h[i] . W_d[n], bf16, by assignment a = perm[i];
+//   combine: y[t] = sum_j w[t, j] yk[t k + j] in j order (one writer per output).
+//
+// Workgroup: 8 waves, a tile of 64 sorted rows x 128 weight rows (gate_up: 64 gate rows and
+// the same 64 up rows, so the activation is formed in the workgroup); wave (wn, wt) owns
+// 32 weight rows x 32 sorted rows on v_mfma_f32_32x32x16_bf16 (weights the A operand,
+// activations the B operand). K advances in pieces of 256 values (one K-quant super-block
+// of each row, or 8 Q8_0 blocks): the piece's raw blocks for the 128 rows come in by
+// buffer-to-LDS copies (a 16-byte-aligned window per row) issued during the previous
+// piece's MFMAs, the activations of the next piece wait in registers meanwhile, and then
+// every thread decodes two 32-value units of one row into the bf16 weight tile.
+//
+// Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
+// weighted scatter), tinyserve/ggml_forward.py:117-151 (bf16 weights, F.linear,
+// act_fn(gate) * up), tinyserve/gguf_dequant_torch.py:118-249 (block formats).
+#include <mutex>
+
+#include "fused_common.h"
+#include "mfma_tile.h"
+
+namespace tsa {
+
+int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                        hipStream_t stream);
+int pf_combine(const uint16_t* yk, const int32_t* idx, const float* w, const int32_t* expert_slot, int64_t E,
+               int64_t n_slots, int64_t T, int k, int H, void* y, int y_dtype, hipStream_t stream);
+
+namespace {
+
+constexpr int GF_THREADS = 512;
+constexpr int GF_BM = 64;                  // sorted rows per tile
+constexpr int GF_BN = 128;                 // weight rows per tile
+constexpr int GF_KP = 256;                 // values per K piece
+constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of the bf16 tiles (bytes)
+constexpr int GF_XOFF = 0;                 // activations: GF_BM rows
+constexpr int GF_WOFF = GF_BM * GF_RS;     // decoded weights: GF_BN rows
+constexpr int GF_ROFF = GF_WOFF + GF_BN * GF_RS;
+constexpr int GF_MAX_NCH = 18;             // 16-byte chunks of a row's raw piece window, at most (Q8_0)
+constexpr int GF_LDS = GF_ROFF + GF_BN * GF_MAX_NCH * 16;  // 138 KB
+constexpr int GF_GS = 64 * 4 + 16;         // gate_up epilogue: fp32 row stride of the staged gate / up values
+static_assert(2 * GF_BM * GF_GS <= GF_BN * GF_RS, "the staged gate and up values fit the weight tile");
+constexpr int GF_MIN_ASSIGN = 64;          // fewer assignments take the decode kernels
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+struct GfEntry {
+    int slot, row0, rows, pad;
+};
+
+// Raw bytes of one row's K piece: a K-quant super-block, or 8 Q8_0 blocks.
+template <int TY> struct GfType { static constexpr int PB = TY == 8 ? 272 : TY == 12 ? 144 : TY == 13 ? 176 : 210; };
+template <int TY> constexpr int gf_nch() { return (GfType<TY>::PB + 15 + 15) / 16; }
+// Alignment of a row's raw piece in LDS, which keeps its global address modulo 16: the
+// K-quant 4/5-bit super-blocks (144 / 176 bytes) stay 16-aligned, Q6_K / Q8_0 2-aligned
+// (the host requires pool, slot size and offsets to keep that).
+template <int TY> constexpr int gf_align() { return TY == 12 || TY == 13 ? 16 : 2; }
+
+struct GfGemm {
+    const uint8_t* pool;
+    int64_t slot_bytes;
+    const int* n_entries;
+    const GfEntry* table;
+    const uint16_t* src;      // gate_up: x [T, K] (rows through perm / k); down: h [n, K] in sorted order
+    const int32_t* perm;      // sorted position -> assignment id (token * k + j)
+    int k;
+    uint16_t* out;            // gate_up: h [n, N]; down: yk [T k, N]
+    int N, K;                 // outputs per row (gate_up: inter; down: hidden), reduction length
+    int64_t w_off, w2_off;    // slot offsets of the matrix (gate_up: gate, then up)
+    int64_t w_bytes;          // bytes of one matrix (N rows)
+    tsa_expert_layout L;
+};
+
+__device__ __forceinline__ void gf_dma(const v4i_t& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ v4i_t gf_desc(const uint8_t* p, int64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t n = bytes < 0xFFFFFFF0ll ? (uint32_t)bytes : 0xFFFFFFF0u;
+    return v4i_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)n, 0x00020000};
+}
+
+// Byte offset of weight row `row`'s K piece `p` in its matrix.
+template <int TY>
+__device__ __forceinline__ uint32_t gf_piece_byte(int row, int p, int K) {
+    return ((uint32_t)row * (uint32_t)(K / GF_KP) + (uint32_t)p) * (uint32_t)GfType<TY>::PB;
+}
+
+// The piece's raw windows of the tile's 128 weight rows into LDS: pair q = (row q / NCH,
+// chunk q % NCH) lands at raw + 16 q, so one wave instruction fills 1 KB. The buffers start
+// at the 16-byte boundary at or below each matrix (m0 / m1 bytes before it) and end at the
+// boundary at or above its end, and a window starts at the boundary at or below its piece,
+// so every copy reads 16 whole aligned bytes; rows past the matrix read zero (buffer range).
+template <int TY, bool GU>
+__device__ __forceinline__ void gf_issue_raw(const v4i_t& r0, const v4i_t& r1, uint32_t m0, uint32_t m1, int n0,
+                                             int p, int K, uint32_t raw, int wave, int lane) {
+    constexpr int NCH = gf_nch<TY>(), TOT = GF_BN * NCH;
+    for (int ii = wave; 64 * ii < TOT; ii += GF_THREADS / 64) {
+        const int q = 64 * ii + lane;
+        if (q < TOT) {
+            const int r = q / NCH, c = q - r * NCH;
+            const bool up = GU && r >= 64;
+            const int row = GU ? n0 + (r & 63) : n0 + r;
+            const uint32_t m = up ? m1 : m0;
+            const uint32_t voff = ((m + gf_piece_byte<TY>(row, p, K)) & ~15u) + 16u * (uint32_t)c;
+            if (up) gf_dma(r1, voff, raw + 1024u * (uint32_t)ii);
+            else gf_dma(r0, voff, raw + 1024u * (uint32_t)ii);
+        }
+    }
+}
+
+// 32 decoded values -> 16 bf16 words (round to nearest even) at dst (16-byte aligned).
+__device__ __forceinline__ void gf_put_bf16(uint8_t* dst, const float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(dst + 16 * i) =
+            make_uint4(pack_bf16x2(v[8 * i], v[8 * i + 1]), pack_bf16x2(v[8 * i + 2], v[8 * i + 3]),
+                       pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7]));
+}
+
+template <int TY, bool GU>
+__global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int en_i = blockIdx.y;
+    if (en_i >= *p.n_entries) return;  // workgroup-uniform
+    const GfEntry en = p.table[en_i];
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const int wn = wave & 3, wt = wave >> 2, g = lane >> 5, rr = lane & 31;
+    const int K = p.K, P = K / GF_KP, N = p.N;
+    const int n0 = (int)blockIdx.x * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
+    const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
+    const uint8_t* mat0 = base + p.w_off;
+    const uint8_t* mat1 = base + (GU ? p.w2_off : p.w_off);
+    const uint32_t mis0 = (uint32_t)reinterpret_cast<uintptr_t>(mat0) & 15u;
+    const uint32_t mis1 = (uint32_t)reinterpret_cast<uintptr_t>(mat1) & 15u;
+    const v4i_t rs0 = gf_desc(mat0 - mis0, (p.w_bytes + mis0 + 15) & ~15ll),
+                rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const uint32_t raw = lds0 + GF_ROFF;
+
+    // This thread's activation segment: sorted row xr, 64 bytes at 64 xs of each piece.
+    const int xr = tid >> 3, xs = tid & 7;
+    const bool xlive = xr < en.rows;
+    int64_t xrow = 0;
+    if (xlive) {
+        const int a = p.perm[en.row0 + xr];
+        xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + xr);
+    }
+    const uint16_t* xsrc = p.src + xrow * K + 32 * xs;
+    uint4 xv[4];
+    auto load_x = [&](int pc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
+    };
+
+    // This thread's decode work: weight row dr, units 2 dq and 2 dq + 1 of each piece.
+    const int dr = tid >> 2, dq = tid & 3;
+    const int drow = GU ? n0 + (dr & 63) : n0 + dr;
+    constexpr int NCH = gf_nch<TY>();
+    const uint8_t* draw = smem + GF_ROFF + 16 * NCH * dr;
+    const uint32_t dmis = GU && dr >= 64 ? mis1 : mis0;
+    uint8_t* dws = smem + GF_WOFF + dr * GF_RS + 128 * dq;
+
+    v16f_t acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+    gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
+    load_x(0);
+    for (int pc = 0; pc < P; ++pc) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(smem + GF_XOFF + xr * GF_RS + 64 * xs + 16 * i) = xv[i];
+        __syncthreads();  // the piece's raw blocks and activations are in LDS
+        {
+            const uint8_t* sb = draw + ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
+            float v[32];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int u = 2 * dq + h;
+                if constexpr (TY == 8) decode_unit<8, 2>(sb + 34 * u, 0, v);
+                else decode_unit<TY, gf_align<TY>()>(sb, u, v);
+                gf_put_bf16(dws + 64 * h, v);
+            }
+        }
+        __syncthreads();  // the bf16 weight tile is complete; the raw area is free
+        if (pc + 1 < P) {
+            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw, wave, lane);
+            load_x(pc + 1);
+        }
+        const uint8_t* wa = smem + GF_WOFF + (32 * wn + rr) * GF_RS + 16 * g;
+        const uint8_t* xb = smem + GF_XOFF + (32 * wt + rr) * GF_RS + 16 * g;
+#pragma unroll
+        for (int j = 0; j < GF_KP / 16; ++j) {
+            const bf16x8 A = *reinterpret_cast<const bf16x8*>(wa + 32 * j);
+            const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * j);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
+        }
+        __syncthreads();  // every wave is done with this piece's tiles
+    }
+
+    // acc[4u + r] = weight row 32 wn + 8u + 4g + r of the tile, sorted row 32 wt + rr.
+    const int tk = 32 * wt + rr;
+    if constexpr (GU) {
+        // gate (wn 0, 1) and up (wn 2, 3) pre-activations as fp32 into LDS, then
+        // h = act(gate, up) rounded once to bf16, 8 columns per thread
+        float* stage = reinterpret_cast<float*>(smem + GF_WOFF + (wn >= 2 ? GF_BM * GF_GS : 0) + tk * GF_GS);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            *reinterpret_cast<float4*>(stage + 32 * (wn & 1) + 8 * u + 4 * g) =
+                make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
+        __syncthreads();
+        const int hr = tid >> 3, hc = 8 * (tid & 7);
+        if (hr < en.rows && n0 + hc < N) {
+            const float* gs = reinterpret_cast<const float*>(smem + GF_WOFF + hr * GF_GS) + hc;
+            const float* us = reinterpret_cast<const float*>(smem + GF_WOFF + GF_BM * GF_GS + hr * GF_GS) + hc;
+            float h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gs[i], us[i]) : gs[i] * sigmoidf_(gs[i]) * us[i];
+            *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
+                make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
+                           pack_bf16x2(h[6], h[7]));
+        }
+    } else {
+        if (tk < en.rows) {
+            const int64_t a = p.perm[en.row0 + tk];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int n = n0 + 32 * wn + 8 * u + 4 * g;
+                if (n < N)  // N % 8 == 0: four rows from n are all in or all out
+                    *reinterpret_cast<uint2*>(p.out + a * N + n) =
+                        make_uint2(pack_bf16x2(acc[4 * u], acc[4 * u + 1]), pack_bf16x2(acc[4 * u + 2], acc[4 * u + 3]));
+            }
+        }
+    }
+}
+
+// Tiles of up to GF_BM sorted rows per resident expert: entry = (slot, first sorted row,
+// rows), experts in id order; n_entries[0] = the count. One workgroup, E <= 1024.
+__global__ void __launch_bounds__(1024) gf_table_kernel(const int32_t* __restrict__ counts,
+                                                        const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ expert_slot, int E,
+                                                        int64_t n_slots, int* __restrict__ n_entries,
+                                                        GfEntry* __restrict__ table) {
+    __shared__ int pre[1024];
+    const int e = threadIdx.x;
+    int slot = -1, c = 0;
+    if (e < E) {
+        slot = expert_slot[e];
+        c = counts[e];
+        if (slot < 0 || slot >= n_slots) c = 0;
+    }
+    const int nt = (c + GF_BM - 1) / GF_BM;
+    pre[e] = nt;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
+        const int v = e >= d ? pre[e - d] : 0;
+        __syncthreads();
+        pre[e] += v;
+        __syncthreads();
+    }
+    const int first = pre[e] - nt;
+    for (int i = 0; i < nt; ++i) {
+        const int r = c - GF_BM * i;
+        table[first + i] = GfEntry{slot, offsets[e] + GF_BM * i, r < GF_BM ? r : GF_BM, 0};
+    }
+    if (e == 1023) n_entries[0] = pre[1023];
+}
+
+template <int TY, bool GU>
+const void* gf_fn() { return reinterpret_cast<const void*>(&gf_gemm_kernel<TY, GU>); }
+
+const void* gf_pick(int t, bool gu) {
+    switch (t) {
+        case 8: return gu ? gf_fn<8, true>() : gf_fn<8, false>();
+        case 12: return gu ? gf_fn<12, true>() : gf_fn<12, false>();
+        case 13: return gu ? gf_fn<13, true>() : gf_fn<13, false>();
+        case 14: return gu ? gf_fn<14, true>() : gf_fn<14, false>();
+    }
+    return nullptr;
+}
+
+int64_t gf_al256(int64_t v) { return (v + 255) / 256 * 256; }
+
+struct GfWs {
+    int64_t counts, offsets, perm, nent, table, h, yk, total;
+};
+
+GfWs gf_ws_layout(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
+    const int64_t n = T * k;
+    GfWs w;
+    int64_t o = 0;
+    w.counts = o; o += gf_al256(4 * E);
+    w.offsets = o; o += gf_al256(4 * (E + 1));
+    w.perm = o; o += gf_al256(4 * n);
+    w.nent = o; o += 256;
+    w.table = o; o += gf_al256((int64_t)sizeof(GfEntry) * (n / GF_BM + E + 1));
+    w.h = o; o += gf_al256(2 * n * L.inter);
+    w.yk = o; o += gf_al256(2 * n * L.hidden);
+    w.total = o;
+    return w;
+}
+
+bool gf_type_ok(int t, int64_t slot_bytes, int64_t off) {
+    if (t != 8 && t != 12 && t != 13 && t != 14) return false;
+    const int a = (t == 12 || t == 13) ? 16 : 2;
+    return slot_bytes % a == 0 && off % a == 0;
+}
+
+}  // namespace
+
+// Whether the grouped GGUF GEMMs cover a prefill call (else the decode kernels run over
+// token chunks): GGUF slots whose gate and up share a type, hidden and inter multiples of
+// 256 (no row straddles a super-block), bf16 activations, block alignment kept by the slot
+// size and offsets, and at least GF_MIN_ASSIGN assignments.
+bool gf_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k) {
+    const int64_t n = T * k;
+    return L.format == TSA_EXPERT_GGUF && L.gate_type == L.up_type && x_dtype == TSA_BF16 && L.hidden % GF_KP == 0 &&
+           L.inter % GF_KP == 0 && L.gate_bias_off < 0 && L.down_bias_off < 0 && n >= GF_MIN_ASSIGN &&
+           n / GF_BM + 1024 < 65535 && 2 * n * L.inter < ((int64_t)1 << 31) &&
+           2 * n * L.hidden < ((int64_t)1 << 31) && gf_type_ok(L.gate_type, L.slot_bytes, L.gate_off) &&
+           gf_type_ok(L.up_type, L.slot_bytes, L.up_off) && gf_type_ok(L.down_type, L.slot_bytes, L.down_off);
+}
+
+int64_t gf_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {
+    return gf_ws_layout(L, T, k, E).total;
+}
+
+int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot, int64_t E,
+               const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y, int y_dtype,
+               uint8_t* ws, hipStream_t stream) {
+    TSA_REQUIRE((reinterpret_cast<uintptr_t>(pool) & 15u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0,
+                TSA_ERR_INVALID_ARG, "GGUF grouped prefill: pool and x must be 16-byte aligned");
+    const GfWs w = gf_ws_layout(L, T, k, E);
+    int32_t* counts = reinterpret_cast<int32_t*>(ws + w.counts);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + w.offsets);
+    int32_t* perm = reinterpret_cast<int32_t*>(ws + w.perm);
+    int* nent = reinterpret_cast<int*>(ws + w.nent);
+    GfEntry* table = reinterpret_cast<GfEntry*>(ws + w.table);
+    uint16_t* h = reinterpret_cast<uint16_t*>(ws + w.h);
+    uint16_t* yk = reinterpret_cast<uint16_t*>(ws + w.yk);
+    const int H = (int)L.hidden, I = (int)L.inter;
+    const int64_t n = T * k;
+
+    int rc = launch_group_kernel(idx, n, (int)E, counts, offsets, perm, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(gf_table_kernel, dim3(1), dim3(1024), 0, stream, counts, offsets, expert_slot, (int)E, n_slots,
+                       nent, table);
+    TSA_LAUNCH_CHECK();
+
+    static std::once_flag lds_once;
+    static hipError_t lds_err = hipSuccess;
+    std::call_once(lds_once, [] {
+        for (int t : {8, 12, 13, 14})
+            for (bool gu : {true, false})
+                if (lds_err == hipSuccess)
+                    lds_err = hipFuncSetAttribute(gf_pick(t, gu), hipFuncAttributeMaxDynamicSharedMemorySize, GF_LDS);
+    });
+    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", GF_LDS, hipGetErrorString(lds_err));
+    const unsigned max_entries = (unsigned)(n / GF_BM + (E < n ? E : n) + 1);
+    auto mat_bytes = [](int t, int64_t rows, int64_t K) {
+        return rows * (K / GF_KP) * (t == 8 ? 272 : t == 12 ? 144 : t == 13 ? 176 : 210);
+    };
+
+    GfGemm g{};
+    g.pool = pool;
+    g.slot_bytes = L.slot_bytes;
+    g.n_entries = nent;
+    g.table = table;
+    g.perm = perm;
+    g.k = k;
+    g.L = L;
+    // gate_up: x [T, H] -> h [n, I]
+    g.src = x;
+    g.out = h;
+    g.N = I;
+    g.K = H;
+    g.w_off = L.gate_off;
+    g.w2_off = L.up_off;
+    g.w_bytes = mat_bytes(L.gate_type, I, H);
+    void* args[] = {&g};
+    TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.gate_type, true), dim3((unsigned)((I + GF_BN / 2 - 1) / (GF_BN / 2)), max_entries),
+                                  dim3(GF_THREADS), args, GF_LDS, stream));
+    // down: h [n, I] -> yk [n, H] by assignment id
+    g.src = h;
+    g.out = yk;
+    g.N = H;
+    g.K = I;
+    g.w_off = L.down_off;
+    g.w2_off = L.down_off;
+    g.w_bytes = mat_bytes(L.down_type, H, I);
+    TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.down_type, false), dim3((unsigned)((H + GF_BN - 1) / GF_BN), max_entries),
+                                  dim3(GF_THREADS), args, GF_LDS, stream));
+    return pf_combine(yk, idx, weights, expert_slot, E, n_slots, T, k, H, y, y_dtype, stream);
+}
+
+}  // namespace tsa

@@ -766,6 +766,16 @@ int64_t pf_mxt_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int
 int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                         hipStream_t stream);
 
+// y[t] = sum_j w[t, j] yk[t k + j] over the live assignments, j in order (H % 8 == 0).
+int pf_combine(const uint16_t* yk, const int32_t* idx, const float* w, const int32_t* expert_slot, int64_t E,
+               int64_t n_slots, int64_t T, int k, int H, void* y, int y_dtype, hipStream_t stream) {
+    const int64_t threads = T * (H / 8);
+    hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, yk, idx, w,
+                       expert_slot, E, n_slots, T, k, H, y, y_dtype);
+    TSA_LAUNCH_CHECK();
+    return TSA_OK;
+}
+
 int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* expert_slot,
                    int64_t E, const int32_t* idx, const float* weights, int64_t T, int k, const uint16_t* x, void* y,
                    int y_dtype, uint8_t* ws, hipStream_t stream) {
@@ -853,11 +863,7 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
     else hipLaunchKernelGGL((pf_gemm_kernel<false, false>), dim3(grid), dim3(PF_THREADS), PF_LDS, stream, g);
     TSA_LAUNCH_CHECK();
 
-    const int64_t threads = T * (H / 8);
-    hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, yk, idx,
-                       weights, expert_slot, E, n_slots, T, k, H, y, y_dtype);
-    TSA_LAUNCH_CHECK();
-    return TSA_OK;
+    return pf_combine(yk, idx, weights, expert_slot, E, n_slots, T, k, H, y, y_dtype, stream);
 }
 
 }  // namespace tsa
