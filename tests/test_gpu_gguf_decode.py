@@ -76,6 +76,43 @@ def test_gguf_decode_routed_repeats_and_missing_expert():
     assert_close_bf16(outs[0], _ref(experts, synth.bf16_to_f32(x_bits), ridx, live_w), "missing expert")
 
 
+@pytest.mark.parametrize("types,H,I,T,x_dtype,pad", [
+    ((12, 12, 14), 2880, 2880, 1, torch.bfloat16, 0),  # the workload-2 expert
+    ((13, 13, 14), 2048, 768, 3, torch.bfloat16, 0),
+    ((8, 8, 8), 512, 1024, 2, torch.float32, 0),
+    ((14, 14, 14), 768, 512, 4, torch.float16, 0),
+    ((12, 12, 8), 512, 512, 2, torch.bfloat16, 2),     # slots 2 bytes off 16-byte boundaries
+])
+def test_gguf_decode_one_expert_stream_kernels(types, H, I, T, x_dtype, pad):
+    """One expert per token (k = 1) runs on the sub-block stream kernels (gs_gate_up_kernel,
+    gs_down_kernel): given slots, then routed from logits with the selection handed on."""
+    rng = np.random.default_rng(H + I + T + pad)
+    E = 6
+    L, experts, pool = _pool(rng, H, I, types, E)
+    if pad:
+        pool = torch.cat([torch.zeros((E, pad), dtype=torch.uint8, device="cuda"), pool], dim=1).contiguous()
+        L.slot_bytes += pad
+        L.gate_off += pad
+        L.up_off += pad
+        L.down_off += pad
+    x = rng.normal(0.0, 1.0, (T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(x_dtype)
+    xf = xt.float().numpy()
+    idx = rng.integers(0, E, size=(T, 1)).astype(np.int32)
+    w = rng.uniform(0.5, 1.5, size=(T, 1)).astype(np.float32)
+    y = ops.moe_decode(L, pool, torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), xt.cuda(),
+                       out_dtype=torch.float32)
+    assert_close_bf16(y, _ref(experts, xf, idx, w), f"one-expert decode {types} H {H} I {I}")
+    if T <= 4:
+        logits = synth.zipf_logits(rng, T, E)
+        y2, ridx, rw = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                             torch.from_numpy(logits).cuda(), xt.cuda(), 1, "softmax_then_topk",
+                                             out_dtype=torch.float32, return_routing=True)
+        eidx, ew = oex.route_softmax_then_topk(logits, 1)
+        assert np.array_equal(ridx.cpu().numpy(), eidx)
+        assert_close_bf16(y2, _ref(experts, xf, eidx, ew), f"one-expert routed decode {types}")
+
+
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
 def test_gguf_decode_wide_activations(x_dtype):
     """fp32 / fp16 activations are staged as a bf16 hi/lo pair: the result follows the fp32

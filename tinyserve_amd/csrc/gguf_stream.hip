@@ -81,17 +81,17 @@ __device__ __forceinline__ void xraw_values(const XRaw& r, int dtype, float (&f)
 }
 
 // The activation items of one workgroup: nvec vectors of C blocks, item i = (vector i /
-// (4C), block (i % 4C) / 4, quarter i % 4) for i = tid + nthr m, quantised by gs_quant.
+// (4C), block (i % 4C) / 4, quarter i % 4) for i = i0 + tid + nthr m, quantised by gs_quant.
 struct XItems {
     XRaw r[GS_ITEMS];
 };
 // The items, read from a raw copy of the vectors in LDS (vectors back to back).
 __device__ __forceinline__ void gs_items_lds(XItems& it, const uint8_t* raw, int dtype, int nvec, int C, int tid,
-                                             int nthr) {
+                                             int nthr, int i0 = 0) {
     const int total = nvec * 4 * C, es = dtype == TSA_F32 ? 4 : 2;
 #pragma unroll
     for (int m = 0; m < GS_ITEMS; ++m) {
-        const int i = tid + nthr * m;
+        const int i = i0 + tid + nthr * m;
         const int ii = i < total ? i : 0;
         const uint8_t* q = raw + 8 * es * ii;  // vectors back to back: item ii starts at value 8 ii
         const u32x4 a = ld16u(q);
@@ -108,12 +108,12 @@ __device__ __forceinline__ void gs_items_lds(XItems& it, const uint8_t* raw, int
 // threads of a block are four consecutive lanes (4C items per vector): their maximum and
 // sums come from DPP quad exchanges.
 __device__ __forceinline__ void gs_quant(const XItems& it, uint8_t* dst, int dtype, int nvec, int C, int tid,
-                                         int nthr) {
+                                         int nthr, int i0 = 0) {
     const int total = nvec * 4 * C;
 #pragma unroll
     for (int m = 0; m < GS_ITEMS; ++m) {
-        const int i = tid + nthr * m;
-        if (nthr * m >= total) break;  // workgroup-uniform: no thread has this item
+        const int i = i0 + tid + nthr * m;
+        if (i0 + nthr * m >= total) break;  // workgroup-uniform: no thread has this item
         float f[8];
         xraw_values(it.r[m], dtype, f);
         float amax = 0.0f, sum = 0.0f;
@@ -157,6 +157,17 @@ __device__ __forceinline__ void gs_quant(const XItems& it, uint8_t* dst, int dty
             if (q == 0) *reinterpret_cast<float2*>(p + 64) = make_float2(s, s32);
             if ((q & 1) == 0) *reinterpret_cast<float*>(p + 72 + 2 * q) = s16;  // q 0: first half, q 2: second
         }
+    }
+}
+
+// All nvec vectors (raw in LDS at raw, back to back) quantised into dst, in rounds of
+// GS_ITEMS items per thread. The caller's barrier makes dst visible.
+__device__ __forceinline__ void gs_quant_all(const uint8_t* raw, uint8_t* dst, int dtype, int nvec, int C, int tid,
+                                             int nthr) {
+    for (int i0 = 0; i0 < nvec * 4 * C; i0 += GS_ITEMS * nthr) {
+        XItems xi;
+        gs_items_lds(xi, raw, dtype, nvec, C, tid, nthr, i0);
+        gs_quant(xi, dst, dtype, nvec, C, tid, nthr, i0);
     }
 }
 
@@ -392,6 +403,242 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_matvec_kernel(GsMvParams
     if ((lane & 7) == 0 && r < nr) store_out(p.y, p.y_dtype, (int64_t)t * N + n0 + r, tot);
 }
 
+// ---------------------------------------------------------------- expert decode
+// Top-k GGUF expert decode as two launches over the same 32-value sub-block units:
+//   gs_gate_up_kernel: workgroup = (row group of the intermediate dimension, (token, expert)
+//     pair); each workgroup quantises its token's activations, each wave streams its rows of
+//     gate and the same rows of up (per-row waits) and writes h = act(gate, up) as bf16, as
+//     the super-block kernels do. Routed calls select the token's experts in the prologue
+//     (the x copies are already out) and the first workgroup of each token writes the
+//     selection for the down launch.
+//   gs_down_kernel: workgroup = (row group of the hidden dimension, token); each workgroup
+//     quantises the token's k h vectors, each wave streams its rows of every selected
+//     expert's down in expert order and keeps sum_j w_j (row . h_j), so every output has one
+//     writer and the sum runs in a fixed order.
+
+constexpr int GS_MISC = 512;  // LDS: the routing tables (slots, weights) of the token group
+
+struct GsDecParams {
+    tsa_expert_layout L;
+    const uint8_t* pool;
+    int64_t n_slots;
+    const int32_t* slots;        // [T, k]: given slots, or (down, routed) the selection gate_up made
+    const float* wts;            // [T, k]
+    const void* logits;          // gate_up, routed: [T, E] (slots unused)
+    const int32_t* expert_slot;  // [E] (routed)
+    int32_t* idx_out;            // [T, k] (routed, optional)
+    float* w_out;
+    int32_t* tab_slot;           // routed: the selection, for the down launch
+    float* tab_w;
+    int logits_dtype, route_mode, E;
+    int T, k;
+    const void* x;               // gate_up: x [T, H]; down: h [T k, I] (bf16)
+    uint32_t x_records;
+    int x_dtype;
+    uint16_t* h;                 // gate_up: h [T k, I] (bf16)
+    void* y;                     // down: y [T, H]
+    int y_dtype;
+    int rm;                      // rows per wave
+    int xq_off, xraw_off, raw_off, raw_stride;
+};
+
+// Rows [n0, n0 + nr) of a matrix of C sub-blocks per row at mat (mat_bytes long) into LDS at
+// dst: the buffer starts at the 16-byte boundary at or below mat, so every copy reads 16
+// whole aligned bytes.
+template <int TY>
+__device__ __forceinline__ Range gs_issue_rows(const uint8_t* mat, uint32_t mat_bytes, int n0, int nr, int C,
+                                               uint32_t dst, int lane) {
+    using G = GsType<TY>;
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(mat) & 15u;
+    const Range r = range_of<TY>(mis, (uint32_t)n0 * C, (uint32_t)(n0 + nr) * C);
+    gq_stage_raw(mat - mis, gq_records(mat_bytes, mis), mis + r.s0 * G::SB - r.shift, r.bytes, dst, lane);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+
+// n bytes of src from byte off into LDS at dst, in 1 KB pieces dealt round the waves.
+__device__ __forceinline__ void gs_stage_vecs(const void* src, uint32_t records, uint32_t off, uint32_t n, uint8_t* dst,
+                                              int wave, int nw, int lane) {
+    for (uint32_t c = 1024u * wave; c < n; c += 1024u * nw)
+        gq_stage_raw(static_cast<const uint8_t*>(src), records, off + c, n - c < 1024u ? n - c : 1024u, lds_addr(dst) + c,
+                     lane);
+}
+
+template <int TY>
+__global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_gate_up_kernel(GsDecParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    using G = GsType<TY>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6), nw = (int)(blockDim.x >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k, C = H / 32;
+    const int a = blockIdx.y, t = a / k, j = a - t * k;
+    int* s_slot = reinterpret_cast<int*>(smem);
+    float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
+    const uint32_t xbytes = (uint32_t)H * (p.x_dtype == TSA_F32 ? 4u : 2u);  // a multiple of 64
+    // the activation copies: every wave, or (routed) every wave but wave 0, which selects the
+    // token's experts meanwhile (its logit loads would otherwise queue behind its copies)
+    if (!p.logits) gs_stage_vecs(p.x, p.x_records, (uint32_t)t * xbytes, xbytes, smem + p.xraw_off, wave, nw, lane);
+    else if (wave > 0)
+        gs_stage_vecs(p.x, p.x_records, (uint32_t)t * xbytes, xbytes, smem + p.xraw_off, wave - 1, nw - 1, lane);
+    int64_t slot;
+    if (p.logits) {
+        if (wave == 0) {
+            int es[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) es[q] = p.expert_slot[min(lane + 64 * q, p.E - 1)];
+            const int sel = route_token(p, t, lane, es, s_slot, s_w);
+            if (blockIdx.x == 0 && j == 0 && lane < k) {
+                if (p.idx_out) {
+                    p.idx_out[t * k + lane] = sel;
+                    p.w_out[t * k + lane] = s_w[t * k + lane];
+                }
+                p.tab_slot[t * k + lane] = s_slot[t * k + lane];
+                p.tab_w[t * k + lane] = s_w[t * k + lane];
+            }
+        }
+        __syncthreads();
+        slot = uniform(s_slot[t * k + j]);
+    } else {
+        slot = uniform(p.slots[(int64_t)t * k + j]);
+    }
+    const bool live = slot >= 0 && slot < p.n_slots;
+    const int n0 = ((int)blockIdx.x * nw + wave) * p.rm;
+    const int nr = !live || n0 >= I ? 0 : (I - n0 < p.rm ? I - n0 : p.rm);
+    uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
+    const uint32_t half = (uint32_t)p.raw_stride / 2;
+    const uint8_t* base = p.pool + (live ? slot : 0) * L.slot_bytes;
+    const uint32_t mat_bytes = (uint32_t)((int64_t)I * C / G::SPB * G::SB);
+    Range rg{}, ru{};
+    int cg = 0, cu = 0;
+    if (nr > 0) {
+        rg = gs_issue_rows<TY>(base + L.gate_off, mat_bytes, n0, nr, C, lds_addr(rbuf), lane);
+        ru = gs_issue_rows<TY>(base + L.up_off, mat_bytes, n0, nr, C, lds_addr(rbuf) + half, lane);
+        cg = (int)chunks(rg);
+        cu = (int)chunks(ru);
+    }
+    gs_wait(cg + cu);  // this wave's activation pieces are in
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    gs_quant_all(smem + p.xraw_off, smem + p.xq_off, p.x_dtype, 1, C, tid, 64 * nw);
+    __syncthreads();
+    if (nr == 0) return;  // a dead pair's h is never read
+    const Lanes ln = lanes_of(C, lane);
+    XQ x0 = xq_read(smem + p.xq_off + XQ_BYTES * ln.c0), x1 = x0;
+    if (ln.ncol > 1) x1 = xq_read(smem + p.xq_off + XQ_BYTES * (ln.c0 + 64));
+    float acc[8];  // gate rows 0..3, up rows 0..3
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    const uint32_t f0 = (uint32_t)n0 * C;
+    for (int m = 0; m < 2; ++m) {
+        const Range& rw = m ? ru : rg;
+        const uint8_t* area = rbuf + (m ? half : 0u) + rw.shift;
+        for (int r0 = 0; r0 < nr; r0 += ln.G) {
+            const int rmax = r0 + ln.G - 1 < nr ? r0 + ln.G - 1 : nr - 1;
+            const int done = (int)chunks_until<TY>(rw, f0 + (uint32_t)(rmax + 1) * C);
+            gs_wait(m ? cu - done : cg - done + cu);
+            const int r = r0 + ln.g;
+            if (ln.ncol == 0 || r >= nr) continue;
+            const uint32_t f = f0 + (uint32_t)r * C + ln.c0;
+            float part = sb_dot<TY>(area + (f / G::SPB - rw.s0) * G::SB, (int)(f % G::SPB), x0);
+            if (ln.ncol > 1)
+                part += sb_dot<TY>(area + ((f + 64) / G::SPB - rw.s0) * G::SB, (int)((f + 64) % G::SPB), x1);
+            acc_put(acc, 4 * m + r, part);
+        }
+    }
+    const float tot = wave_sum_rows<8>(acc, lane);  // lane 8 i: gate row i (i < 4), up row i - 4
+    // up row r (lane 32 + 8 r) beside gate row r: the swap's second half, lower lanes
+    const float up = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(tot), __float_as_uint(tot), false, false)[1]);
+    const int r = lane >> 3;
+    if ((lane & 7) == 0 && r < nr) {
+        const float hv = L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(L, tot, up) : tot * sigmoidf_(tot) * up;
+        p.h[(int64_t)a * I + n0 + r] = f32_to_bf16_bits(hv);
+    }
+}
+
+template <int TY>
+__global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_down_kernel(GsDecParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    using G = GsType<TY>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6), nw = (int)(blockDim.x >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k, C = I / 32, t = blockIdx.y;
+    const uint32_t vbytes = (uint32_t)k * (uint32_t)I * 2u;  // the token's k h vectors (bf16), back to back
+    gs_stage_vecs(p.x, p.x_records, (uint32_t)t * vbytes, vbytes, smem + p.xraw_off, wave, nw, lane);
+    const int n0 = ((int)blockIdx.x * nw + wave) * p.rm;
+    const int nr = n0 >= H ? 0 : (H - n0 < p.rm ? H - n0 : p.rm);
+    uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
+    const uint32_t area = (uint32_t)p.raw_stride / (uint32_t)k;
+    const uint32_t mat_bytes = (uint32_t)((int64_t)H * C / G::SPB * G::SB);
+    // the token's slots and weights, lane j holding expert j's (one load for all of them: a
+    // load per expert inside the copy loop would wait for each in turn)
+    const int my_slot = lane < k ? p.slots[(int64_t)t * k + lane] : -1;
+    const float my_w = lane < k ? p.wts[(int64_t)t * k + lane] : 0.0f;
+    int total = 0;
+    if (nr > 0) {
+        for (int j = 0; j < k; ++j) {  // every live expert's rows, in expert order
+            const int64_t slot = __builtin_amdgcn_readlane(my_slot, j);
+            if (slot < 0 || slot >= p.n_slots) continue;
+            const Range rj = gs_issue_rows<TY>(p.pool + slot * L.slot_bytes + L.down_off, mat_bytes, n0, nr, C,
+                                               lds_addr(rbuf) + area * (uint32_t)j, lane);
+            total += (int)chunks(rj);
+        }
+    }
+    gs_wait(total);  // this wave's pieces of the h vectors are in
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    gs_quant_all(smem + p.xraw_off, smem + p.xq_off, TSA_BF16, k, C, tid, 64 * nw);
+    __syncthreads();
+    if (nr == 0) return;
+    const Lanes ln = lanes_of(C, lane);
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    const uint32_t f0 = (uint32_t)n0 * C;
+    int before = 0;
+    for (int j = 0; j < k; ++j) {
+        const int64_t slot = __builtin_amdgcn_readlane(my_slot, j);
+        if (slot < 0 || slot >= p.n_slots) continue;
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+        const uint8_t* mat = p.pool + slot * L.slot_bytes + L.down_off;
+        const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(mat) & 15u;
+        const Range rj = range_of<TY>(mis, f0, f0 + (uint32_t)nr * C);  // as issued
+        const uint8_t* xqj = smem + p.xq_off + XQ_BYTES * j * C;
+        XQ x0 = xq_read(xqj + XQ_BYTES * ln.c0), x1 = x0;
+        if (ln.ncol > 1) x1 = xq_read(xqj + XQ_BYTES * (ln.c0 + 64));
+        const uint8_t* ar = rbuf + area * (uint32_t)j + rj.shift;
+        for (int r0 = 0; r0 < nr; r0 += ln.G) {
+            const int rmax = r0 + ln.G - 1 < nr ? r0 + ln.G - 1 : nr - 1;
+            gs_wait(total - before - (int)chunks_until<TY>(rj, f0 + (uint32_t)(rmax + 1) * C));
+            const int r = r0 + ln.g;
+            if (ln.ncol == 0 || r >= nr) continue;
+            const uint32_t f = f0 + (uint32_t)r * C + ln.c0;
+            float part = sb_dot<TY>(ar + (f / G::SPB - rj.s0) * G::SB, (int)(f % G::SPB), x0);
+            if (ln.ncol > 1)
+                part += sb_dot<TY>(ar + ((f + 64) / G::SPB - rj.s0) * G::SB, (int)((f + 64) % G::SPB), x1);
+            acc_put(acc, r, wj * part);
+        }
+        before += (int)chunks(rj);
+    }
+    const float tot = wave_sum_rows<8>(acc, lane);
+    const int r = lane >> 3;
+    if ((lane & 7) == 0 && r < nr) store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + r, tot);
+}
+
+template <int TY>
+const void* gs_gu_fn() { return reinterpret_cast<const void*>(&gs_gate_up_kernel<TY>); }
+template <int TY>
+const void* gs_dn_fn() { return reinterpret_cast<const void*>(&gs_down_kernel<TY>); }
+const void* gs_pick_dec(int t, bool gate_up) {
+    switch (t) {
+        case 8: return gate_up ? gs_gu_fn<8>() : gs_dn_fn<8>();
+        case 12: return gate_up ? gs_gu_fn<12>() : gs_dn_fn<12>();
+        case 13: return gate_up ? gs_gu_fn<13>() : gs_dn_fn<13>();
+        case 14: return gate_up ? gs_gu_fn<14>() : gs_dn_fn<14>();
+    }
+    return nullptr;
+}
+
 const void* gs_pick(int t) {
     switch (t) {
         case 8: return reinterpret_cast<const void*>(&gs_matvec_kernel<8>);
@@ -460,6 +707,121 @@ int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_
     void* args[] = {&p};
     const dim3 grid((unsigned)((N + (int64_t)nw * p.rm - 1) / ((int64_t)nw * p.rm)), (unsigned)T);
     TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(64 * nw), args, lds, st));
+    return TSA_OK;
+}
+
+namespace {
+
+// Launch shape of a decode launch: rows per wave (a multiple of the lane row group, at most
+// rmax; fewer while the grid would hold under 4 waves per CU), waves per workgroup (about
+// one workgroup per CU, 4..16, as LDS allows). rm == 0: the shape does not fit.
+struct GsShape {
+    int rm = 0, nw = 0;
+    size_t raw = 0, lds = 0;
+};
+
+GsShape gs_shape(int type, int64_t rows, int64_t groups, int C, int rmax, size_t fixed, int areas, int cus) {
+    GsShape s;
+    const int GM = C >= 64 ? 1 : 64 / C;
+    if (GM > rmax) return s;
+    int rm = rmax / GM * GM;
+    while (rm > GM && (double)((rows + rm - 1) / rm) * groups < 4.0 * cus) rm -= GM;
+    const size_t raw = gs_raw_bytes(type, rm, C) * (size_t)areas;
+    const double waves = (double)((rows + rm - 1) / rm) * groups;
+    int nw = (int)((waves + cus - 1) / cus);
+    nw = nw < GS_MIN_WAVES ? GS_MIN_WAVES : nw > GS_MAX_WAVES ? GS_MAX_WAVES : nw;
+    while (nw > GS_MIN_WAVES && fixed + (size_t)nw * raw > 160 * 1024) --nw;
+    if (fixed + (size_t)nw * raw > 160 * 1024) return s;
+    s.rm = rm;
+    s.nw = nw;
+    s.raw = raw;
+    s.lds = fixed + (size_t)nw * raw;
+    return s;
+}
+
+}  // namespace
+
+// Top-k GGUF expert decode on the sub-block stream kernels, with the same workspace layout
+// as the super-block kernels (h as bf16 [T k, I], then the routed selection). Returns a
+// positive value, having launched nothing, when the call is outside what these kernels
+// cover (the caller then takes the super-block kernels).
+int gs_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
+              const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
+              float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws,
+              int64_t ws_bytes, hipStream_t st) {
+    const int64_t H = L.hidden, I = L.inter;
+    const int es = x_dtype == TSA_F32 ? 4 : 2;
+    // One expert per token only: with several, each down wave walks every expert's rows in
+    // turn and the super-block kernels (one expert per wave) measured faster (workload 4:
+    // 29.6 against 18.7 us); one expert (workload 2): 15.1 against 16.6 us.
+    if (k != 1 || L.format != TSA_EXPERT_GGUF || L.gate_type != L.up_type || !gs_pick_dec(L.gate_type, true) ||
+        !gs_pick_dec(L.down_type, false) || H % 32 || I % 32 || H > 4096 || I > 4096 || k > FUSED_MAXK ||
+        T * k > 65535 || (logits && (T > FUSED_MAXT || E > 256)) || (reinterpret_cast<uintptr_t>(x) & 15) ||
+        T * H * es >= ((int64_t)1 << 32) - 16 || T * k * I * 2 >= ((int64_t)1 << 32) - 16)
+        return 1;
+    const int cus = num_cus();
+    const int CA = (int)(H / 32), CB = (int)(I / 32);
+    const size_t fixed_a = GS_MISC + (size_t)XQ_BYTES * CA + (size_t)H * es;
+    const size_t fixed_b = GS_MISC + (size_t)XQ_BYTES * k * CB + (size_t)k * I * 2;
+    const GsShape sa = gs_shape(L.gate_type, I, T * k, CA, 4, fixed_a, 2, cus);
+    const GsShape sb = gs_shape(L.down_type, H, T, CB, 8, fixed_b, k, cus);
+    if (!sa.rm || !sb.rm) return 1;
+    const int64_t h_bytes = T * k * I * 2, tab_off = (h_bytes + 255) / 256 * 256;
+    TSA_REQUIRE(ws_bytes >= tab_off + T * k * 8, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
+    GsDecParams p{};
+    p.L = L;
+    p.pool = pool;
+    p.n_slots = n_slots;
+    p.slots = slots;
+    p.wts = wts;
+    p.logits = logits;
+    p.expert_slot = expert_slot;
+    p.idx_out = idx_out;
+    p.w_out = w_out;
+    p.tab_slot = reinterpret_cast<int32_t*>(ws + tab_off);
+    p.tab_w = reinterpret_cast<float*>(ws + tab_off + T * k * 4);
+    p.logits_dtype = logits_dtype;
+    p.route_mode = mode;
+    p.E = (int)E;
+    p.T = (int)T;
+    p.k = k;
+    p.h = reinterpret_cast<uint16_t*>(ws);
+    // gate_up
+    p.x = x;
+    p.x_records = (uint32_t)(T * H * es);
+    p.x_dtype = x_dtype;
+    p.rm = sa.rm;
+    p.xq_off = GS_MISC;
+    p.xraw_off = GS_MISC + XQ_BYTES * CA;
+    p.raw_off = (int)fixed_a;
+    p.raw_stride = (int)sa.raw;
+    const void* fa = gs_pick_dec(L.gate_type, true);
+    if (sa.lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fa, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sa.lds));
+    void* args_a[] = {&p};
+    TSA_HIP_CHECK(hipLaunchKernel(fa, dim3((unsigned)((I + (int64_t)sa.nw * sa.rm - 1) / ((int64_t)sa.nw * sa.rm)), (unsigned)(T * k)),
+                                  dim3(64 * sa.nw), args_a, sa.lds, st));
+    // down: the selection gate_up made (routed) or the given table
+    GsDecParams q = p;
+    if (logits) {
+        q.logits = nullptr;
+        q.slots = p.tab_slot;
+        q.wts = p.tab_w;
+    }
+    q.x = ws;
+    q.x_records = (uint32_t)h_bytes;
+    q.x_dtype = TSA_BF16;
+    q.y = y;
+    q.y_dtype = y_dtype;
+    q.rm = sb.rm;
+    q.xq_off = GS_MISC;
+    q.xraw_off = (int)(GS_MISC + (size_t)XQ_BYTES * k * CB);
+    q.raw_off = (int)fixed_b;
+    q.raw_stride = (int)sb.raw;
+    const void* fb = gs_pick_dec(L.down_type, false);
+    if (sb.lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fb, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sb.lds));
+    void* args_b[] = {&q};
+    TSA_HIP_CHECK(hipLaunchKernel(fb, dim3((unsigned)((H + (int64_t)sb.nw * sb.rm - 1) / ((int64_t)sb.nw * sb.rm)), (unsigned)T),
+                                  dim3(64 * sb.nw), args_b, sb.lds, st));
     return TSA_OK;
 }
 

@@ -300,6 +300,11 @@ const char* gq_unsupported(const tsa_expert_layout& L) {
     return "";
 }
 
+int gs_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
+              const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
+              float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws,
+              int64_t ws_bytes, hipStream_t st);
+
 int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots, const float* wts,
               const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E, int32_t* idx_out,
               float* w_out, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws,
@@ -313,6 +318,10 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     // h (bf16) then, for routed calls, the slot / weight table phase A writes for phase B
     const int64_t h_bytes = T * k * L.inter * 2, tab_off = (h_bytes + 255) / 256 * 256;
     TSA_REQUIRE(ws_bytes >= tab_off + T * k * 8, TSA_ERR_WORKSPACE, "workspace too small for the GGUF decode");
+    // the sub-block stream kernels where they cover the call
+    const int rs = gs_decode(L, pool, n_slots, slots, wts, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
+                             T, k, x, x_dtype, y, y_dtype, ws, ws_bytes, st);
+    if (rs <= 0) return rs;
     GqParams p{};
     p.L = L;
     p.pool = pool;
