@@ -79,7 +79,7 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 
 # The kernels of one step of each decode workload (name substrings; "3c" = workload 3 with
 # the experts in checkpoint order).
-STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gq_phase_a", "gq_phase_b"),
+STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
                 "4": ("gq_phase_a", "gq_phase_b")}
 
