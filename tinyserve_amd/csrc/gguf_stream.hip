@@ -563,6 +563,11 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_down_kernel(GsDecParams 
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6), nw = (int)(blockDim.x >> 6);
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k, C = I / 32, t = blockIdx.y;
+    // the token's slots first, as scalar loads issued together (after the copies below they
+    // would become vector loads that wait for those copies)
+    int sl[FUSED_MAXK];
+#pragma unroll
+    for (int q = 0; q < FUSED_MAXK; ++q) sl[q] = uniform(p.slots[(int64_t)t * k + (q < k ? q : k - 1)]);
     const uint32_t vbytes = (uint32_t)k * (uint32_t)I * 2u;  // the token's k h vectors (bf16), back to back
     gs_stage_vecs(p.x, p.x_records, (uint32_t)t * vbytes, vbytes, smem + p.xraw_off, wave, nw, lane);
     const int n0 = ((int)blockIdx.x * nw + wave) * p.rm;
@@ -570,14 +575,12 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_down_kernel(GsDecParams 
     uint8_t* rbuf = smem + p.raw_off + wave * p.raw_stride;
     const uint32_t area = (uint32_t)p.raw_stride / (uint32_t)k;
     const uint32_t mat_bytes = (uint32_t)((int64_t)H * C / G::SPB * G::SB);
-    // the token's slots and weights, lane j holding expert j's (one load for all of them: a
-    // load per expert inside the copy loop would wait for each in turn)
-    const int my_slot = lane < k ? p.slots[(int64_t)t * k + lane] : -1;
-    const float my_w = lane < k ? p.wts[(int64_t)t * k + lane] : 0.0f;
     int total = 0;
     if (nr > 0) {
-        for (int j = 0; j < k; ++j) {  // every live expert's rows, in expert order
-            const int64_t slot = __builtin_amdgcn_readlane(my_slot, j);
+#pragma unroll
+        for (int j = 0; j < FUSED_MAXK; ++j) {  // every live expert's rows, in expert order
+            if (j >= k) break;
+            const int64_t slot = sl[j];
             if (slot < 0 || slot >= p.n_slots) continue;
             const Range rj = gs_issue_rows<TY>(p.pool + slot * L.slot_bytes + L.down_off, mat_bytes, n0, nr, C,
                                                lds_addr(rbuf) + area * (uint32_t)j, lane);
@@ -597,9 +600,9 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_down_kernel(GsDecParams 
     const uint32_t f0 = (uint32_t)n0 * C;
     int before = 0;
     for (int j = 0; j < k; ++j) {
-        const int64_t slot = __builtin_amdgcn_readlane(my_slot, j);
+        const int64_t slot = uniform(p.slots[(int64_t)t * k + j]);
         if (slot < 0 || slot >= p.n_slots) continue;
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+        const float wj = __int_as_float(uniform(__float_as_int(p.wts[(int64_t)t * k + j])));
         const uint8_t* mat = p.pool + slot * L.slot_bytes + L.down_off;
         const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(mat) & 15u;
         const Range rj = range_of<TY>(mis, f0, f0 + (uint32_t)nr * C);  // as issued
