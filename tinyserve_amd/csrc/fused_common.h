@@ -248,6 +248,21 @@ __device__ int route_token_v(const P& p, int t, int lane, const float v[4], cons
     return mysel;
 }
 
+// The token's first nr selections within one wave (route_select: rounds of a DPP wave max):
+// lane r < nr ends with the key, expert id and slot of the r-th selection (NaN first, then
+// descending logit, ties to the lower id). lg / es: the token's logits and slot table as
+// load4 lays them out.
+template <class P>
+__device__ __forceinline__ void select_topk(const P& p, int lane, const float lg[4], const int es[4], int nr,
+                                            uint32_t& myk, int& mysel, int& myslot) {
+    switch ((p.E + 63) >> 6) {
+        case 1: route_select<1>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        case 2: route_select<2>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        case 3: route_select<3>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+        default: route_select<4>(p, lane, lg, es, nr, myk, mysel, myslot); break;
+    }
+}
+
 // route_token_v with the token's logits loaded here.
 template <class P>
 __device__ int route_token(const P& p, int t, int lane, const int es[4], int* s_slot, float* s_w) {

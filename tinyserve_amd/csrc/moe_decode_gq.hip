@@ -60,15 +60,26 @@ __device__ __forceinline__ float gq_act(const tsa_expert_layout& L, float gate, 
 }
 
 // Routing (wave 0) or the given slot table for token t into s_slot / s_w; expert j of the
-// token is at index gq_sel(p, t) + j (routing writes the whole [T, k] table, T <= 4).
+// token is at index gq_sel(p, t) + j (routing writes the whole [T, k] table, T <= 4). With
+// need >= 0 and no table to write, only selection `need` is made (need + 1 rounds), and
+// only its slot is written.
 __device__ __forceinline__ int gq_sel(const GqParams& p, int t) { return p.logits ? t * p.k : 0; }
-__device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, float* s_w) {
+__device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, float* s_w, int need = -1) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (p.logits) {
         if (tid < 64) {
             int es[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+            if (!write_out && need >= 0) {
+                float lg[4];
+                load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
+                uint32_t myk;
+                int mysel, myslot;
+                select_topk(p, lane, lg, es, need + 1, myk, mysel, myslot);
+                if (lane == need) s_slot[t * p.k + need] = myslot;
+                return;
+            }
             const int sel = route_token(p, t, lane, es, s_slot, s_w);
             if (write_out && lane < p.k) {
                 if (p.idx_out) {
@@ -140,7 +151,7 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
     const bool split = p.x_dtype != TSA_BF16;
     const GqVec xv = gq_vec(smem + GQ_MISC, H, split);
-    gq_route(p, t, blockIdx.x == 0 && a % k == 0, s_slot, s_w);
+    gq_route(p, t, blockIdx.x == 0 && a % k == 0, s_slot, s_w, a % k);
     if (!p.logits) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid, 256);
     else if (tid >= 64) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid - 64, 192);
     __syncthreads();

@@ -220,21 +220,6 @@ __device__ __forceinline__ void lds_zero(uint8_t* a, int from, int to, int me, i
 constexpr int GU_WAVES = 2;        // waves per gate_up workgroup (one 16-row tile each)
 constexpr int XCH = 3072 / 8 / 64;  // x chunks (8 values) per lane when a wave loads all of x (H <= 3072)
 
-// The token's first nr selections within one wave (route_select: rounds of a DPP wave max):
-// lane r < nr ends with the key, expert id and slot of the r-th selection (NaN first, then
-// descending logit, ties to the lower id). lg / es: the token's logits and slot table as
-// load4 lays them out.
-template <class P>
-__device__ __forceinline__ void select_topk(const P& p, int lane, const float lg[4], const int es[4], int nr,
-                                            uint32_t& myk, int& mysel, int& myslot) {
-    switch ((p.E + 63) >> 6) {
-        case 1: route_select<1>(p, lane, lg, es, nr, myk, mysel, myslot); break;
-        case 2: route_select<2>(p, lane, lg, es, nr, myk, mysel, myslot); break;
-        case 3: route_select<3>(p, lane, lg, es, nr, myk, mysel, myslot); break;
-        default: route_select<4>(p, lane, lg, es, nr, myk, mysel, myslot); break;
-    }
-}
-
 // ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h terms to the workspace.
 // Workgroup b: pair b % (T k), 32-row block b / (T k) (pair-major, so neighbouring
 // workgroups stream different experts). Two waves per workgroup: for GPT-OSS-20B shapes the
