@@ -19,9 +19,10 @@
 // 32 weight rows x 32 sorted rows on v_mfma_f32_32x32x16_bf16 (weights the A operand,
 // activations the B operand). K advances in pieces of 256 values (one K-quant super-block
 // of each row, or 8 Q8_0 blocks): the piece's raw blocks for the 128 rows come in by
-// buffer-to-LDS copies (a 16-byte-aligned window per row) issued during the previous
-// piece's MFMAs, the activations of the next piece wait in registers meanwhile, and then
-// every thread decodes two 32-value units of one row into the bf16 weight tile.
+// buffer-to-LDS copies (a 16-byte-aligned window per row) into one of two raw areas,
+// issued when the previous piece starts, the next piece's activations wait in registers,
+// and each half of the piece is decoded (one 32-value unit per thread) into the bf16
+// weight tile and multiplied.
 //
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/ggml_forward.py:117-151 (bf16 weights, F.linear,
@@ -44,14 +45,16 @@ constexpr int GF_THREADS = 512;
 constexpr int GF_BM = 64;                  // sorted rows per tile
 constexpr int GF_BN = 128;                 // weight rows per tile
 constexpr int GF_KP = 256;                 // values per K piece
-constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of the bf16 tiles (bytes)
-constexpr int GF_XOFF = 0;                 // activations: GF_BM rows
-constexpr int GF_WOFF = GF_BM * GF_RS;     // decoded weights: GF_BN rows
-constexpr int GF_ROFF = GF_WOFF + GF_BN * GF_RS;
+constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of the activation tile (bytes)
+constexpr int GF_WS = GF_KP + 16;          // ... of the decoded weights: half a piece (128 values) at a time
+constexpr int GF_XOFF = 0;                 // activations: GF_BM rows of a whole piece
+constexpr int GF_WOFF = GF_BM * GF_RS;     // decoded weights: GF_BN rows of half a piece
+constexpr int GF_ROFF = GF_WOFF + GF_BN * GF_WS;
 constexpr int GF_MAX_NCH = 18;             // 16-byte chunks of a row's raw piece window, at most (Q8_0)
-constexpr int GF_LDS = GF_ROFF + GF_BN * GF_MAX_NCH * 16;  // 138 KB
+constexpr int GF_RAW = GF_BN * GF_MAX_NCH * 16;  // one raw area; two, for the piece in use and the next
+constexpr int GF_LDS = GF_ROFF + 2 * GF_RAW;     // 139 KB
 constexpr int GF_GS = 64 * 4 + 16;         // gate_up epilogue: fp32 row stride of the staged gate / up values
-static_assert(2 * GF_BM * GF_GS <= GF_BN * GF_RS, "the staged gate and up values fit the weight tile");
+static_assert(2 * GF_BM * GF_GS <= GF_BN * GF_WS, "the staged gate and up values fit the weight tile");
 constexpr int GF_MIN_ASSIGN = 64;          // fewer assignments take the decode kernels
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -169,50 +172,52 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
             xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
     };
 
-    // This thread's decode work: weight row dr, units 2 dq and 2 dq + 1 of each piece.
+    // This thread's decode work: weight row dr, unit 4 h + dq of each half h of each piece.
     const int dr = tid >> 2, dq = tid & 3;
     const int drow = GU ? n0 + (dr & 63) : n0 + dr;
     constexpr int NCH = gf_nch<TY>();
-    const uint8_t* draw = smem + GF_ROFF + 16 * NCH * dr;
     const uint32_t dmis = GU && dr >= 64 ? mis1 : mis0;
-    uint8_t* dws = smem + GF_WOFF + dr * GF_RS + 128 * dq;
+    uint8_t* dws = smem + GF_WOFF + dr * GF_WS + 64 * dq;
 
     v16f_t acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 
+    // Piece pc's raw blocks sit in raw area pc % 2; the next piece's copies go out as soon as
+    // the piece starts, so they fly during both halves' decode and MFMAs.
     gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
     load_x(0);
     for (int pc = 0; pc < P; ++pc) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(smem + GF_XOFF + xr * GF_RS + 64 * xs + 16 * i) = xv[i];
-        __syncthreads();  // the piece's raw blocks and activations are in LDS
-        {
-            const uint8_t* sb = draw + ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
-            float v[32];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int u = 2 * dq + h;
-                if constexpr (TY == 8) decode_unit<8, 2>(sb + 34 * u, 0, v);
-                else decode_unit<TY, gf_align<TY>()>(sb, u, v);
-                gf_put_bf16(dws + 64 * h, v);
-            }
-        }
-        __syncthreads();  // the bf16 weight tile is complete; the raw area is free
+        __syncthreads();  // the piece's raw blocks and activations are in LDS; the other raw area is free
         if (pc + 1 < P) {
-            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw, wave, lane);
+            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw + (uint32_t)((pc + 1) & 1) * GF_RAW, wave, lane);
             load_x(pc + 1);
         }
-        const uint8_t* wa = smem + GF_WOFF + (32 * wn + rr) * GF_RS + 16 * g;
-        const uint8_t* xb = smem + GF_XOFF + (32 * wt + rr) * GF_RS + 16 * g;
+        const uint8_t* sb = smem + GF_ROFF + (pc & 1) * GF_RAW + 16 * NCH * dr +
+                            ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
 #pragma unroll
-        for (int j = 0; j < GF_KP / 16; ++j) {
-            const bf16x8 A = *reinterpret_cast<const bf16x8*>(wa + 32 * j);
-            const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * j);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
+        for (int h = 0; h < 2; ++h) {
+            {
+                float v[32];
+                const int u = 4 * h + dq;
+                if constexpr (TY == 8) decode_unit<8, 2>(sb + 34 * u, 0, v);
+                else decode_unit<TY, gf_align<TY>()>(sb, u, v);
+                gf_put_bf16(dws, v);
+            }
+            __syncthreads();  // this half's bf16 weights are complete
+            const uint8_t* wa = smem + GF_WOFF + (32 * wn + rr) * GF_WS + 16 * g;
+            const uint8_t* xb = smem + GF_XOFF + (32 * wt + rr) * GF_RS + 256 * h + 16 * g;
+#pragma unroll
+            for (int j = 0; j < GF_KP / 32; ++j) {
+                const bf16x8 A = *reinterpret_cast<const bf16x8*>(wa + 32 * j);
+                const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * j);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
+            }
+            __syncthreads();  // every wave is done with this half's weights (and, after the second, the activations)
         }
-        __syncthreads();  // every wave is done with this piece's tiles
     }
 
     // acc[4u + r] = weight row 32 wn + 8u + 4g + r of the tile, sorted row 32 wt + rr.
