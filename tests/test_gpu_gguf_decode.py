@@ -82,6 +82,7 @@ def test_gguf_decode_routed_repeats_and_missing_expert():
     ((8, 8, 8), 512, 1024, 2, torch.float32, 0),
     ((14, 14, 14), 768, 512, 4, torch.float16, 0),
     ((12, 12, 8), 512, 512, 2, torch.bfloat16, 2),     # slots 2 bytes off 16-byte boundaries
+    ((13, 13, 14), 1024, 512, 100, torch.bfloat16, 0),  # many tokens, one expert each
 ])
 def test_gguf_decode_one_expert_stream_kernels(types, H, I, T, x_dtype, pad):
     """One expert per token (k = 1) runs on the sub-block stream kernels (gs_gate_up_kernel,
