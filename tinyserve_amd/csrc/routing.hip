@@ -1,4 +1,5 @@
-// Router top-k: one wave64 per token; up to 16 logits per lane (E <= 1024).
+// Router top-k: one wave64 per token; up to 16 logits per lane (E <= 1024), or for E <= 256
+// the decode kernels' DPP selection.
 // Router logits (router_logits_kernel): the MoE block's linear gate ahead of it.
 //
 // Selection is by logit value, descending, ties to the lower expert id, NaN ranked
@@ -79,6 +80,45 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const void* __restrict_
     if (lane < k) {
         idx[t * k + lane] = sel_i;
         wout[t * k + lane] = wgt;
+    }
+}
+
+// E <= 256: the same selection from DPP wave maxima and ballots (route_select, as the decode
+// kernels route), up to 4 logits per lane, and the weights from the selected logits.
+struct RouteParams {
+    const void* logits;
+    int logits_dtype, route_mode, E, k;
+};
+__global__ void __launch_bounds__(256) route_topk_dpp_kernel(const void* __restrict__ logits, int ldt, int64_t T,
+                                                             int E, int k, int mode, int32_t* __restrict__ idx,
+                                                             float* __restrict__ wout) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const RouteParams p{logits, ldt, mode, E, k};
+    float v[4];
+    load4(logits, ldt, t * E, E, lane, v);
+    const int es[4] = {lane, lane + 64, lane + 128, lane + 192};
+    uint32_t myk;
+    int mysel, myslot;
+    select_topk(p, lane, v, es, k, myk, mysel, myslot);
+    const float myval = route_key_value(myk);  // lane r < k: the r-th selected logit
+    const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));
+    float w;
+    if (mode == TSA_ROUTE_SOFTMAX_TOPK) {  // full softmax, not renormalised
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j < E) sum += expf(v[j] - top);
+        const float z = wave_sum(sum);  // every lane takes part in the exchange
+        w = lane < k ? expf(myval - top) / z : 0.0f;
+    } else {  // softmax over the k selected (= the renormalised full softmax)
+        const float ex = lane < k ? expf(myval - top) : 0.0f;
+        w = ex / wave_sum(ex);
+    }
+    if (lane < k) {
+        idx[t * k + lane] = mysel;
+        wout[t * k + lane] = w;
     }
 }
 
@@ -178,8 +218,12 @@ extern "C" int tsa_route_topk(const void* logits, int logits_dtype, int64_t T, i
     TSA_REQUIRE(T >= 0, TSA_ERR_INVALID_ARG, "negative token count");
     if (T == 0) return TSA_OK;
     TSA_REQUIRE(logits && idx && weights, TSA_ERR_INVALID_ARG, "null pointer");
-    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, as_stream(stream), logits,
-                       logits_dtype, T, (int)E, k, mode, idx, weights);
+    if (E <= 256)
+        hipLaunchKernelGGL(route_topk_dpp_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, as_stream(stream), logits,
+                           logits_dtype, T, (int)E, k, mode, idx, weights);
+    else
+        hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, as_stream(stream), logits,
+                           logits_dtype, T, (int)E, k, mode, idx, weights);
     TSA_LAUNCH_CHECK();
     return TSA_OK;
 }
