@@ -386,6 +386,11 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     const bool hbias = L.down_bias_off >= 0;
     const int rounds = (k + WAVES - 1) / WAVES;
 
+    // the first round's selection as scalar loads, ahead of every transfer (inside the loop
+    // they would be vector loads whose wait covers the transfers issued before them)
+    const int j0 = wave < k ? wave : k - 1;
+    const int64_t slot0 = uniform(p.sel_slot[t * k + j0]);
+    const float w0 = __int_as_float(uniform(__float_as_int(p.sel_w[t * k + j0])));
     lds_zero(zero, 0, KP, tid, 256);
     __syncthreads();  // the only barrier before the weighted sum: the waves stream independently
     float yv = 0.0f;  // lanes 0..15: row n0 + lane, this wave's weighted experts
@@ -393,9 +398,10 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     for (int rd = 0; rd < rounds; ++rd) {
         const int j = rd * WAVES + wave;
         if (j >= k) break;
-        // h(t, j) first, straight into LDS (each term zero-filled to TPB by the buffer
-        // bound; its address needs no routing), then the selection, the bias and the tile:
-        // CHUNKS + MM + 1 buffer loads younger than the transfer
+        // h(t, j) straight into LDS (each term zero-filled to TPB by the buffer bound), then
+        // the bias and the tile: CHUNKS + MM + 1 buffer loads younger than the transfer
+        const int64_t slot = rd == 0 ? slot0 : uniform(p.sel_slot[t * k + j]);
+        const float w = rd == 0 ? w0 : __int_as_float(uniform(__float_as_int(p.sel_w[t * k + j])));
         const uint8_t* src = p.h + (int64_t)(t * k + j) * 2 * I;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -405,8 +411,6 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
             for (int i = 0; i < TPB / 1024; ++i)
                 lds_dma16(rh, (uint32_t)(1024 * i + 16 * lane), hs_lds + (uint32_t)(r * TPB + 1024 * i));
         }
-        const int64_t slot = uniform(p.sel_slot[t * k + j]);
-        const float w = p.sel_w[t * k + j];
         if (slot < 0 || slot >= p.n_slots) {  // contributes nothing; the transfer must land before reuse or exit
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             continue;
