@@ -475,6 +475,9 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_gate_up_kernel(GsDecPara
     const int a = blockIdx.y, t = a / k, j = a - t * k;
     int* s_slot = reinterpret_cast<int*>(smem);
     float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
+    // given slots: the pair's slot as a scalar load ahead of the copies (after them it would
+    // be a vector load whose wait covers them)
+    const int64_t given = p.logits ? -1 : uniform(p.slots[(int64_t)t * k + j]);
     const uint32_t xbytes = (uint32_t)H * (p.x_dtype == TSA_F32 ? 4u : 2u);  // a multiple of 64
     // the activation copies: every wave, or (routed) every wave but wave 0, which selects the
     // token's experts meanwhile (its logit loads would otherwise queue behind its copies)
@@ -500,7 +503,7 @@ __global__ void __launch_bounds__(64 * GS_MAX_WAVES) gs_gate_up_kernel(GsDecPara
         __syncthreads();
         slot = uniform(s_slot[t * k + j]);
     } else {
-        slot = uniform(p.slots[(int64_t)t * k + j]);
+        slot = given;
     }
     const bool live = slot >= 0 && slot < p.n_slots;
     const int n0 = ((int)blockIdx.x * nw + wave) * p.rm;
