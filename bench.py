@@ -22,7 +22,11 @@ dense bf16 MFMA peak.
 --workload 1 / 2 / 4 measure the GGUF paths (a Q8_0 matvec, one Q4_K/Q6_K expert, a
 Qwen3-30B-A3B-shaped Q5_K/Q6_K MoE layer) the same way, in GB/s of algorithmic bytes.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5}]
+--workload 6 measures the grouped GGUF prefill at workload 4's layer shape (1024 tokens,
+128 Q5_K/Q6_K experts, zipf top-8): routing, grouping, both grouped GEMMs on bf16 MFMA
+(blocks decoded to bf16 in LDS) and the combine, in TFLOP/s against the dense bf16 peak.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5,6}]
 """
 from __future__ import annotations
 
@@ -298,9 +302,58 @@ class PrefillWorkload:
             _lib.BF16, self.ws.data_ptr(), self.ws.numel(), st))
 
 
+class GgufPrefillWorkload:
+    """Workload 6: resident GGUF layers at workload 4's expert shapes (Q5_K gate/up
+    2048 -> 768, Q6_K down, 128 experts), router logits and activations of a 1024-token
+    prefill; one step = one layer's whole batched MoE (softmax -> top-8)."""
+
+    TOKENS = 1024
+
+    def __init__(self, n_layers: int, dev: torch.device):
+        base = synth.workload(4, tokens=self.TOKENS)
+        self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
+        lay = base["layout"]
+        self.L = gguf_expert_layout(lay, {"gate": 13, "up": 13, "down": 14},
+                                    {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
+        g = torch.Generator(device=dev)
+        g.manual_seed(20261206)
+        self.pools = [torch.from_numpy(base["pool"]).to(dev)]
+        for _ in range(1, n_layers):  # further layers: random codes, super-block scales in range
+            p = torch.randint(0, 256, base["pool"].shape, dtype=torch.uint8, device=dev, generator=g)
+            MoEWorkload._fix_scales(p, lay, g)
+            self.pools.append(p)
+        self.logits = torch.from_numpy(base["logits"]).to(dev)
+        self.x = _bf16(base["x_bits"], dev)
+        self.T = self.x.shape[0]
+        self.y = torch.empty_like(self.x)
+        self.idx = torch.empty((self.T, self.k), dtype=torch.int32, device=dev)
+        self.w = torch.empty((self.T, self.k), dtype=torch.float32, device=dev)
+        self.expert_slot = torch.arange(self.E, dtype=torch.int32, device=dev)
+        self.ws = ops.moe_prefill_workspace(self.L, self.T, self.k, self.E, dev)
+        self.n_layers = n_layers
+
+    def flops_per_step(self) -> int:
+        return 2 * self.T * self.k * (2 * self.I * self.H + self.H * self.I)
+
+    def step(self, s: int) -> None:
+        lib = _lib.load()
+        st = torch.cuda.current_stream().cuda_stream
+        pool = self.pools[s % self.n_layers]
+        _lib.check(lib.tsa_route_topk(self.logits.data_ptr(), _lib.F32, self.T, self.E, self.k,
+                                      ops.ROUTE_MODES["softmax_then_topk"], self.idx.data_ptr(), self.w.data_ptr(), st))
+        _lib.check(lib.tsa_moe_prefill(
+            ctypes.byref(self.L), pool.data_ptr(), pool.shape[0], self.expert_slot.data_ptr(), self.E,
+            self.idx.data_ptr(), self.w.data_ptr(), self.T, self.k, self.x.data_ptr(), _lib.BF16, self.y.data_ptr(),
+            _lib.BF16, self.ws.data_ptr(), self.ws.numel(), st))
+
+
 def run_prefill(args, dev) -> int:
-    fp6 = args.prefill_mfma == "fp6"
-    wl = PrefillWorkload(args.layers_prefill, dev, _lib.PREFILL_FP6 if fp6 else _lib.PREFILL_BF16)
+    gguf = args.workload == 6
+    fp6 = args.prefill_mfma == "fp6" and not gguf
+    if gguf:
+        wl = GgufPrefillWorkload(args.layers_prefill, dev)
+    else:
+        wl = PrefillWorkload(args.layers_prefill, dev, _lib.PREFILL_FP6 if fp6 else _lib.PREFILL_BF16)
     peak = MFMA_F6F4_ALGO_PEAK_TFLOPS if fp6 else MFMA_BF16_PEAK_TFLOPS
     K, W = args.steps, args.warmup
     for s in range(W):
@@ -318,7 +371,7 @@ def run_prefill(args, dev) -> int:
     ms_step = ev0.elapsed_time(ev1) / K
     tflops = wl.flops_per_step() / (ms_step * 1e-3) / 1e12
     line = {
-        "metric": "MoE batched-prefill grouped MXFP4 expert GEMM TFLOP/s",
+        "metric": "MoE batched-prefill grouped " + ("GGUF" if gguf else "MXFP4") + " expert GEMM TFLOP/s",
         "value": round(tflops, 1),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -329,13 +382,18 @@ def run_prefill(args, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("mxfp4 weights x activations as two fp6 (e2m3) terms with per-32 e8m0 scales (from bf16), "
+        "dtype": ("gguf q5_k/q6_k blocks decoded and rounded to bf16 (as the reference's .to(bf16)), bf16 "
+                  "activations, bf16 MFMA, fp32 accumulate" if gguf else
+                  "mxfp4 weights x activations as two fp6 (e2m3) terms with per-32 e8m0 scales (from bf16), "
                   "scaled fp4 x fp6 MFMA, fp32 accumulate" if fp6 else
                   "mxfp4 weights expanded exactly to bf16, bf16 activations, bf16 MFMA, fp32 accumulate"),
-        "data": f"synthetic: seeded workload-5 layer + {args.layers_prefill - 1} random layers rotated per step",
-        "config": {"workload": "gpt-oss-20b-shaped mxfp4 moe layer prefill (2048 tokens, hidden 2880, 32 experts, "
-                               "zipf top-4)", "flops_per_step": wl.flops_per_step(), "tokens": wl.T,
-                   "prefill_mfma": args.prefill_mfma},
+        "data": f"synthetic: seeded workload-{4 if gguf else 5} layer + {args.layers_prefill - 1} random layers "
+                "rotated per step",
+        "config": {"workload": ("qwen3-30b-a3b-shaped gguf moe layer prefill (1024 tokens, hidden 2048, 128 "
+                                "experts, zipf top-8)" if gguf else
+                                "gpt-oss-20b-shaped mxfp4 moe layer prefill (2048 tokens, hidden 2880, 32 experts, "
+                                "zipf top-4)"), "flops_per_step": wl.flops_per_step(), "tokens": wl.T,
+                   "prefill_mfma": "bf16" if gguf else args.prefill_mfma},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None,
                      "note": "whole step (routing, grouping, activation terms, both GEMMs, combine) per HIP-event "
@@ -344,7 +402,7 @@ def run_prefill(args, dev) -> int:
                                          "peak = dense bf16 MFMA")},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(5)
+        line["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(line))
     return 0
 
@@ -369,13 +427,13 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
     """The reference's CPU path restated in torch (oracle.torch_cpu: whole-tensor vectorised
     dequant, then fp32 matmuls), timed on this host's cores: the median of >= min_runs runs
     after `warmup`, dequant and matmul timed separately. Workloads 1-4 time one decode step
-    (router top-k, then the selected experts); workload 5 a grouped prefill of a token
+    (router top-k, then the selected experts); workloads 5 and 6 a grouped prefill of a token
     sample. The routing itself (numpy top-k over the step's logits) is outside the timing."""
     from oracle import expert as oex
     from oracle import torch_cpu as otc
 
     cores, model = _cpu_host()
-    wl = synth.workload(wl_id)
+    wl = synth.workload(4, tokens=GgufPrefillWorkload.TOKENS) if wl_id == 6 else synth.workload(wl_id)
     if wl_id == 1:
         x = torch.from_numpy(wl["x"]).reshape(1, -1)
         w = otc.as_u8(wl["w"])
@@ -404,19 +462,24 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
         unit, what = "GB/s", f"single-token MoE-layer decodes (top-{wl['top_k']} of {wl['E']} experts)"
     else:
         n_tok = 64
-        idx, wts = oex.route_topk_then_softmax(wl["logits"][:n_tok], wl["top_k"])
+        route = oex.route_topk_then_softmax if wl_id == 5 else oex.route_softmax_then_topk
+        idx, wts = route(wl["logits"][:n_tok], wl["top_k"])
         x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"][:n_tok]))
         groups = oex.group_tokens_by_expert(idx)
         sel = {e: otc.torch_expert(wl["experts"][e]) for e in groups}
-        dequant = lambda: {e: otc.mxfp4_expert_weights(t) for e, t in sel.items()}  # noqa: E731
+        if wl_id == 5:
+            dequant = lambda: {e: otc.mxfp4_expert_weights(t) for e, t in sel.items()}  # noqa: E731
+            ffn = lambda xs, W, e: otc.mxfp4_expert_ffn(xs, *W, sel[e]["gate_up_bias"], sel[e]["down_bias"])  # noqa: E731
+        else:
+            dequant = lambda: {e: otc.gguf_expert_weights(t) for e, t in sel.items()}  # noqa: E731
+            ffn = lambda xs, W, e: otc.gguf_expert_ffn(xs, *W)  # noqa: E731
 
         def matmul(Ws):
             out = torch.zeros_like(x)
             for e, pairs in groups.items():
                 toks = torch.tensor([p[0] for p in pairs])
                 c = torch.tensor([float(wts[t, j]) for t, j in pairs]).unsqueeze(1)
-                out.index_add_(0, toks, c * otc.mxfp4_expert_ffn(x[toks], *Ws[e], sel[e]["gate_up_bias"],
-                                                                 sel[e]["down_bias"]))
+                out.index_add_(0, toks, c * ffn(x[toks], Ws[e], e))
             return out
 
         work = 2 * n_tok * wl["top_k"] * 3 * wl["hidden"] * wl["inter"]
@@ -450,8 +513,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
-    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--layers-prefill", type=int, default=3, help="workload 5: distinct layers rotated per step")
+    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5, 6])
+    ap.add_argument("--layers-prefill", type=int, default=3, help="workloads 5, 6: distinct layers rotated per step")
     ap.add_argument("--prefill-mfma", choices=["fp6", "bf16"], default="fp6",
                     help="workload 5: the GEMMs' MFMA form (fp4 x fp6 terms, or weights expanded to bf16)")
     ap.add_argument("--layers", type=int, default=24)
@@ -480,7 +543,7 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload == 5:
+    if args.workload in (5, 6):
         if "--steps" not in sys.argv:
             args.steps = 20
         if "--warmup" not in sys.argv:
