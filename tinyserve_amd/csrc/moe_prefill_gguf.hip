@@ -139,13 +139,21 @@ __device__ __forceinline__ void gf_put_bf16(uint8_t* dst, const float (&v)[32]) 
 template <int TY, bool GU>
 __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int en_i = blockIdx.y;
-    if (en_i >= *p.n_entries) return;  // workgroup-uniform
+    // Work id w = (entry, column tile) of this workgroup. Workgroups are dealt round the 8
+    // XCDs by linear id, so the ids are renumbered to give each XCD a run of consecutive
+    // work: the column tiles of an entry (which gather the same activation rows) and the
+    // tiles of an expert's consecutive entries (the same weight rows) then share one L2.
+    const int tiles = (int)gridDim.x, nact = *p.n_entries * tiles;
+    const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    if (lin >= nact) return;  // workgroup-uniform
+    const int xcd = lin & 7, q8 = nact >> 3, rem = nact & 7;
+    const int wid = xcd * q8 + (xcd < rem ? xcd : rem) + (lin >> 3);  // a bijection of [0, nact)
+    const int en_i = wid / tiles, tile = wid - en_i * tiles;
     const GfEntry en = p.table[en_i];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const int wn = wave & 3, wt = wave >> 2, g = lane >> 5, rr = lane & 31;
     const int K = p.K, P = K / GF_KP, N = p.N;
-    const int n0 = (int)blockIdx.x * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
+    const int n0 = tile * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
     const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
     const uint8_t* mat0 = base + p.w_off;
     const uint8_t* mat1 = base + (GU ? p.w2_off : p.w_off);
@@ -156,7 +164,8 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const uint32_t raw = lds0 + GF_ROFF;
 
-    // This thread's activation segment: sorted row xr, 64 bytes at 64 xs of each piece.
+    // This thread's activation segments: sorted row xr, 16 bytes at 128 i + 16 xs of each
+    // piece (i < 4), so the 8 threads of a row read 128 contiguous bytes per load.
     const int xr = tid >> 3, xs = tid & 7;
     const bool xlive = xr < en.rows;
     int64_t xrow = 0;
@@ -164,12 +173,12 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
         const int a = p.perm[en.row0 + xr];
         xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + xr);
     }
-    const uint16_t* xsrc = p.src + xrow * K + 32 * xs;
+    const uint16_t* xsrc = p.src + xrow * K + 8 * xs;
     uint4 xv[4];
     auto load_x = [&](int pc) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
+            xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 64 * i) : make_uint4(0u, 0u, 0u, 0u);
     };
 
     // This thread's decode work: weight row dr, unit 4 h + dq of each half h of each piece.
@@ -190,7 +199,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     for (int pc = 0; pc < P; ++pc) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(smem + GF_XOFF + xr * GF_RS + 64 * xs + 16 * i) = xv[i];
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(smem + GF_XOFF + xr * GF_RS + 128 * i + 16 * xs) = xv[i];
         __syncthreads();  // the piece's raw blocks and activations are in LDS; the other raw area is free
         if (pc + 1 < P) {
             gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw + (uint32_t)((pc + 1) & 1) * GF_RAW, wave, lane);
