@@ -136,6 +136,58 @@ __device__ __forceinline__ void gf_put_bf16(uint8_t* dst, const float (&v)[32]) 
                        pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7]));
 }
 
+// Unit u (32 values) of the K-quant super-block at sb (in LDS) as 16 packed bf16 pairs,
+// rounded to nearest even from the values decode_unit gives, working on four codes per
+// dword: the 4-bit codes of four values come out of one shift and mask, their fifth
+// (Q5_K) or fifth and sixth (Q6_K) bits out of another, and each byte converts to float in
+// one instruction. The arithmetic per value is decode_unit's: Q4_K / Q5_K a*q - c (a*q
+// exact, so one rounding, fused or not); Q6_K (d*sc) * (q - 32), here as (d*sc/4) times
+// the signed byte 4 (q - 32) (q ^ 32 is q - 32 as a 6-bit two's-complement field, and two
+// more bits to the left make the byte's sign), exact like the reference's product,
+// signed zeros included.
+template <int TY>
+__device__ __forceinline__ void gf_decode_bf16(const uint8_t* sb, int u, uint32_t o[16]) {
+    if constexpr (TY == 12 || TY == 13) {
+        uint32_t s[3], q[8], hb[8];
+        const uint32_t hd = ld_u32<4>(sb);
+        s[0] = ld_u32<4>(sb + 4);
+        s[1] = ld_u32<4>(sb + 8);
+        s[2] = ld_u32<4>(sb + 12);
+        ld_32bytes<16>(sb + (TY == 12 ? 16 : 48) + 32 * (u >> 1), q);
+        if constexpr (TY == 13) ld_32bytes<16>(sb + 16, hb);
+        const float d = f16_bits_to_f32(hd & 0xFFFFu), dmin = f16_bits_to_f32(hd >> 16);
+        uint32_t sc, m;
+        k_scale_min(s, u, sc, m);
+        const float a = d * (float)sc, c = dmin * (float)m;
+        const int sh = (u & 1) * 4;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            uint32_t qq = (q[w] >> sh) & 0x0F0F0F0Fu;
+            if constexpr (TY == 13) qq |= ((hb[w] >> u) & 0x01010101u) << 4;
+            o[2 * w] = pack_bf16x2(a * (float)(qq & 0xFFu) - c, a * (float)((qq >> 8) & 0xFFu) - c);
+            o[2 * w + 1] = pack_bf16x2(a * (float)((qq >> 16) & 0xFFu) - c, a * (float)(qq >> 24) - c);
+        }
+    } else {
+        static_assert(TY == 14, "K-quant types only");
+        const int hh = u >> 2, t = u & 3;
+        uint32_t ql[8], qh[8];
+        ld_32bytes<2>(sb + 64 * hh + 32 * (t & 1), ql);
+        ld_32bytes<2>(sb + 128 + 32 * hh, qh);
+        const uint32_t scw = ld_u16<2>(sb + 192 + 2 * u);
+        const float d = f16_bits_to_f32(ld_u16<2>(sb + 208));
+        const float d0 = 0.25f * (d * (float)(int8_t)(scw & 0xFF)), d1 = 0.25f * (d * (float)(int8_t)(scw >> 8));
+        const int shl = 4 * (t >> 1), shh = 2 * t;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t qq = ((ql[w] >> shl) & 0x0F0F0F0Fu) | (((qh[w] >> shh) & 0x03030303u) << 4);
+            const uint32_t y = (qq ^ 0x20202020u) << 2;  // four signed bytes 4 (q - 32)
+            const float dd = w < 4 ? d0 : d1;            // values 4w..4w+3: the first 16 take sc[2u]
+            o[2 * w] = pack_bf16x2(dd * (float)(int8_t)(y & 0xFFu), dd * (float)(int8_t)((y >> 8) & 0xFFu));
+            o[2 * w + 1] = pack_bf16x2(dd * (float)(int8_t)((y >> 16) & 0xFFu), dd * (float)(int8_t)(y >> 24));
+        }
+    }
+}
+
 template <int TY, bool GU>
 __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -210,11 +262,18 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             {
-                float v[32];
                 const int u = 4 * h + dq;
-                if constexpr (TY == 8) decode_unit<8, 2>(sb + 34 * u, 0, v);
-                else decode_unit<TY, gf_align<TY>()>(sb, u, v);
-                gf_put_bf16(dws, v);
+                if constexpr (TY == 8) {
+                    float v[32];
+                    decode_unit<8, 2>(sb + 34 * u, 0, v);
+                    gf_put_bf16(dws, v);
+                } else {
+                    uint32_t o[16];
+                    gf_decode_bf16<TY>(sb, u, o);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<uint4*>(dws + 16 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+                }
             }
             __syncthreads();  // this half's bf16 weights are complete
             const uint8_t* wa = smem + GF_WOFF + (32 * wn + rr) * GF_WS + 16 * g;
