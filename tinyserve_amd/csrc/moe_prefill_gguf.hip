@@ -169,12 +169,27 @@ __device__ __forceinline__ void gf_decode_bf16(const uint8_t* sb, int u, uint32_
         }
     } else {
         static_assert(TY == 14, "K-quant types only");
+        // A Q6_K block sits 2 bytes off a dword boundary for half the rows: read whole
+        // dwords from the boundary below and shift each pair into place (v_alignbyte_b32).
+        const uint32_t ob = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;  // 0 or 2
+        const uint32_t* wb = reinterpret_cast<const uint32_t*>(sb - ob);
+        auto ld32 = [&](int off, uint32_t (&w)[8]) {  // the 32 bytes at sb + off (off % 4 == 0)
+            uint32_t t9[9];
+#pragma unroll
+            for (int i = 0; i < 9; ++i) t9[i] = wb[(off >> 2) + i];  // the ninth stays inside the block
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_alignbyte(t9[i + 1], t9[i], ob);
+        };
+        auto ld16 = [&](int off) {  // the 2 bytes at sb + off (off even)
+            const uint32_t a = ob + (uint32_t)off;
+            return (wb[a >> 2] >> (8u * (a & 3u))) & 0xFFFFu;
+        };
         const int hh = u >> 2, t = u & 3;
         uint32_t ql[8], qh[8];
-        ld_32bytes<2>(sb + 64 * hh + 32 * (t & 1), ql);
-        ld_32bytes<2>(sb + 128 + 32 * hh, qh);
-        const uint32_t scw = ld_u16<2>(sb + 192 + 2 * u);
-        const float d = f16_bits_to_f32(ld_u16<2>(sb + 208));
+        ld32(64 * hh + 32 * (t & 1), ql);
+        ld32(128 + 32 * hh, qh);
+        const uint32_t scw = ld16(192 + 2 * u);
+        const float d = f16_bits_to_f32(ld16(208));
         const float d0 = 0.25f * (d * (float)(int8_t)(scw & 0xFF)), d1 = 0.25f * (d * (float)(int8_t)(scw >> 8));
         const int shl = 4 * (t >> 1), shh = 2 * t;
 #pragma unroll
