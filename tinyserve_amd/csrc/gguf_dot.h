@@ -141,6 +141,23 @@ template <> struct GqUnit<14> { static constexpr int V = 128, SB = 210, PER_SB =
 
 __device__ __forceinline__ u32x4 ld16u(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// N dwords of LDS data at byte address p, whatever its alignment. A ds_read_b128 / b64 off
+// its natural alignment is split by the LDS into slow pieces (Q8_0 blocks of 34 bytes and
+// Q6_K super-blocks of 210 sit off 16-byte boundaries), so whole dwords are read from the
+// boundary at or below p and each pair is shifted into place (v_alignbyte_b32). The dword
+// after the last is read only when p is off a dword boundary, when it holds data bytes.
+template <int N>
+__device__ __forceinline__ void lds_words(const uint8_t* p, uint32_t (&w)[N]) {
+    const uint32_t ob = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;
+    const uint32_t* b = reinterpret_cast<const uint32_t*>(p - ob);
+    uint32_t t[N + 1];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = b[i];
+    t[N] = ob ? b[N] : 0u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], ob);
+}
+
 typedef int gq_v4i __attribute__((ext_vector_type(4)));
 
 // Records of a buffer that starts mis bytes below n bytes of data: whole 16-byte chunks, so
@@ -390,11 +407,12 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
     if constexpr (TYPE == 8) {
         if (outside(g0)) return;
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b));
-        const u32x4 a = ld16u(b + 2), c = ld16u(b + 18);
+        uint32_t qw[8];
+        lds_words<8>(b + 2, qw);
         uint32_t ql[8], qh[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t wa = a[i] ^ 0x80808080u, wc = c[i] ^ 0x80808080u;  // q + 128
+            const uint32_t wa = qw[i] ^ 0x80808080u, wc = qw[4 + i] ^ 0x80808080u;  // q + 128
             ql[i] = wa & 0x0F0F0F0Fu;
             qh[i] = (wa >> 4) & 0x0F0F0F0Fu;
             ql[4 + i] = wc & 0x0F0F0F0Fu;
@@ -441,12 +459,16 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         }
     } else {  // Q6_K, half h of super-block u / 2: ql[64h, +64), qh[32h, +32), sc[8h, +8), d @208
         const uint32_t hh = u & 1;
+        uint32_t lw[16], hw[8], sw2[2];
+        lds_words<16>(b + 64 * hh, lw);
+        lds_words<8>(b + 128 + 32 * hh, hw);
+        lds_words<2>(b + 192 + 8 * hh, sw2);
         u32x4 l[4], qh[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) l[i] = ld16u(b + 64 * hh + 16 * i);
-        qh[0] = ld16u(b + 128 + 32 * hh);
-        qh[1] = ld16u(b + 144 + 32 * hh);
-        const uint2 scw = *reinterpret_cast<const uint2*>(b + 192 + 8 * hh);
+        for (int i = 0; i < 4; ++i) l[i] = u32x4{lw[4 * i], lw[4 * i + 1], lw[4 * i + 2], lw[4 * i + 3]};
+        qh[0] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        qh[1] = u32x4{hw[4], hw[5], hw[6], hw[7]};
+        const uint2 scw = make_uint2(sw2[0], sw2[1]);
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(b + 208));
         GqXr xr[2];
         ldx(0, xr[0]);

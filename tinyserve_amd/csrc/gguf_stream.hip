@@ -205,12 +205,7 @@ __device__ __forceinline__ float sb_dot(const uint8_t* p, int j, const XQ& x) {
     uint32_t q[8];
     if constexpr (TY == 8) {
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
-        const u32x4 a = ld16u(p + 2), b = ld16u(p + 18);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q[i] = a[i];
-            q[4 + i] = b[i];
-        }
+        lds_words<8>(p + 2, q);
         return d * qdot<0, 8>(q, x);
     } else if constexpr (TY == 12 || TY == 13) {
         constexpr int QS = TY == 12 ? 16 : 48;
@@ -237,14 +232,12 @@ __device__ __forceinline__ float sb_dot(const uint8_t* p, int j, const XQ& x) {
         return d * (float)sc * qdot<0, 8>(q, x) - dmin * (float)m * x.s32;
     } else {  // Q6_K: half h = j / 4, quarter t = j % 4 of it
         const int h = j >> 2, t = j & 3;
-        const u32x4 la = ld16u(p + 64 * h + 32 * (t & 1)), lb = ld16u(p + 64 * h + 32 * (t & 1) + 16);
-        const u32x4 ha = ld16u(p + 128 + 32 * h), hb = ld16u(p + 144 + 32 * h);
+        uint32_t lw[8], hw[8];
+        lds_words<8>(p + 64 * h + 32 * (t & 1), lw);
+        lds_words<8>(p + 128 + 32 * h, hw);
         const int shl = 4 * (t >> 1), shh = 2 * t;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q[i] = ((la[i] >> shl) & 0x0F0F0F0Fu) | (((ha[i] >> shh) & 0x03030303u) << 4);
-            q[4 + i] = ((lb[i] >> shl) & 0x0F0F0F0Fu) | (((hb[i] >> shh) & 0x03030303u) << 4);
-        }
+        for (int i = 0; i < 8; ++i) q[i] = ((lw[i] >> shl) & 0x0F0F0F0Fu) | (((hw[i] >> shh) & 0x03030303u) << 4);
         const uint32_t scw = *reinterpret_cast<const uint16_t*>(p + 192 + 2 * j);
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 208));
         const float sc0 = (float)(int8_t)(scw & 0xFFu), sc1 = (float)(int8_t)(scw >> 8);
