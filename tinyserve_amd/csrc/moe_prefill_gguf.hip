@@ -4,8 +4,8 @@
 // The reference's batched GGUF expert (tinyserve/ggml_forward.py:117-151,
 // _fallback_forward) decodes each projection to fp32, casts it to the activations' dtype
 // (bf16) and runs F.linear; here the same bf16 weights (decode_unit's bit-exact fp32 values,
-// rounded to nearest even) are formed in LDS piece by piece from the native blocks and never
-// reach HBM.
+// rounded to nearest even) are formed in registers piece by piece from the native blocks
+// and never reach HBM.
 //
 // After group_kernel has sorted the (token, j) assignments expert-major, each resident
 // expert's run of sorted rows is cut into tiles of up to 64 rows (gf_table_kernel). Two
@@ -15,14 +15,15 @@
 //   combine: y[t] = sum_j w[t, j] yk[t k + j] in j order (one writer per output).
 //
 // Workgroup: 8 waves, a tile of 64 sorted rows x 128 weight rows (gate_up: 64 gate rows and
-// the same 64 up rows, so the activation is formed in the workgroup); wave (wn, wt) owns
-// 32 weight rows x 32 sorted rows on v_mfma_f32_32x32x16_bf16 (weights the A operand,
-// activations the B operand). K advances in pieces of 256 values (one K-quant super-block
-// of each row, or 8 Q8_0 blocks): the piece's raw blocks for the 128 rows come in by
-// buffer-to-LDS copies (a 16-byte-aligned window per row) into one of two raw areas,
-// issued when the previous piece starts, the next piece's activations wait in registers,
-// and each half of the piece is decoded (one 32-value unit per thread) into the bf16
-// weight tile and multiplied.
+// the same 64 up rows, so the activation is formed in the workgroup). K advances in pieces
+// of 256 values (one K-quant super-block of each row, or 8 Q8_0 blocks): the piece's raw
+// blocks for the 128 rows come in by buffer-to-LDS copies (a 16-byte-aligned window per
+// row) into one of two raw areas, and its activations through registers into one of two
+// activation tiles, both issued when the previous piece starts. Wave (wr, kh) owns weight
+// rows 32 wr .. + 31 and K half kh of every piece: each lane decodes the values of its row
+// that it feeds v_mfma_f32_32x32x16_bf16 as the A operand straight into registers (no row
+// is decoded twice, no weight tile goes through LDS), the activations are the B operand
+// from LDS, and the two K halves' sums meet in LDS after the last piece.
 //
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/ggml_forward.py:117-151 (bf16 weights, F.linear,
@@ -45,16 +46,14 @@ constexpr int GF_THREADS = 512;
 constexpr int GF_BM = 64;                  // sorted rows per tile
 constexpr int GF_BN = 128;                 // weight rows per tile
 constexpr int GF_KP = 256;                 // values per K piece
-constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of the activation tile (bytes)
-constexpr int GF_WS = GF_KP + 16;          // ... of the decoded weights: half a piece (128 values) at a time
-constexpr int GF_XOFF = 0;                 // activations: GF_BM rows of a whole piece
-constexpr int GF_WOFF = GF_BM * GF_RS;     // decoded weights: GF_BN rows of half a piece
-constexpr int GF_ROFF = GF_WOFF + GF_BN * GF_WS;
+constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of an activation tile (bytes)
+constexpr int GF_XB = GF_BM * GF_RS;       // one activation tile: GF_BM rows of a whole piece; two of them
+constexpr int GF_ROFF = 2 * GF_XB;
 constexpr int GF_MAX_NCH = 18;             // 16-byte chunks of a row's raw piece window, at most (Q8_0)
 constexpr int GF_RAW = GF_BN * GF_MAX_NCH * 16;  // one raw area; two, for the piece in use and the next
-constexpr int GF_LDS = GF_ROFF + 2 * GF_RAW;     // 139 KB
-constexpr int GF_GS = 64 * 4 + 16;         // gate_up epilogue: fp32 row stride of the staged gate / up values
-static_assert(2 * GF_BM * GF_GS <= GF_BN * GF_WS, "the staged gate and up values fit the weight tile");
+constexpr int GF_LDS = GF_ROFF + 2 * GF_RAW;     // 138 KB
+constexpr int GF_SS = GF_BN + 4;           // epilogue: fp32 stride of a sorted row's staged sums (per K half)
+static_assert(2 * GF_BM * GF_SS * 4 <= GF_ROFF, "the staged sums fit the activation tiles");
 constexpr int GF_MIN_ASSIGN = 64;          // fewer assignments take the decode kernels
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -127,78 +126,81 @@ __device__ __forceinline__ void gf_issue_raw(const v4i_t& r0, const v4i_t& r1, u
     }
 }
 
-// 32 decoded values -> 16 bf16 words (round to nearest even) at dst (16-byte aligned).
-__device__ __forceinline__ void gf_put_bf16(uint8_t* dst, const float (&v)[32]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint4*>(dst + 16 * i) =
-            make_uint4(pack_bf16x2(v[8 * i], v[8 * i + 1]), pack_bf16x2(v[8 * i + 2], v[8 * i + 3]),
-                       pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7]));
-}
-
-// Unit u (32 values) of the K-quant super-block at sb (in LDS) as 16 packed bf16 pairs,
-// rounded to nearest even from the values decode_unit gives, working on four codes per
-// dword: the 4-bit codes of four values come out of one shift and mask, their fifth
-// (Q5_K) or fifth and sixth (Q6_K) bits out of another, and each byte converts to float in
-// one instruction. The arithmetic per value is decode_unit's: Q4_K / Q5_K a*q - c (a*q
-// exact, so one rounding, fused or not); Q6_K (d*sc) * (q - 32), here as (d*sc/4) times
-// the signed byte 4 (q - 32) (q ^ 32 is q - 32 as a 6-bit two's-complement field, and two
-// more bits to the left make the byte's sign), exact like the reference's product,
-// signed zeros included.
+// The 16 values of unit u (32 values) of the block at sb (in LDS) that lane half g feeds
+// the A operand with, values 8g .. 8g + 7 and 16 + 8g .. 16 + 8g + 7, as 8 packed bf16 words
+// rounded to nearest even from the values decode_unit gives, four codes per dword: the
+// 4-bit codes of four values come out of one shift and mask, their fifth (Q5_K) or fifth
+// and sixth (Q6_K) bits out of another, and each byte converts to float in one instruction.
+// The arithmetic per value is decode_unit's: Q4_K / Q5_K a*q - c (a*q exact, so one
+// rounding, fused or not); Q6_K (d*sc) * (q - 32), here as (d*sc/4) times the signed byte
+// 4 (q - 32) (q ^ 32 is q - 32 as a 6-bit two's-complement field, and two more bits to the
+// left make the byte's sign), exact like the reference's product, signed zeros included.
 template <int TY>
-__device__ __forceinline__ void gf_decode_bf16(const uint8_t* sb, int u, uint32_t o[16]) {
-    if constexpr (TY == 12 || TY == 13) {
-        uint32_t s[3], q[8], hb[8];
-        const uint32_t hd = ld_u32<4>(sb);
-        s[0] = ld_u32<4>(sb + 4);
-        s[1] = ld_u32<4>(sb + 8);
-        s[2] = ld_u32<4>(sb + 12);
-        ld_32bytes<16>(sb + (TY == 12 ? 16 : 48) + 32 * (u >> 1), q);
-        if constexpr (TY == 13) ld_32bytes<16>(sb + 16, hb);
-        const float d = f16_bits_to_f32(hd & 0xFFFFu), dmin = f16_bits_to_f32(hd >> 16);
+__device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uint32_t (&o)[8]) {
+    if constexpr (TY == 12 || TY == 13) {  // sb is 16-byte aligned
+        const u32x4 hdr = *reinterpret_cast<const u32x4*>(sb);
+        const uint8_t* qs = sb + (TY == 12 ? 16 : 48) + 32 * (u >> 1);
+        const uint2 q0 = *reinterpret_cast<const uint2*>(qs + 8 * g), q1 = *reinterpret_cast<const uint2*>(qs + 16 + 8 * g);
+        const uint32_t q[4] = {q0.x, q0.y, q1.x, q1.y};
+        uint32_t hb[4] = {0u, 0u, 0u, 0u};
+        if constexpr (TY == 13) {
+            const uint2 h0 = *reinterpret_cast<const uint2*>(sb + 16 + 8 * g), h1 = *reinterpret_cast<const uint2*>(sb + 32 + 8 * g);
+            hb[0] = h0.x; hb[1] = h0.y; hb[2] = h1.x; hb[3] = h1.y;
+        }
+        const float d = f16_bits_to_f32(hdr[0] & 0xFFFFu), dmin = f16_bits_to_f32(hdr[0] >> 16);
+        const uint32_t s3[3] = {hdr[1], hdr[2], hdr[3]};
         uint32_t sc, m;
-        k_scale_min(s, u, sc, m);
+        k_scale_min(s3, u, sc, m);
         const float a = d * (float)sc, c = dmin * (float)m;
         const int sh = (u & 1) * 4;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
+        for (int w = 0; w < 4; ++w) {
             uint32_t qq = (q[w] >> sh) & 0x0F0F0F0Fu;
             if constexpr (TY == 13) qq |= ((hb[w] >> u) & 0x01010101u) << 4;
             o[2 * w] = pack_bf16x2(a * (float)(qq & 0xFFu) - c, a * (float)((qq >> 8) & 0xFFu) - c);
             o[2 * w + 1] = pack_bf16x2(a * (float)((qq >> 16) & 0xFFu) - c, a * (float)(qq >> 24) - c);
         }
-    } else {
-        static_assert(TY == 14, "K-quant types only");
-        // A Q6_K block sits 2 bytes off a dword boundary for half the rows: read whole
-        // dwords from the boundary below and shift each pair into place (v_alignbyte_b32).
+    } else if constexpr (TY == 14) {
+        // A Q6_K block sits 2 bytes off a dword boundary for half the rows: whole dwords from
+        // the boundary below, each pair shifted into place (v_alignbyte_b32).
         const uint32_t ob = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;  // 0 or 2
         const uint32_t* wb = reinterpret_cast<const uint32_t*>(sb - ob);
-        auto ld32 = [&](int off, uint32_t (&w)[8]) {  // the 32 bytes at sb + off (off % 4 == 0)
-            uint32_t t9[9];
-#pragma unroll
-            for (int i = 0; i < 9; ++i) t9[i] = wb[(off >> 2) + i];  // the ninth stays inside the block
-#pragma unroll
-            for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_alignbyte(t9[i + 1], t9[i], ob);
+        auto ld4 = [&](int off, uint32_t (&w)[4]) {  // dwords 2g, 2g + 1, 2g + 4, 2g + 5 of the 32 bytes at sb + off
+            const int b0 = (off >> 2) + 2 * g;
+            const uint32_t t0 = wb[b0], t1 = wb[b0 + 1], t2 = wb[b0 + 2];
+            const uint32_t t4 = wb[b0 + 4], t5 = wb[b0 + 5], t6 = wb[b0 + 6];  // at most the ninth: inside the block
+            w[0] = __builtin_amdgcn_alignbyte(t1, t0, ob);
+            w[1] = __builtin_amdgcn_alignbyte(t2, t1, ob);
+            w[2] = __builtin_amdgcn_alignbyte(t5, t4, ob);
+            w[3] = __builtin_amdgcn_alignbyte(t6, t5, ob);
         };
         auto ld16 = [&](int off) {  // the 2 bytes at sb + off (off even)
             const uint32_t a = ob + (uint32_t)off;
             return (wb[a >> 2] >> (8u * (a & 3u))) & 0xFFFFu;
         };
         const int hh = u >> 2, t = u & 3;
-        uint32_t ql[8], qh[8];
-        ld32(64 * hh + 32 * (t & 1), ql);
-        ld32(128 + 32 * hh, qh);
+        uint32_t ql[4], qh[4];
+        ld4(64 * hh + 32 * (t & 1), ql);
+        ld4(128 + 32 * hh, qh);
         const uint32_t scw = ld16(192 + 2 * u);
         const float d = f16_bits_to_f32(ld16(208));
         const float d0 = 0.25f * (d * (float)(int8_t)(scw & 0xFF)), d1 = 0.25f * (d * (float)(int8_t)(scw >> 8));
         const int shl = 4 * (t >> 1), shh = 2 * t;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
+        for (int w = 0; w < 4; ++w) {
             const uint32_t qq = ((ql[w] >> shl) & 0x0F0F0F0Fu) | (((qh[w] >> shh) & 0x03030303u) << 4);
             const uint32_t y = (qq ^ 0x20202020u) << 2;  // four signed bytes 4 (q - 32)
-            const float dd = w < 4 ? d0 : d1;            // values 4w..4w+3: the first 16 take sc[2u]
+            const float dd = w < 2 ? d0 : d1;            // values below 16 take sc[2u], the rest sc[2u + 1]
             o[2 * w] = pack_bf16x2(dd * (float)(int8_t)(y & 0xFFu), dd * (float)(int8_t)((y >> 8) & 0xFFu));
             o[2 * w + 1] = pack_bf16x2(dd * (float)(int8_t)((y >> 16) & 0xFFu), dd * (float)(int8_t)(y >> 24));
+        }
+    } else {  // Q8_0: unit u is block u of the piece (34 bytes, 2-byte aligned)
+        float v[32];
+        decode_unit<8, 2>(sb + 34 * u, 0, v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // constant indices and a select (a variable index would go through scratch)
+            o[i] = g ? pack_bf16x2(v[8 + 2 * i], v[9 + 2 * i]) : pack_bf16x2(v[2 * i], v[2 * i + 1]);
+            o[4 + i] = g ? pack_bf16x2(v[24 + 2 * i], v[25 + 2 * i]) : pack_bf16x2(v[16 + 2 * i], v[17 + 2 * i]);
         }
     }
 }
@@ -218,7 +220,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const int en_i = wid / tiles, tile = wid - en_i * tiles;
     const GfEntry en = p.table[en_i];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
-    const int wn = wave & 3, wt = wave >> 2, g = lane >> 5, rr = lane & 31;
+    const int wr = wave & 3, kh = wave >> 2, g = lane >> 5, rr = lane & 31;
     const int K = p.K, P = K / GF_KP, N = p.N;
     const int n0 = tile * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
     const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
@@ -228,8 +230,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const uint32_t mis1 = (uint32_t)reinterpret_cast<uintptr_t>(mat1) & 15u;
     const v4i_t rs0 = gf_desc(mat0 - mis0, (p.w_bytes + mis0 + 15) & ~15ll),
                 rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
-    const uint32_t raw = lds0 + GF_ROFF;
+    const uint32_t raw = (uint32_t)reinterpret_cast<uintptr_t>(smem) + GF_ROFF;
 
     // This thread's activation segments: sorted row xr, 16 bytes at 128 i + 16 xs of each
     // piece (i < 4), so the 8 threads of a row read 128 contiguous bytes per load.
@@ -248,94 +249,97 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
             xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 64 * i) : make_uint4(0u, 0u, 0u, 0u);
     };
 
-    // This thread's decode work: weight row dr, unit 4 h + dq of each half h of each piece.
-    const int dr = tid >> 2, dq = tid & 3;
-    const int drow = GU ? n0 + (dr & 63) : n0 + dr;
+    // This lane's weight row: tile row 32 wr + rr (gate_up: rows 64.. are the up rows).
+    const int trow = 32 * wr + rr;
+    const int drow = GU ? n0 + (trow & 63) : n0 + trow;
     constexpr int NCH = gf_nch<TY>();
-    const uint32_t dmis = GU && dr >= 64 ? mis1 : mis0;
-    uint8_t* dws = smem + GF_WOFF + dr * GF_WS + 64 * dq;
+    const uint32_t dmis = GU && trow >= 64 ? mis1 : mis0;
 
-    v16f_t acc;
+    v16f_t acc[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
-    // Piece pc's raw blocks sit in raw area pc % 2; the next piece's copies go out as soon as
-    // the piece starts, so they fly during both halves' decode and MFMAs.
+    // Piece pc's raw blocks sit in raw area pc % 2 and its activations in tile pc % 2; the
+    // next piece's copies and loads go out as soon as the piece starts, so they fly during
+    // its decode and MFMAs. A tile or area is rewritten two pieces after it was read, with
+    // the barrier of the piece between.
     gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
     load_x(0);
     for (int pc = 0; pc < P; ++pc) {
+        uint8_t* xt = smem + (pc & 1) * GF_XB;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(smem + GF_XOFF + xr * GF_RS + 128 * i + 16 * xs) = xv[i];
-        __syncthreads();  // the piece's raw blocks and activations are in LDS; the other raw area is free
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(xt + xr * GF_RS + 128 * i + 16 * xs) = xv[i];
+        __syncthreads();  // the piece's raw blocks and activations are in LDS; area and tile (pc + 1) % 2 are free
         if (pc + 1 < P) {
             gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw + (uint32_t)((pc + 1) & 1) * GF_RAW, wave, lane);
             load_x(pc + 1);
         }
-        const uint8_t* sb = smem + GF_ROFF + (pc & 1) * GF_RAW + 16 * NCH * dr +
+        const uint8_t* sb = smem + GF_ROFF + (pc & 1) * GF_RAW + 16 * NCH * trow +
                             ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
+        // unit uu of the half, then its two K steps (the next unit's decode can issue while
+        // these MFMAs run); step j: K 16 j .. + 15 of the half, lane half g holds K 16 j + 8 g .. + 7
+        const uint8_t* xb = xt + rr * GF_RS + 256 * kh + 16 * g;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            {
-                const int u = 4 * h + dq;
-                if constexpr (TY == 8) {
-                    float v[32];
-                    decode_unit<8, 2>(sb + 34 * u, 0, v);
-                    gf_put_bf16(dws, v);
-                } else {
-                    uint32_t o[16];
-                    gf_decode_bf16<TY>(sb, u, o);
+        for (int uu = 0; uu < 4; ++uu) {
+            uint32_t av[8];
+            gf_decode_a<TY>(sb, 4 * kh + uu, g, av);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        *reinterpret_cast<uint4*>(dws + 16 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int j = 2 * uu + s2;
+                const bf16x8 A = __builtin_bit_cast(bf16x8, u32x4{av[4 * s2], av[4 * s2 + 1], av[4 * s2 + 2], av[4 * s2 + 3]});
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * t * GF_RS + 32 * j);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc[t], 0, 0, 0);
                 }
             }
-            __syncthreads();  // this half's bf16 weights are complete
-            const uint8_t* wa = smem + GF_WOFF + (32 * wn + rr) * GF_WS + 16 * g;
-            const uint8_t* xb = smem + GF_XOFF + (32 * wt + rr) * GF_RS + 256 * h + 16 * g;
-#pragma unroll
-            for (int j = 0; j < GF_KP / 32; ++j) {
-                const bf16x8 A = *reinterpret_cast<const bf16x8*>(wa + 32 * j);
-                const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * j);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc, 0, 0, 0);
-            }
-            __syncthreads();  // every wave is done with this half's weights (and, after the second, the activations)
         }
     }
 
-    // acc[4u + r] = weight row 32 wn + 8u + 4g + r of the tile, sorted row 32 wt + rr.
-    const int tk = 32 * wt + rr;
-    if constexpr (GU) {
-        // gate (wn 0, 1) and up (wn 2, 3) pre-activations as fp32 into LDS, then
-        // h = act(gate, up) rounded once to bf16, 8 columns per thread
-        float* stage = reinterpret_cast<float*>(smem + GF_WOFF + (wn >= 2 ? GF_BM * GF_GS : 0) + tk * GF_GS);
+    // acc[t][4u + r] = tile row 32 wr + 8u + 4g + r, sorted row 32 t + rr, over K half kh.
+    // Both halves' sums into LDS (the activation tiles are free once every wave is here),
+    // stage[kh][sorted row][tile row], then each output adds its two halves.
+    __syncthreads();
+    float* stage = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            *reinterpret_cast<float4*>(stage + 32 * (wn & 1) + 8 * u + 4 * g) =
-                make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
-        __syncthreads();
+            *reinterpret_cast<float4*>(stage + (kh * GF_BM + 32 * t + rr) * GF_SS + 32 * wr + 8 * u + 4 * g) =
+                make_float4(acc[t][4 * u], acc[t][4 * u + 1], acc[t][4 * u + 2], acc[t][4 * u + 3]);
+    __syncthreads();
+    if constexpr (GU) {
+        // h = act(gate, up) rounded once to bf16, 8 columns per thread
         const int hr = tid >> 3, hc = 8 * (tid & 7);
         if (hr < en.rows && n0 + hc < N) {
-            const float* gs = reinterpret_cast<const float*>(smem + GF_WOFF + hr * GF_GS) + hc;
-            const float* us = reinterpret_cast<const float*>(smem + GF_WOFF + GF_BM * GF_GS + hr * GF_GS) + hc;
+            const float* s0 = stage + hr * GF_SS + hc;
+            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
             float h[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gs[i], us[i]) : gs[i] * sigmoidf_(gs[i]) * us[i];
+            for (int i = 0; i < 8; ++i) {
+                const float gv = s0[i] + s1[i], uv = s0[64 + i] + s1[64 + i];
+                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gv, uv) : gv * sigmoidf_(gv) * uv;
+            }
             *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
                 make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
                            pack_bf16x2(h[6], h[7]));
         }
     } else {
-        if (tk < en.rows) {
-            const int64_t a = p.perm[en.row0 + tk];
+        // 16 output rows per thread, bf16 per assignment
+        const int hr = tid >> 3, hc = 16 * (tid & 7);
+        if (hr < en.rows && n0 + hc < N) {  // N % 16 == 0
+            const int64_t a = p.perm[en.row0 + hr];
+            const float* s0 = stage + hr * GF_SS + hc;
+            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
+            uint32_t o[8];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int n = n0 + 32 * wn + 8 * u + 4 * g;
-                if (n < N)  // N % 8 == 0: four rows from n are all in or all out
-                    *reinterpret_cast<uint2*>(p.out + a * N + n) =
-                        make_uint2(pack_bf16x2(acc[4 * u], acc[4 * u + 1]), pack_bf16x2(acc[4 * u + 2], acc[4 * u + 3]));
-            }
+            for (int i = 0; i < 8; ++i) o[i] = pack_bf16x2(s0[2 * i] + s1[2 * i], s0[2 * i + 1] + s1[2 * i + 1]);
+            uint4* dst = reinterpret_cast<uint4*>(p.out + a * N + n0 + hc);
+            dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+            dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
         }
     }
 }
