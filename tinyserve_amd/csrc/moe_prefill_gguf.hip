@@ -17,9 +17,9 @@
 // Workgroup: 8 waves, a tile of 64 sorted rows x 128 weight rows (gate_up: 64 gate rows and
 // the same 64 up rows, so the activation is formed in the workgroup). K advances in pieces
 // of 256 values (one K-quant super-block of each row, or 8 Q8_0 blocks): the piece's raw
-// blocks for the 128 rows come in by buffer-to-LDS copies (a 16-byte-aligned window per
-// row) into one of two raw areas, and its activations through registers into one of two
-// activation tiles, both issued when the previous piece starts. Wave (wr, kh) owns weight
+// blocks for the 128 rows (a 16-byte-aligned window per row) and its activations come in
+// by buffer-to-LDS copies, the activations into one of two tiles as the previous piece
+// starts, the raw blocks into one of three areas two pieces ahead. Wave (wr, kh) owns weight
 // rows 32 wr .. + 31 and K half kh of every piece: each lane decodes the values of its row
 // that it feeds v_mfma_f32_32x32x16_bf16 as the A operand straight into registers (no row
 // is decoded twice, no weight tile goes through LDS), the activations are the B operand
@@ -46,14 +46,11 @@ constexpr int GF_THREADS = 512;
 constexpr int GF_BM = 64;                  // sorted rows per tile
 constexpr int GF_BN = 128;                 // weight rows per tile
 constexpr int GF_KP = 256;                 // values per K piece
-constexpr int GF_RS = 2 * GF_KP + 16;      // LDS row stride of an activation tile (bytes)
-constexpr int GF_XB = GF_BM * GF_RS;       // one activation tile: GF_BM rows of a whole piece; two of them
-constexpr int GF_ROFF = 2 * GF_XB;
-constexpr int GF_MAX_NCH = 18;             // 16-byte chunks of a row's raw piece window, at most (Q8_0)
-constexpr int GF_RAW = GF_BN * GF_MAX_NCH * 16;  // one raw area; two, for the piece in use and the next
-constexpr int GF_LDS = GF_ROFF + 2 * GF_RAW;     // 138 KB
+constexpr int GF_RS = 2 * GF_KP;           // an activation tile row: one piece of a sorted row (bf16), 32 chunks
+constexpr int GF_XB = GF_BM * GF_RS;       // one activation tile; two of them
+constexpr int GF_ROFF = 2 * GF_XB;         // then the raw areas
 constexpr int GF_SS = GF_BN + 4;           // epilogue: fp32 stride of a sorted row's staged sums (per K half)
-static_assert(2 * GF_BM * GF_SS * 4 <= GF_ROFF, "the staged sums fit the activation tiles");
+constexpr int GF_STAGE = 2 * GF_BM * GF_SS * 4;
 constexpr int GF_MIN_ASSIGN = 64;          // fewer assignments take the decode kernels
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -66,6 +63,15 @@ struct GfEntry {
 // Raw bytes of one row's K piece: a K-quant super-block, or 8 Q8_0 blocks.
 template <int TY> struct GfType { static constexpr int PB = TY == 8 ? 272 : TY == 12 ? 144 : TY == 13 ? 176 : 210; };
 template <int TY> constexpr int gf_nch() { return (GfType<TY>::PB + 15 + 15) / 16; }
+// Raw areas: the piece in use and the next two (one ahead for Q8_0, whose windows would not
+// fit three areas beside the activation tiles). One area: the 128 rows' windows.
+template <int TY> constexpr int gf_depth() { return TY == 8 ? 2 : 3; }
+template <int TY> constexpr int gf_raw() { return GF_BN * gf_nch<TY>() * 16; }
+template <int TY> constexpr int gf_lds() {
+    return GF_ROFF + gf_depth<TY>() * gf_raw<TY>() > GF_STAGE ? GF_ROFF + gf_depth<TY>() * gf_raw<TY>() : GF_STAGE;
+}
+static_assert(gf_lds<8>() <= 160 * 1024 && gf_lds<12>() <= 160 * 1024 && gf_lds<13>() <= 160 * 1024 &&
+                  gf_lds<14>() <= 160 * 1024, "LDS per workgroup");
 // Alignment of a row's raw piece in LDS, which keeps its global address modulo 16: the
 // K-quant 4/5-bit super-blocks (144 / 176 bytes) stay 16-aligned, Q6_K / Q8_0 2-aligned
 // (the host requires pool, slot size and offsets to keep that).
@@ -77,6 +83,7 @@ struct GfGemm {
     const int* n_entries;
     const GfEntry* table;
     const uint16_t* src;      // gate_up: x [T, K] (rows through perm / k); down: h [n, K] in sorted order
+    int64_t src_bytes;
     const int32_t* perm;      // sorted position -> assignment id (token * k + j)
     int k;
     uint16_t* out;            // gate_up: h [n, N]; down: yk [T k, N]
@@ -230,24 +237,35 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const uint32_t mis1 = (uint32_t)reinterpret_cast<uintptr_t>(mat1) & 15u;
     const v4i_t rs0 = gf_desc(mat0 - mis0, (p.w_bytes + mis0 + 15) & ~15ll),
                 rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
-    const uint32_t raw = (uint32_t)reinterpret_cast<uintptr_t>(smem) + GF_ROFF;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const uint32_t raw = lds0 + GF_ROFF;
+    constexpr int D = gf_depth<TY>(), RAW = gf_raw<TY>();
 
-    // This thread's activation segments: sorted row xr, 16 bytes at 128 i + 16 xs of each
-    // piece (i < 4), so the 8 threads of a row read 128 contiguous bytes per load.
-    const int xr = tid >> 3, xs = tid & 7;
-    const bool xlive = xr < en.rows;
-    int64_t xrow = 0;
-    if (xlive) {
-        const int a = p.perm[en.row0 + xr];
-        xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + xr);
-    }
-    const uint16_t* xsrc = p.src + xrow * K + 8 * xs;
-    uint4 xv[4];
-    auto load_x = [&](int pc) {
+    // Activation tiles: row r holds sorted row r's piece as 32 chunks of 16 bytes, chunk c in
+    // slot c ^ (r % 32), so the 32 rows of an MFMA operand read fall on distinct banks. They
+    // arrive by buffer-to-LDS copies: wave w's copy i fills rows 8w + 2i and 8w + 2i + 1 (1 KB,
+    // lane l: row 8w + 2i + l / 32, slot l % 32, so it reads chunk (l % 32) ^ row % 32).
+    // Rows past the tile's read zeros (an offset past the buffer's end).
+    const v4i_t rx = gf_desc(reinterpret_cast<const uint8_t*>(p.src), p.src_bytes);
+    uint32_t xo[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            xv[i] = xlive ? *reinterpret_cast<const uint4*>(xsrc + (int64_t)pc * GF_KP + 64 * i) : make_uint4(0u, 0u, 0u, 0u);
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * wave + 2 * i + (lane >> 5);
+        xo[i] = 0x80000000u;
+        if (r < en.rows) {
+            const int a = p.perm[en.row0 + r];
+            const int64_t xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + r);
+            xo[i] = (uint32_t)(xrow * K * 2) + 16u * (uint32_t)((lane & 31) ^ (r & 31));
+        }
+    }
+    auto issue_x = [&](int pc) {
+        const uint32_t t = lds0 + (uint32_t)(pc & 1) * GF_XB + (uint32_t)(8 * wave) * GF_RS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gf_dma(rx, xo[i] + (uint32_t)pc * (2 * GF_KP), t + (uint32_t)(2 * i) * GF_RS);
     };
+    // this wave's raw copies per piece: instructions ii = wave, wave + 8, .. below NI
+    constexpr int NI = (GF_BN * gf_nch<TY>() + 63) / 64, RWA = (NI + 7) / 8, RWB = NI / 8;
+    const bool rw_more = wave < NI % 8;
 
     // This lane's weight row: tile row 32 wr + rr (gate_up: rows 64.. are the up rows).
     const int trow = 32 * wr + rr;
@@ -261,27 +279,33 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
-    // Piece pc's raw blocks sit in raw area pc % 2 and its activations in tile pc % 2; the
-    // next piece's copies and loads go out as soon as the piece starts, so they fly during
-    // its decode and MFMAs. A tile or area is rewritten two pieces after it was read, with
-    // the barrier of the piece between.
+    // Piece pc's activations sit in tile pc % 2 and its raw blocks in area pc % D. As piece
+    // pc starts, the copies of piece pc + 1's activations and then of piece pc + D - 1's raw
+    // blocks go out, so the raw blocks fly for D - 1 pieces. A tile or area is rewritten one
+    // piece after it was last read, with the barrier of the piece between. Every load here
+    // is an inline-assembly copy (the compiler counts none of them), so the waits are
+    // explicit: at the top of piece pc everything but the last raw copies issued (those of
+    // piece pc + D - 2, RWA or RWB instructions for this wave) must have landed.
+    issue_x(0);
     gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
-    load_x(0);
+    if (D == 3 && P > 1) gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 1, K, raw + RAW, wave, lane);
     for (int pc = 0; pc < P; ++pc) {
-        uint8_t* xt = smem + (pc & 1) * GF_XB;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(xt + xr * GF_RS + 128 * i + 16 * xs) = xv[i];
-        __syncthreads();  // the piece's raw blocks and activations are in LDS; area and tile (pc + 1) % 2 are free
-        if (pc + 1 < P) {
-            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + 1, K, raw + (uint32_t)((pc + 1) & 1) * GF_RAW, wave, lane);
-            load_x(pc + 1);
+        const uint8_t* xt = smem + (pc & 1) * GF_XB;
+        if (D == 3 && pc + 1 < P) {
+            if (rw_more) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RWA) : "memory");
+            else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RWB) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        const uint8_t* sb = smem + GF_ROFF + (pc & 1) * GF_RAW + 16 * NCH * trow +
+        __syncthreads();  // piece pc's raw blocks and activations are in LDS; tile (pc + 1) % 2 and area (pc + D - 1) % D are free
+        if (pc + 1 < P) issue_x(pc + 1);
+        if (pc + D - 1 < P)
+            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + D - 1, K, raw + (uint32_t)((pc + D - 1) % D) * RAW, wave, lane);
+        const uint8_t* sb = smem + GF_ROFF + (pc % D) * RAW + 16 * NCH * trow +
                             ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
         // unit uu of the half, then its two K steps (the next unit's decode can issue while
         // these MFMAs run); step j: K 16 j .. + 15 of the half, lane half g holds K 16 j + 8 g .. + 7
-        const uint8_t* xb = xt + rr * GF_RS + 256 * kh + 16 * g;
+        const uint8_t* xr0 = xt + rr * GF_RS;  // sorted row rr (t = 0) and 32 + rr (t = 1): same swizzle
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {
             uint32_t av[8];
@@ -292,7 +316,8 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
                 const bf16x8 A = __builtin_bit_cast(bf16x8, u32x4{av[4 * s2], av[4 * s2 + 1], av[4 * s2 + 2], av[4 * s2 + 3]});
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    const bf16x8 B = *reinterpret_cast<const bf16x8*>(xb + 32 * t * GF_RS + 32 * j);
+                    const int c = (16 * kh + 2 * j + g) ^ rr;  // chunk of K 128 kh + 16 j + 8 g
+                    const bf16x8 B = *reinterpret_cast<const bf16x8*>(xr0 + 32 * t * GF_RS + 16 * c);
                     acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc[t], 0, 0, 0);
                 }
             }
@@ -300,7 +325,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     }
 
     // acc[t][4u + r] = tile row 32 wr + 8u + 4g + r, sorted row 32 t + rr, over K half kh.
-    // Both halves' sums into LDS (the activation tiles are free once every wave is here),
+    // Both halves' sums into LDS (nothing is in flight and every wave is here),
     // stage[kh][sorted row][tile row], then each output adds its two halves.
     __syncthreads();
     float* stage = reinterpret_cast<float*>(smem);
@@ -389,6 +414,8 @@ const void* gf_pick(int t, bool gu) {
     return nullptr;
 }
 
+int gf_lds_of(int t) { return t == 8 ? gf_lds<8>() : t == 12 ? gf_lds<12>() : t == 13 ? gf_lds<13>() : gf_lds<14>(); }
+
 int64_t gf_al256(int64_t v) { return (v + 255) / 256 * 256; }
 
 struct GfWs {
@@ -463,9 +490,9 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
         for (int t : {8, 12, 13, 14})
             for (bool gu : {true, false})
                 if (lds_err == hipSuccess)
-                    lds_err = hipFuncSetAttribute(gf_pick(t, gu), hipFuncAttributeMaxDynamicSharedMemorySize, GF_LDS);
+                    lds_err = hipFuncSetAttribute(gf_pick(t, gu), hipFuncAttributeMaxDynamicSharedMemorySize, gf_lds_of(t));
     });
-    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", GF_LDS, hipGetErrorString(lds_err));
+    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS): %s", hipGetErrorString(lds_err));
     const unsigned max_entries = (unsigned)(n / GF_BM + (E < n ? E : n) + 1);
     auto mat_bytes = [](int t, int64_t rows, int64_t K) {
         return rows * (K / GF_KP) * (t == 8 ? 272 : t == 12 ? 144 : t == 13 ? 176 : 210);
@@ -481,6 +508,7 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     g.L = L;
     // gate_up: x [T, H] -> h [n, I]
     g.src = x;
+    g.src_bytes = T * L.hidden * 2;
     g.out = h;
     g.N = I;
     g.K = H;
@@ -489,9 +517,10 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     g.w_bytes = mat_bytes(L.gate_type, I, H);
     void* args[] = {&g};
     TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.gate_type, true), dim3((unsigned)((I + GF_BN / 2 - 1) / (GF_BN / 2)), max_entries),
-                                  dim3(GF_THREADS), args, GF_LDS, stream));
+                                  dim3(GF_THREADS), args, gf_lds_of(L.gate_type), stream));
     // down: h [n, I] -> yk [n, H] by assignment id
     g.src = h;
+    g.src_bytes = n * L.inter * 2;
     g.out = yk;
     g.N = H;
     g.K = I;
@@ -499,7 +528,7 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     g.w2_off = L.down_off;
     g.w_bytes = mat_bytes(L.down_type, H, I);
     TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.down_type, false), dim3((unsigned)((H + GF_BN - 1) / GF_BN), max_entries),
-                                  dim3(GF_THREADS), args, GF_LDS, stream));
+                                  dim3(GF_THREADS), args, gf_lds_of(L.down_type), stream));
     return pf_combine(yk, idx, weights, expert_slot, E, n_slots, T, k, H, y, y_dtype, stream);
 }
 
