@@ -205,7 +205,7 @@ int tsa_moe_prefill_workspace_size(const tsa_expert_layout* layout, int64_t T, i
 /* Batched prefill: tokens grouped by expert, one grouped dequant-GEMM per phase on MFMA,
  * then the weighted combine out[t] = sum_j weights[t, j] * y_(t,j). Tiled MXFP4 pools (bf16
  * x) run fp4 x fp6 (or bf16) GEMMs; GGUF pools (bf16 x, hidden and inter multiples of 256,
- * T k >= 64, block-aligned slots) run bf16 GEMMs with the blocks decoded in LDS, as the
+ * T k >= 64, block-aligned slots) run bf16 GEMMs on blocks decoded on the fly, as the
  * reference's batched GGUF expert casts its weights to bf16 (tinyserve/ggml_forward.py:
  * 117-151); other calls run the decode kernels over the assignments.
  * expert_slot [E] int32 maps expert id -> slot (-1: not resident, contributes zero);
