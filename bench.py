@@ -26,7 +26,11 @@ Qwen3-30B-A3B-shaped Q5_K/Q6_K MoE layer) the same way, in GB/s of algorithmic b
 128 Q5_K/Q6_K experts, zipf top-8): routing, grouping, both grouped GEMMs on bf16 MFMA
 (blocks decoded to bf16 in LDS) and the combine, in TFLOP/s against the dense bf16 peak.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5,6}]
+--workload 7 measures the standalone MXFP4 matvec (tsa_mxfp4_matvec, the reference's
+dot_scaled_vecmat / _mxfp4_linear) at GPT-OSS-20B's gate_up shape: 5760 x 2880 checkpoint-order
+blocks and scales, bf16 bias and x, batch 1, in GB/s of algorithmic bytes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5,6,7}]
 """
 from __future__ import annotations
 
@@ -85,7 +89,7 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 # the experts in checkpoint order).
 STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
-                "4": ("gq_phase_a", "gq_phase_b")}
+                "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_kernel",)}
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str, key: str, command: str) -> dict:
@@ -259,6 +263,39 @@ class GgufWorkload:
                                           st))
 
 
+class MxMatvecWorkload:
+    """Workload 7: one MXFP4 matrix in the checkpoint order ([N, K/32, 16] blocks, [N, K/32]
+    e8m0 scales, bf16 bias), GPT-OSS-20B's gate_up shape, y = x W^T + b for one bf16 token
+    (tsa_mxfp4_matvec), over copies rotated per step (about 0.56 GB) so the 256 MB
+    Infinity Cache cannot serve them. Random codes, scales in 2^-8 .. 2^-2."""
+
+    def __init__(self, n_steps: int, dev: torch.device):
+        self.N, self.K = 5760, 2880
+        G = self.K // 32
+        self.copies = 64
+        g = torch.Generator(device=dev)
+        g.manual_seed(20261207)
+        self.blocks = torch.randint(0, 256, (self.copies, self.N, G * 16), dtype=torch.uint8, device=dev, generator=g)
+        self.scales = torch.randint(119, 126, (self.copies, self.N, G), dtype=torch.uint8, device=dev, generator=g)
+        self.bias = (torch.randn(self.N, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        self.x = torch.randn((n_steps, self.K), device=dev, generator=g).to(torch.bfloat16)
+        self.y = torch.empty((n_steps, self.N), device=dev, dtype=torch.bfloat16)
+        self.logits = self.x  # the step count source for the warmup loop
+        self.tiled = False
+
+    def bytes_per_step(self) -> int:
+        """Blocks (K/2 bytes per row) + scales (K/32) + bf16 bias, x and y."""
+        return self.N * (self.K // 2 + self.K // 32) + 2 * self.N + 2 * self.K + 2 * self.N
+
+    def step(self, s: int) -> None:
+        lib = _lib.load()
+        st = torch.cuda.current_stream().cuda_stream
+        c = s % self.copies
+        _lib.check(lib.tsa_mxfp4_matvec(self.blocks[c].data_ptr(), self.scales[c].data_ptr(), self.bias.data_ptr(),
+                                        _lib.BF16, self.x[s].data_ptr(), _lib.BF16, 1, self.y[s].data_ptr(), _lib.BF16,
+                                        self.N, self.K, st))
+
+
 class PrefillWorkload:
     """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
     2048-token prefill; one step = one layer's whole batched MoE."""
@@ -428,12 +465,12 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
     dequant, then fp32 matmuls), timed on this host's cores: the median of >= min_runs runs
     after `warmup`, dequant and matmul timed separately. Workloads 1-4 time one decode step
     (router top-k, then the selected experts); workloads 5 and 6 a grouped prefill of a token
-    sample. The routing itself (numpy top-k over the step's logits) is outside the timing."""
+    sample; workload 7 one MXFP4 matvec. The routing itself (numpy top-k over the step's logits) is outside the timing."""
     from oracle import expert as oex
     from oracle import torch_cpu as otc
 
     cores, model = _cpu_host()
-    wl = synth.workload(4, tokens=GgufPrefillWorkload.TOKENS) if wl_id == 6 else synth.workload(wl_id)
+    wl = {6: lambda: synth.workload(4, tokens=GgufPrefillWorkload.TOKENS), 7: dict}.get(wl_id, lambda: synth.workload(wl_id))()
     if wl_id == 1:
         x = torch.from_numpy(wl["x"]).reshape(1, -1)
         w = otc.as_u8(wl["w"])
@@ -446,6 +483,16 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
         dequant = lambda: otc.gguf_expert_weights(e)  # noqa: E731
         matmul = lambda W: otc.gguf_expert_ffn(x, *W)  # noqa: E731
         work, unit, what = wl["layout"].total_bytes + 2 * 2 * wl["hidden"], "GB/s", "single-expert FFNs"
+    elif wl_id == 7:
+        N, K = 5760, 2880
+        rng = np.random.default_rng(7)
+        blocks = torch.from_numpy(rng.integers(0, 256, (N, K // 32, 16), dtype=np.uint8))
+        scales = torch.from_numpy(rng.integers(119, 126, (N, K // 32), dtype=np.uint8))
+        bias = torch.from_numpy(rng.normal(0.0, 0.02, N).astype(np.float32))
+        x = torch.from_numpy(rng.normal(0.0, 1.0, (1, K)).astype(np.float32))
+        dequant = lambda: otc.mxfp4_dequant(blocks, scales)  # noqa: E731
+        matmul = lambda W: x @ W.T + bias  # noqa: E731
+        work, unit, what = N * (K // 2 + K // 32) + 2 * N + 2 * K + 2 * N, "GB/s", "MXFP4 5760 x 2880 matvecs"
     elif wl_id in (3, 4):
         x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"][:1]))
         route = oex.route_topk_then_softmax if wl_id == 3 else oex.route_softmax_then_topk
@@ -513,7 +560,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
-    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5, 6])
+    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5, 6, 7])
     ap.add_argument("--layers-prefill", type=int, default=3, help="workloads 5, 6: distinct layers rotated per step")
     ap.add_argument("--prefill-mfma", choices=["fp6", "bf16"], default="fp6",
                     help="workload 5: the GEMMs' MFMA form (fp4 x fp6 terms, or weights expanded to bf16)")
@@ -556,13 +603,16 @@ def main() -> int:
     if args.workload in (1, 2):
         wl = GgufWorkload(args.workload, max(K, W), dev)
         n_layers = wl.copies
+    elif args.workload == 7:
+        wl = MxMatvecWorkload(max(K, W), dev)
+        n_layers = wl.copies
     else:
         wl = MoEWorkload(args.workload, n_layers, max(K, W, n_layers), dev, tiled=not args.checkpoint_order)
     torch.cuda.synchronize()
 
     # warmup (eager), also validates every call
     for s in range(W):
-        wl.step(s % max(len(wl.logits), 1) if args.workload > 2 else s)
+        wl.step(s % max(len(wl.logits), 1) if args.workload in (3, 4) else s)
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream()
@@ -608,13 +658,15 @@ def main() -> int:
         "dtype": {1: "gguf q8_0 weights, fp32 activations (int8 hi/lo terms per 32 values), int32 dots, fp32 accumulate",
                   2: "gguf q4_k/q6_k weights, bf16 activations, fp32 accumulate",
                   3: "mxfp4 weights (e2m1 x e8m0), bf16 activations, fp32 accumulate",
-                  4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate"}[args.workload],
+                  4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate",
+                  7: "mxfp4 weights (e2m1 x e8m0), bf16 activations and bias, fp32 accumulate"}[args.workload],
         "data": f"synthetic: seeded native-format weights, {n_layers} resident layers (or copies) rotated per step",
         "config": {
             "workload": {1: "gguf q8_0 matvec 2880 x 2880 (GGMLLinear, batch 1)",
                          2: "one gguf expert ffn, q4_k gate/up 2880 -> 2880, q6_k down (batch 1)",
                          3: "gpt-oss-20b-shaped mxfp4 moe layer decode (hidden 2880, 32 experts, top-4, batch 1)",
-                         4: "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)"}[args.workload],
+                         4: "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)",
+                         7: "mxfp4 matvec 5760 x 2880 (gpt-oss-20b gate_up shape, dot_scaled_vecmat, batch 1)"}[args.workload],
             "bytes_per_step": nbytes,
             "layers_rotated": n_layers,
             "pool_layout": "mxfp4 16-row mfma tiles" if wl.tiled else "checkpoint order",

@@ -13,12 +13,48 @@ namespace {
 constexpr int ROWS_PER_WG = 8;
 constexpr int MAX_X_LDS_BYTES = 64 * 1024;
 
+// The chunk's tn token rows of x (contiguous in memory) as float32 into xs, rows past tn
+// zero. From a 16-byte-aligned source in 16-byte loads, four per thread issued before any
+// is converted (one element per load, as below, costs a memory round trip per element).
 template <int TCH>
 __device__ __forceinline__ int stage_x(float* xs, const void* x, int x_dtype, int64_t t0, int64_t T, int64_t K) {
     const int tn = (int)((T - t0) < TCH ? (T - t0) : TCH);
-    for (int64_t i = threadIdx.x; i < (int64_t)TCH * K; i += blockDim.x) {
-        const int64_t t = i / K;
-        xs[i] = t < tn ? load_act(x, x_dtype, (t0 + t) * K + (i - t * K)) : 0.0f;
+    const int es = x_dtype == TSA_F32 ? 4 : 2, per = 16 / es;  // elements per 16-byte chunk
+    const uint8_t* src = static_cast<const uint8_t*>(x) + t0 * K * es;
+    if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {  // K % 32 == 0: rows are whole chunks
+        const int64_t nch = (int64_t)tn * K / per;
+        for (int64_t c0 = 0; c0 < nch; c0 += 4 * (int64_t)blockDim.x) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t c = c0 + u * (int64_t)blockDim.x + threadIdx.x;
+                v[u] = c < nch ? reinterpret_cast<const uint4*>(src)[c] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t c = c0 + u * (int64_t)blockDim.x + threadIdx.x;
+                if (c >= nch) continue;
+                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                float* d = xs + c * per;
+                if (x_dtype == TSA_F32) {
+                    *reinterpret_cast<float4*>(d) = make_float4(__uint_as_float(w[0]), __uint_as_float(w[1]),
+                                                                __uint_as_float(w[2]), __uint_as_float(w[3]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float lo = x_dtype == TSA_BF16 ? bf16_bits_to_f32(w[i] & 0xFFFFu) : f16_bits_to_f32(w[i]);
+                        const float hi = x_dtype == TSA_BF16 ? bf16_bits_to_f32(w[i] >> 16) : f16_bits_to_f32(w[i] >> 16);
+                        *reinterpret_cast<float2*>(d + 2 * i) = make_float2(lo, hi);
+                    }
+                }
+            }
+        }
+        for (int64_t i = (int64_t)tn * K + threadIdx.x; i < (int64_t)TCH * K; i += blockDim.x) xs[i] = 0.0f;
+    } else {
+        for (int64_t i = threadIdx.x; i < (int64_t)TCH * K; i += blockDim.x) {
+            const int64_t t = i / K;
+            xs[i] = t < tn ? load_act(x, x_dtype, (t0 + t) * K + (i - t * K)) : 0.0f;
+        }
     }
     __syncthreads();
     return tn;
@@ -101,6 +137,87 @@ __global__ void __launch_bounds__(256) mxfp4_matvec_kernel(const uint8_t* __rest
             if (lane == 0 && t < tn) store_out(y, y_dtype, (t0 + t) * N + n, s + b);
         }
     }
+}
+
+// MXFP4 on 16-byte-aligned blocks: each wave owns MR rows and issues every block and scale
+// load of them (GH 16-byte groups per lane and row, G <= 64 GH) before the first is used, so
+// a lane has MR * GH loads in flight rather than one; the activations are staged meanwhile.
+// Same arithmetic as mxfp4_matvec_kernel (per group: the fp4 dot in fp32, times the scale).
+template <int GH, int MR, int TCH>
+__global__ void __launch_bounds__(256) mxfp4_mv_kernel(const uint8_t* __restrict__ blocks,
+                                                       const uint8_t* __restrict__ scales,
+                                                       const void* __restrict__ bias, int bias_dtype,
+                                                       const void* __restrict__ x, int x_dtype, int64_t T,
+                                                       void* __restrict__ y, int y_dtype, int64_t N, int64_t K) {
+    extern __shared__ float xs[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t G = K / 32;
+    const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * MR;
+    uint4 q[MR][GH];
+    uint32_t sc[MR][GH];
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            const int64_t g = lane + 64 * h, c = (n0 + r) * G + g;
+            const bool ok = g < G && n0 + r < N;
+            q[r][h] = ok ? reinterpret_cast<const uint4*>(blocks)[c] : make_uint4(0u, 0u, 0u, 0u);
+            sc[r][h] = ok ? scales[c] : 127u;
+        }
+    const int64_t t0 = (int64_t)blockIdx.y * TCH;
+    const int tn = stage_x<TCH>(xs, x, x_dtype, t0, T, K);
+    float acc[MR][TCH];
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) acc[r][t] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        const int64_t g = lane + 64 * h;
+        if (g >= G) break;
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const uint32_t qq[4] = {q[r][h].x, q[r][h].y, q[r][h].z, q[r][h].w};
+            const float s = e8m0_to_f32(sc[r][h]);
+#pragma unroll
+            for (int t = 0; t < TCH; ++t) acc[r][t] += mx16_dot(qq, xs + t * K + 32 * g) * s;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        const int64_t n = n0 + r;
+        const float b = bias && n < N ? load_act(bias, bias_dtype, n) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TCH; ++t) {
+            const float s = wave_sum(acc[r][t]);
+            if (lane == 0 && t < tn && n < N) store_out(y, y_dtype, (t0 + t) * N + n, s + b);
+        }
+    }
+}
+
+template <int GH, int MR>
+hipError_t launch_mv(const uint8_t* bl, const uint8_t* sc, const void* bias, int bias_dtype, const void* x,
+                     int x_dtype, int64_t T, void* y, int y_dtype, int64_t N, int64_t K, int tch, hipStream_t st) {
+    const dim3 block(256), grid((unsigned)((N + 4 * MR - 1) / (4 * MR)), (unsigned)((T + tch - 1) / tch));
+    const size_t lds = (size_t)tch * K * sizeof(float);
+    switch (tch) {
+        case 4: hipLaunchKernelGGL((mxfp4_mv_kernel<GH, MR, 4>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+        case 2: hipLaunchKernelGGL((mxfp4_mv_kernel<GH, MR, 2>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+        default: hipLaunchKernelGGL((mxfp4_mv_kernel<GH, MR, 1>), grid, block, lds, st, bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K); break;
+    }
+    return hipGetLastError();
+}
+
+// Groups per lane GH = ceil(G / 64) (K <= 16384: G <= 512), rows per wave MR so that a lane
+// holds 8 groups (4 rows at most).
+hipError_t launch_mx_aligned(const uint8_t* bl, const uint8_t* sc, const void* bias, int bias_dtype, const void* x,
+                             int x_dtype, int64_t T, void* y, int y_dtype, int64_t N, int64_t K, int tch,
+                             hipStream_t st) {
+    const int64_t G = K / 32;
+    if (G <= 64) return launch_mv<1, 4>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
+    if (G <= 128) return launch_mv<2, 4>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
+    if (G <= 256) return launch_mv<4, 2>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
+    return launch_mv<8, 1>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
 }
 
 template <int TYPE, int A>
@@ -217,7 +334,7 @@ extern "C" int tsa_mxfp4_matvec(const void* blocks, const void* scales, const vo
     const int tch = pick_tch(T, K);
     hipStream_t st = as_stream(stream);
     hipError_t e = (reinterpret_cast<uintptr_t>(blocks) & 15) == 0
-                       ? launch_mx<16>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st)
+                       ? launch_mx_aligned(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st)
                        : launch_mx<1>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);
     TSA_HIP_CHECK(e);
     return TSA_OK;
