@@ -284,8 +284,8 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     // blocks go out, so the raw blocks fly for D - 1 pieces. A tile or area is rewritten one
     // piece after it was last read, with the barrier of the piece between. Every load here
     // is an inline-assembly copy (the compiler counts none of them), so the waits are
-    // explicit: at the top of piece pc everything but the last raw copies issued (those of
-    // piece pc + D - 2, RWA or RWB instructions for this wave) must have landed.
+    // explicit: at the top of piece pc everything must have landed but, with three areas,
+    // the raw copies of piece pc + 1 (the newest: RWA or RWB instructions of this wave).
     issue_x(0);
     gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
     if (D == 3 && P > 1) gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 1, K, raw + RAW, wave, lane);
