@@ -657,7 +657,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": {1: "gguf q8_0 weights, fp32 activations (int8 hi/lo terms per 32 values), int32 dots, fp32 accumulate",
                   2: "gguf q4_k/q6_k weights, bf16 activations, fp32 accumulate",
-                  3: "mxfp4 weights (e2m1 x e8m0), bf16 activations, fp32 accumulate",
+                  3: "mxfp4 weights (e2m1 x e8m0) x bf16 activations carried as two fp8 e4m3 terms per value "
+                     "with a per-32-value e8m0 block scale (exact for values within 2^9 of their block's maximum) "
+                     "on the scaled fp8 x fp4 MFMA, fp32 accumulate; h rounded to bf16 between the launches",
                   4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate",
                   7: "mxfp4 weights (e2m1 x e8m0), bf16 activations and bias, fp32 accumulate"}[args.workload],
         "data": f"synthetic: seeded native-format weights, {n_layers} resident layers (or copies) rotated per step",

@@ -52,20 +52,8 @@ def bf16_dev(bits: np.ndarray, device: str = "cuda") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).copy()).view(torch.bfloat16).to(device)
 
 
-def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
-    """OCP fp8 e4m3 (bias 7, no infinities, 0x7F / 0xFF NaN) -> float32, exact."""
-    c = np.asarray(codes, dtype=np.int64)
-    sign = np.where(c & 0x80, -1.0, 1.0)
-    e, m = (c >> 3) & 15, c & 7
-    v = sign * np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10))
-    v[(c & 0x7F) == 0x7F] = np.nan
-    return v.astype(np.float32)
-
-
-def tiled_h(ws: torch.Tensor, pairs: int, inter: int, swiglu_limit: float = 7.0) -> np.ndarray:
-    """The intermediate h [pairs, inter] the tiled decode wrote at the start of its workspace:
-    per pair two e4m3 terms (hi then lo) of inter values, scaled by 2^(7 - e) with
-    (limit + 1) * limit < 2^e."""
-    raw = ws[: pairs * 2 * inter].cpu().numpy().view(np.uint8).reshape(pairs, 2, inter)
-    e = int(np.frexp(np.float32((swiglu_limit + 1.0) * swiglu_limit))[1])
-    return (e4m3_to_f32(raw[:, 0]) + e4m3_to_f32(raw[:, 1])) * np.float32(2.0 ** (e - 7))
+def tiled_h(ws: torch.Tensor, pairs: int, inter: int) -> np.ndarray:
+    """The intermediate h [pairs, inter] (bf16) the tiled decode wrote at the start of its
+    workspace, as float32."""
+    raw = ws[: pairs * 2 * inter].cpu().numpy().view(np.uint16).reshape(pairs, inter)
+    return (raw.astype(np.uint32) << 16).view(np.float32)

@@ -190,3 +190,74 @@ def test_tiled_rejects_non_bf16_activations():
     w = torch.ones((1, 1), device="cuda")
     with pytest.raises(RuntimeError, match="bf16 activations"):
         ops.moe_decode(L, pool, s, w, x)
+
+
+@pytest.mark.parametrize("H,I,E,k,T", [(2880, 2880, 8, 4, 1), (512, 1024, 6, 3, 3)])
+def test_tiled_decode_small_h(H, I, E, k, T):
+    """Experts with e8m0 block scales 2^-14 .. 2^-10 and no biases: |gate_up| ~ 0.04, so
+    |h| ~ 0.01 - 0.05 and y carries h's precision alone. Output and h against the oracle."""
+    rng = np.random.default_rng(H + I + T)
+    lay = synth.mxfp4_tiled_layout(H, I, bias=False)
+    experts = [synth.make_mxfp4_expert(rng, H, I, bias=False, scale_lo=113, scale_hi=117) for _ in range(E)]
+    pool = torch.from_numpy(np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in experts])).cuda()
+    L = mxfp4_expert_layout(lay, tiled=True)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    ws = ops.moe_decode_workspace(L, T, k, "cuda")
+    y, gidx, gw = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                        torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k, workspace=ws,
+                                        return_routing=True)
+    torch.cuda.synchronize()
+    idx, w = oex.route_topk_then_softmax(logits, k)
+    assert np.array_equal(gidx.cpu().numpy(), idx)
+    xf = synth.bf16_to_f32(x_bits)
+    h = tiled_h(ws, T * k, I).reshape(T, k, I)
+    h_rms = []
+    for t in range(T):
+        for j in range(k):
+            wgu, _ = oex.mxfp4_expert_weights(experts[idx[t, j]])
+            h_ref = oex.gptoss_swiglu(xf[t : t + 1] @ wgu.T).reshape(-1)
+            h_rms.append(float(np.sqrt(np.mean(h_ref.astype(np.float64) ** 2))))
+            assert_close_bf16(h[t, j], h_ref, f"h[{t},{j}]")
+    assert 0.003 < np.median(h_rms) < 0.06, f"h rms {h_rms} outside the small-h regime the test is for"
+    assert_close_bf16(y, _ref(experts, xf, idx, w), "small-h decode")
+
+
+@pytest.mark.parametrize("routed", [True, False])
+def test_tiled_decode_outlier_channel(routed):
+    """x with one channel 1000x the others (a different channel per token): each 32-value
+    block of x has its own scale, so the other channels keep their bf16 precision."""
+    H, I, E, k, T = 2880, 2880, 6, 4, 2
+    rng = np.random.default_rng(77)
+    lay = synth.mxfp4_tiled_layout(H, I)
+    experts = [synth.make_mxfp4_expert(rng, H, I) for _ in range(E)]
+    pool = torch.from_numpy(np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in experts])).cuda()
+    L = mxfp4_expert_layout(lay, tiled=True)
+    x = rng.normal(size=(T, H)).astype(np.float32) * np.float32(0.01)
+    x[0, 17] = 10.0
+    x[1, 2000] = -10.0
+    u = x.view(np.uint32).astype(np.uint64)  # to bf16, round to nearest even
+    x_bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    idx, w = oex.route_topk_then_softmax(logits, k)
+    xf = synth.bf16_to_f32(x_bits)
+    ref = _ref(experts, xf, idx, w)
+    if routed:
+        y = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                  torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k)
+    else:
+        y = ops.moe_decode(L, pool, torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
+                           bf16_dev(x_bits))
+    torch.cuda.synchronize()
+    assert_close_bf16(y, ref, "outlier channel")
+    # the contribution of the small channels alone (outliers removed) must be carried too
+    xs = xf.copy()
+    xs[0, 17] = 0.0
+    xs[1, 2000] = 0.0
+    wl = [oex.mxfp4_expert_weights(e) for e in experts]
+    for t in range(T):
+        for j in range(k):
+            wgu, _ = wl[idx[t, j]]
+            full = xf[t] @ wgu.T
+            small = xs[t] @ wgu.T
+            assert np.abs(small).max() > 0.02 * np.abs(full).max(), "the small channels must matter"

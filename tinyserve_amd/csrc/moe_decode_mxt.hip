@@ -10,21 +10,23 @@
 // as the lane's B scale: the block scales are applied by the matrix core. The A operand
 // carries the activation vector v (x for gate_up, h for down) as two fp8 e4m3 terms in
 // rows 0 and 1 (rows 2..15 zero), so D[r][i] accumulates sum_k W[i][k] term_r(k) over the
-// pieces and lane i adds rows 0 and 1 at the end. The two terms are v*s = hi + lo with
-// hi = e4m3(v*s) and lo = e4m3(v*s - hi): for a bf16 v the pair is exact (hi keeps 4
-// significant bits, lo the remaining 4) unless v is more than 2^10 below the scaled
-// maximum, so the products are those of the reference's bf16 arithmetic. The scale s is a
-// power of two: per token for x (from max |x|), fixed for h (|h| <= (limit + 1) * limit
-// after the clamped SwiGLU).
+// pieces and lane i adds rows 0 and 1 at the end. Every 32-value block b of v has its own
+// power-of-two scale s_b = 2^(7 - e_b), e_b the exponent of the block's largest |v|, and the
+// terms are v s_b = hi + lo with hi = e4m3(v s_b) and lo = e4m3(v s_b - hi); the A scale of
+// block b is 1 / s_b (e8m0), so the matrix core undoes the scaling. For a bf16 v the pair is
+// exact (hi keeps 4 significant bits, lo the remaining 4) unless v is more than 2^9 below
+// its block's maximum, so the products are those of the reference's bf16 arithmetic whatever
+// the magnitude of v and however it varies across blocks.
 //
-// Launch 1 (gate_up): workgroup (kb, pair) multiplies 64 gate_up rows of the pair's expert
+// Launch 1 (gate_up): workgroup (kb, pair) multiplies 32 gate_up rows of the pair's expert
 //   (one 16-row tile per wave) by x of the pair's token; bias, clamped SwiGLU, h rounded to
-//   bf16 (the reference runs its experts in bf16) and written to the workspace as its two
-//   fp8 terms. A routed launch selects the experts in every workgroup (one wave, from the
-//   token's logits); the first workgroup of each token also writes the selection.
+//   bf16 (the reference runs its experts in bf16) and written to the workspace. A routed
+//   launch selects the experts in every workgroup (one wave, from the token's logits); the
+//   first workgroup of each token also writes the selection.
 // Launch 2 (down): workgroup (token, 16 output rows): wave j multiplies expert j's 16-row
-//   down tile by h(token, j); the waves' weighted rows are summed in a fixed order in LDS
-//   (one writer per output, deterministic).
+//   down tile by h(token, j), which it turns into block-scaled terms while its tile streams
+//   in; the waves' weighted rows are summed in a fixed order in LDS (one writer per output,
+//   deterministic).
 // No workgroup waits for another: stream order between the launches is the only
 // synchronisation, so the grid needs no co-residency and the workspace carries no state
 // from one call to the next.
@@ -44,7 +46,9 @@ namespace {
 constexpr int MAXT = FUSED_MAXT;
 constexpr int MAXK = FUSED_MAXK;
 constexpr int WAVES = 4;
-constexpr int MISC_LDS = 1024;  // slot/weight tables, per-wave maxima and rows
+constexpr int MISC_LDS = 1024;  // down launch: weighted rows [WAVES][16] floats, then the waves' A-scale tables
+constexpr int VCH = 3072 / 8 / 64;  // 8-value chunks per lane when a wave holds a whole vector (length <= 3072)
+constexpr int ASC_BYTES = 16 * VCH;  // A-scale table of one vector: one e8m0 byte per 32-value block (<= 96 blocks)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
@@ -64,9 +68,8 @@ struct MxtParams {
     const uint16_t* x;  // bf16 [T, H]
     void* y;
     int y_dtype;
-    uint8_t* h;  // [T k][2][I] fp8 terms of h * h_scale (hi, then lo)
+    uint16_t* h;  // [T k][I] bf16
     int64_t gu_tile, gu_stile, dn_tile, dn_stile;  // bytes per 16-row tile: blocks, scale words
-    float h_scale, h_inv;
 };
 
 // A wave's 16-row tile: MM pieces of 1 KB and the scale words (byte m%4 of word m/4) as
@@ -130,20 +133,22 @@ __device__ __forceinline__ float bias_word_value(uint32_t w, int dtype, int64_t 
     return dtype == TSA_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
 }
 
-// One scaled MFMA: D = A * B (+ C) with A's blocks at scale 1 and B's block scales taken
-// per lane: lane 16q + i supplies the e8m0 scale of column i, K block q, as byte OPB of sb.
-template <int OPB>
-__device__ __forceinline__ v4f mfma_fp8_fp4(const v8i& A, const v8i& B, const v4f& C, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, C, 0, 4, 0, 0x7F7F7F7F, OPB, sb);
+// One scaled MFMA: D = A * B (+ C) with both operands' block scales taken per lane: lane
+// 16q + r supplies the e8m0 scale of A row r, K block q, as byte OP of sa, and lane 16q + i
+// that of B column i, K block q, as byte OP of sb.
+template <int OP>
+__device__ __forceinline__ v4f mfma_fp8_fp4(const v8i& A, const v8i& B, const v4f& C, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, C, 0, 4, OP, sa, OP, sb);
 }
 
-// sum over the tile's K of W[i][k] * (term_0(k) + term_1(k)) in lane i < 16, W the wave's
-// 16-row tile and term_r the fp8 terms of a vector in LDS. Piece m is one
-// v_mfma_scale_f32_16x16x128_f8f6f4 (fp8 e4m3 A, cbsz 0; fp4 e2m1 B, blgp 4): A row r is
-// term r over the piece's 128 K (rows 2..15 zero), B is the piece as loaded, and the block
-// scales are applied by the instruction: lane 16q + i holds the scale word of (row i, blocks
-// 4m' + q), so byte m % 4 of its word m / 4 is exactly its B scale for piece m. The MFMA
-// accumulates across pieces. src: the lane's A-operand source (a_source). The A operands
+// sum over the tile's K of W[i][k] v(k) in lane i < 16, W the wave's 16-row tile and v a
+// vector held in LDS as two fp8 terms per value with per-block scales (chunk_terms). Piece m
+// is one v_mfma_scale_f32_16x16x128_f8f6f4 (fp8 e4m3 A, cbsz 0; fp4 e2m1 B, blgp 4): A row r
+// is term r over the piece's 128 K (rows 2..15 zero), B is the piece as loaded, and the block
+// scales of both operands are applied by the instruction: lane 16q + i holds the scale word
+// of (row i, blocks 4m' + q), so byte m % 4 of its word m / 4 is exactly its B scale for
+// piece m, and byte m % 4 of asc[m / 4] (a_scales) is the A scale of block q of piece m. The
+// MFMA accumulates across pieces. src: the lane's A-operand source (a_source). The A operands
 // of the next two pieces are read ahead of each MFMA (sched barriers keep them there: left
 // alone the scheduler moves the reads next to their use and the MFMAs wait for LDS, and
 // the reads are volatile so that no earlier pass hoists them all to the top).
@@ -155,7 +160,7 @@ __device__ __forceinline__ u32x4 lds16(const uint8_t* p) {
     return *(lds_u32x4*)(p);
 }
 template <int MM>
-__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src) {
+__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src, const uint32_t (&asc)[Tile<MM>::MS]) {
     constexpr int PD = 2;
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     u32x4 lo[PD + 1], hi[PD + 1];
@@ -171,11 +176,12 @@ __device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src
                        (int)hi[b][0], (int)hi[b][1], (int)hi[b][2], (int)hi[b][3]};
         const v8i B = {(int)tl.q[m][0], (int)tl.q[m][1], (int)tl.q[m][2], (int)tl.q[m][3], 0, 0, 0, 0};
         const int sb = m / 4 < tl.w ? (int)tl.sc[m / 4] : 0x7F7F7F7F;  // past the row end: any finite scale
+        const int sa = (int)asc[m / 4];
         switch (m & 3) {
-            case 0: acc = mfma_fp8_fp4<0>(A, B, acc, sb); break;
-            case 1: acc = mfma_fp8_fp4<1>(A, B, acc, sb); break;
-            case 2: acc = mfma_fp8_fp4<2>(A, B, acc, sb); break;
-            default: acc = mfma_fp8_fp4<3>(A, B, acc, sb); break;
+            case 0: acc = mfma_fp8_fp4<0>(A, B, acc, sa, sb); break;
+            case 1: acc = mfma_fp8_fp4<1>(A, B, acc, sa, sb); break;
+            case 2: acc = mfma_fp8_fp4<2>(A, B, acc, sa, sb); break;
+            default: acc = mfma_fp8_fp4<3>(A, B, acc, sa, sb); break;
         }
         asm volatile("" : "+v"(acc));  // piece m's MFMA stays ahead of the next reads
         if (m + PD + 1 < MM) {
@@ -196,14 +202,6 @@ __device__ __forceinline__ const uint8_t* a_source(const uint8_t* terms, const u
     return row < 2 ? terms + row * kp + 16 * kq : zero;
 }
 
-// 16 bytes per lane from buffer offset voff straight into LDS at lds + 16 lane (one 1 KB
-// wave transfer). Issued from inline assembly: the compiler does not count these loads, so
-// the caller waits for them with its own s_waitcnt before reading the LDS area.
-__device__ __forceinline__ void lds_dma16(const __amdgpu_buffer_rsrc_t& r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(lds)
-                 : "memory", "m0");
-}
-
 // Two e4m3 terms of v * s: hi = RNE(v s), lo = RNE(v s - hi) (OCP e4m3; |v s| < 448).
 __device__ __forceinline__ void fp8_terms(float v0, float v1, uint32_t& hi2, uint32_t& lo2) {
     const int h = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
@@ -212,24 +210,63 @@ __device__ __forceinline__ void fp8_terms(float v0, float v1, uint32_t& hi2, uin
     lo2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false) & 0xFFFFu;
 }
 
+// A vector's A-scale table: one e8m0 byte per 32-value block b, at byte 4 (4 (b / 16) + b % 4)
+// + (b % 16) / 4, so that dword 4g + q holds in byte j the scale of block 16g + 4j + q, which
+// is block q of piece 4g + j: lane 16q + r reads dword 4g + q for pieces 4g .. 4g + 3.
+// All lanes read a word (rows 2..15 of A are zero; every table byte is a finite scale).
+template <int MS>
+__device__ __forceinline__ void a_scales(const uint8_t* table, int lane, uint32_t (&asc)[MS]) {
+    typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+#pragma unroll
+    for (int g = 0; g < MS; ++g) asc[g] = *(lds_u32*)(table + 4 * (4 * g + (lane >> 4)));
+}
+
+// Block-scaled fp8 terms of chunk set i of a bf16 vector: lane l holds chunk c = l + 64 i (8
+// values, zero past the vector's end), so a lane quad holds one 32-value block, block
+// 16 i + l / 4. The quad's largest magnitude has exponent e (clamped to [-120, 127]; 0 for
+// an all-zero block); the lane writes its values' terms v 2^(7 - e) (largest in [128, 256))
+// at terms + 8c (hi) and terms + kp + 8c (lo) if 8c < kp, and the quad's first lane writes
+// the block's A scale 2^(e - 7) (e8m0 byte 120 + e) into the table. Every lane of the wave
+// must be active (the quad maximum is taken by DPP).
+__device__ __forceinline__ void chunk_terms(const u32x4& v, int i, int lane, uint8_t* terms, int kp, uint8_t* table) {
+    us2 mb = us2{0, 0};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) mb = __builtin_elementwise_max(mb, __builtin_bit_cast(us2, v[d] & 0x7FFF7FFFu));
+    // for non-negative bf16 the integer order of the bits is the order of the values
+    int m = mb[0] > mb[1] ? mb[0] : mb[1];
+    m = max(m, __builtin_amdgcn_mov_dpp(m, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    m = max(m, __builtin_amdgcn_mov_dpp(m, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    const int e = m ? min(max((m >> 7) - 127, -120), 127) : 0;
+    const float s = __uint_as_float((uint32_t)(134 - e) << 23);  // 2^(7 - e)
+    const int c = lane + 64 * i;
+    if (8 * c < kp) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            fp8_terms(bf16_bits_to_f32(v[d] & 0xFFFFu) * s, bf16_bits_to_f32(v[d] >> 16) * s, hw[d], lw[d]);
+        *reinterpret_cast<uint2*>(terms + 8 * c) = uint2{hw[0] | (hw[1] << 16), hw[2] | (hw[3] << 16)};
+        *reinterpret_cast<uint2*>(terms + kp + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
+    }
+    if ((lane & 3) == 0) table[4 * (4 * i + ((lane >> 2) & 3)) + (lane >> 4)] = (uint8_t)(120 + e);
+}
+
 // Zero bytes [from, to) of an LDS area (16-byte multiples), spread over nthr threads.
 __device__ __forceinline__ void lds_zero(uint8_t* a, int from, int to, int me, int nthr) {
     for (int o = from + 16 * me; o < to; o += 16 * nthr) *reinterpret_cast<u32x4*>(a + o) = u32x4{0u, 0u, 0u, 0u};
 }
 
-constexpr int GU_WAVES = 2;        // waves per gate_up workgroup (one 16-row tile each)
-constexpr int XCH = 3072 / 8 / 64;  // x chunks (8 values) per lane when a wave loads all of x (H <= 3072)
+constexpr int GU_WAVES = 2;  // waves per gate_up workgroup (one 16-row tile each)
 
-// ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h terms to the workspace.
+// ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h (bf16) to the workspace.
 // Workgroup b: pair b % (T k), 32-row block b / (T k) (pair-major, so neighbouring
 // workgroups stream different experts). Two waves per workgroup: for GPT-OSS-20B shapes the
 // 720 workgroups spread over the 256 CUs more evenly than 360 four-wave ones would, which
 // shortens the weight stream (measured 6.2 against 6.8 us for the stream alone).
 //
 // Each wave selects the token's experts itself and issues its tile's loads as soon as it
-// knows the slot. Each wave also loads all of x (so its max needs no exchange); in the
-// shadow of the tile loads the two waves convert one half of x each into the shared terms
-// and meet at the workgroup's only barrier before the dot.
+// knows the slot. Each wave also loads all of x; in the shadow of the tile loads the two
+// waves convert alternate 512-value chunk sets of x into the shared block-scaled terms and
+// meet at the workgroup's only barrier before the dot.
 template <int MM>
 __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -239,15 +276,16 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int pairs = p.T * k;
     const int kb = (int)blockIdx.x / pairs, pr = (int)blockIdx.x % pairs, t = pr / k, jj = pr % k;
-    uint8_t* vec = smem;  // x terms [2][KP], then a zero area [KP]
+    uint8_t* vec = smem;  // x terms [2][KP], a zero area [KP], then x's A-scale table
     uint8_t* zero = vec + 2 * KP;
+    uint8_t* table = zero + KP;
     const bool routed = p.logits != nullptr;
 
     // ---- loads, all issued before any is used: x of token t, then the routing inputs
-    u32x4 xr[XCH];
+    u32x4 xr[VCH];
     const uint16_t* xt = p.x + (int64_t)t * H;
 #pragma unroll
-    for (int i = 0; i < XCH; ++i) {
+    for (int i = 0; i < VCH; ++i) {
         const int c = lane + 64 * i;
         xr[i] = c < H / 8 ? *reinterpret_cast<const u32x4*>(xt + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
@@ -311,59 +349,26 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
                   base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
     if (publisher) publish();  // while the tile streams in
 
-    // ---- x terms: scale 2^(7 - e), e = exponent of max |x| (scaled maximum in [128, 256)).
-    // The max over magnitude bits: for non-negative floats the integer order is the float
-    // order (v_pk_max_u16, two values per instruction).
-    us2 mb = us2{0, 0};
+    // ---- x as block-scaled terms (chunk sets i = wave, wave + 2, ...; past H they are zero)
 #pragma unroll
-    for (int i = 0; i < XCH; ++i)
-#pragma unroll
-        for (int d = 0; d < 4; ++d) mb = __builtin_elementwise_max(mb, __builtin_bit_cast(us2, xr[i][d] & 0x7FFF7FFFu));
-    const float mx = wave_max_u(bf16_bits_to_f32(mb[0] > mb[1] ? mb[0] : mb[1]));
-    int e = (int)((__float_as_uint(mx) >> 23) & 255u) - 127;
-    e = mx > 0.0f ? min(max(e, -100), 100) : 0;
-    const float sc = __uint_as_float((uint32_t)(127 + 7 - e) << 23);
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-        const int c = lane + 64 * i;
-        if (i % GU_WAVES == wave && c < H / 8) {  // this wave's half
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t h2, l2;
-                fp8_terms(bf16_bits_to_f32(xr[i][d] & 0xFFFFu) * sc, bf16_bits_to_f32(xr[i][d] >> 16) * sc, h2, l2);
-                hw[d] = h2;
-                lw[d] = l2;
-            }
-            *reinterpret_cast<uint2*>(vec + 8 * c) = uint2{hw[0] | (hw[1] << 16), hw[2] | (hw[3] << 16)};
-            *reinterpret_cast<uint2*>(vec + KP + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
-        }
-    }
-    lds_zero(vec, H, KP, tid, 64 * GU_WAVES);
-    lds_zero(vec + KP, H, KP, tid, 64 * GU_WAVES);
+    for (int i = 0; i < VCH; ++i)
+        if (i % GU_WAVES == wave) chunk_terms(xr[i], i, lane, vec, KP, table);
     lds_zero(zero, 0, KP, tid, 64 * GU_WAVES);
     __syncthreads();  // every pair is live or dead for both waves: both get here or neither
 
-    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane));
-    const float x_inv = __uint_as_float((uint32_t)(127 - 7 + e) << 23);
+    uint32_t asc[Tile<MM>::MS];
+    a_scales(table, lane, asc);
+    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane), asc);
     const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
-    const float tot = a * x_inv + bias;  // lanes 0..15: row row0 + lane
-    // rows alternate gate, up: lane 2r holds h[row0 / 2 + r]
+    const float tot = a + bias;  // lanes 0..15: row row0 + lane
+    // rows alternate gate, up: lane 2r holds h[row0 / 2 + r]; lanes 0, 4, 8, 12 store two
+    // values each (their own and lane + 2's, by quad_perm [2,3,2,3])
     const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(tot), 0xB1, 0xF, 0xF, false));
-    const float hv = bf16_bits_to_f32(f32_to_bf16_bits(swiglu_oai(L, tot, up))) * p.h_scale;
-    uint32_t hi, lo;
-    fp8_terms(hv, 0.0f, hi, lo);
-    // lanes 0 and 8 gather four values each and store 4 bytes per term
-    const uint32_t hb = (hi & 255u) | ((lo & 255u) << 8);
-    const uint32_t b1 = (uint32_t)__shfl_down((int)hb, 2), b2 = (uint32_t)__shfl_down((int)hb, 4),
-                   b3 = (uint32_t)__shfl_down((int)hb, 6);
-    if (lane == 0 || lane == 8) {
-        const uint32_t ph = (hb & 255u) | ((b1 & 255u) << 8) | ((b2 & 255u) << 16) | ((b3 & 255u) << 24);
-        const uint32_t pl = (hb >> 8) | ((b1 >> 8) << 8) | ((b2 >> 8) << 16) | ((b3 >> 8) << 24);
-        uint8_t* dst = p.h + (int64_t)pr * 2 * I + row0 / 2 + (lane >> 1);
-        *reinterpret_cast<uint32_t*>(dst) = ph;
-        *reinterpret_cast<uint32_t*>(dst + I) = pl;
-    }
+    const int hb = (int)f32_to_bf16_bits(swiglu_oai(L, tot, up));
+    const int hb2 = __builtin_amdgcn_mov_dpp(hb, 0xEE, 0xF, 0xF, false);
+    if (lane < 16 && (lane & 3) == 0)
+        *reinterpret_cast<uint32_t*>(p.h + (int64_t)pr * I + row0 / 2 + (lane >> 1)) =
+            ((uint32_t)hb & 0xFFFFu) | ((uint32_t)hb2 << 16);
 }
 
 // ---- launch 2: down tiles of every selected expert of one token, weighted sum in a fixed
@@ -371,23 +376,22 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
 template <int MM>
 __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int KP = 128 * MM;                   // padded vector length
-    constexpr int TPB = (KP + 1023) / 1024 * 1024;  // bytes per h term in LDS (whole 1 KB transfers)
+    constexpr int KP = 128 * MM;  // padded vector length
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int RB = H / 16;
     const int t = (int)blockIdx.x / RB;
     const int64_t n0 = (int64_t)((int)blockIdx.x % RB) * 16;
-    float* s_y = reinterpret_cast<float*>(smem);  // [WAVES][16]
-    uint8_t* hs = smem + MISC_LDS + wave * 2 * TPB;  // this wave's h terms
-    uint8_t* zero = smem + MISC_LDS + WAVES * 2 * TPB;
-    const uint32_t hs_lds = (uint32_t)reinterpret_cast<uintptr_t>(hs);
+    float* s_y = reinterpret_cast<float*>(smem);             // [WAVES][16]
+    uint8_t* table = smem + 64 * WAVES + ASC_BYTES * wave;  // this wave's h A-scale table
+    uint8_t* hs = smem + MISC_LDS + wave * 2 * KP;          // this wave's h terms [2][KP]
+    uint8_t* zero = smem + MISC_LDS + WAVES * 2 * KP;
     const bool hbias = L.down_bias_off >= 0;
     const int rounds = (k + WAVES - 1) / WAVES;
 
-    // the first round's selection as scalar loads, ahead of every transfer (inside the loop
-    // they would be vector loads whose wait covers the transfers issued before them)
+    // the first round's selection as scalar loads, ahead of every vector load (inside the loop
+    // they would be vector loads whose wait covers the h loads issued before them)
     const int j0 = wave < k ? wave : k - 1;
     const int64_t slot0 = uniform(p.sel_slot[t * k + j0]);
     const float w0 = __int_as_float(uniform(__float_as_int(p.sel_w[t * k + j0])));
@@ -398,35 +402,33 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     for (int rd = 0; rd < rounds; ++rd) {
         const int j = rd * WAVES + wave;
         if (j >= k) break;
-        // h(t, j) straight into LDS (each term zero-filled to TPB by the buffer bound), then
-        // the bias and the tile: CHUNKS + MM + 1 buffer loads younger than the transfer
+        // h(t, j) in 8-value chunks into registers (bounded to the vector: zero past its end),
+        // then the bias and the tile
         const int64_t slot = rd == 0 ? slot0 : uniform(p.sel_slot[t * k + j]);
         const float w = rd == 0 ? w0 : __int_as_float(uniform(__float_as_int(p.sel_w[t * k + j])));
-        const uint8_t* src = p.h + (int64_t)(t * k + j) * 2 * I;
+        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(p.h + (int64_t)(t * k + j) * I), (short)0, 2 * I, 0x00020000);
+        u32x4 hr[VCH];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const __amdgpu_buffer_rsrc_t rh =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src + r * I), (short)0, I, 0x00020000);
-#pragma unroll
-            for (int i = 0; i < TPB / 1024; ++i)
-                lds_dma16(rh, (uint32_t)(1024 * i + 16 * lane), hs_lds + (uint32_t)(r * TPB + 1024 * i));
-        }
-        if (slot < 0 || slot >= p.n_slots) {  // contributes nothing; the transfer must land before reuse or exit
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            continue;
-        }
+        for (int i = 0; i < VCH; ++i)
+            hr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, 16 * (lane + 64 * i), 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        if (slot < 0 || slot >= p.n_slots) continue;  // contributes nothing
         const uint8_t* base = p.pool + slot * L.slot_bytes;
         Tile<MM> tl;
         const int64_t brow = n0 + (lane & 15);
         const uint32_t bw = bias_word(base + (hbias ? L.down_bias_off : 0), L.bias_dtype, hbias ? (int64_t)H : 0, brow);
         tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
                       base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Tile<MM>::CHUNKS + MM + 1) : "memory");
-        const float a = tile_dot<MM>(tl, a_source(hs, zero, TPB, lane));
-        // used unconditionally (zero without a bias: the load's bound is 0), so the load
-        // stays and the count above holds
-        const float bias = bias_word_value(bw, L.bias_dtype, brow);
-        yv += w * (a * p.h_inv + bias);
+        // h as block-scaled terms while the tile streams in (the h loads are the oldest)
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) chunk_terms(hr[i], i, lane, hs, KP, table);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own terms and table are in LDS
+        uint32_t asc[Tile<MM>::MS];
+        a_scales(table, lane, asc);
+        const float a = tile_dot<MM>(tl, a_source(hs, zero, KP, lane), asc);
+        const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
+        yv += w * (a + bias);
     }
     if (lane < 16) s_y[wave * 16 + lane] = yv;
     __syncthreads();
@@ -464,7 +466,7 @@ int64_t al256(int64_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
-// Workspace bytes of the tiled decode (after the header): h terms, 2 inter bytes per
+// Workspace bytes of the tiled decode (after the header): h in bf16, 2 inter bytes per
 // (token, expert) pair, then the routed selection (int32 slots, float weights).
 int64_t mxt_ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
     return al256(T * k * 2 * L.inter) + 2 * al256(T * k * 4);
@@ -524,22 +526,14 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     p.x = static_cast<const uint16_t*>(x);
     p.y = y;
     p.y_dtype = y_dtype;
-    p.h = h;
+    p.h = reinterpret_cast<uint16_t*>(h);
     p.gu_tile = 8 * L.hidden;
     p.gu_stile = mx_tile_scale_bytes(L.hidden);
     p.dn_tile = 8 * L.inter;
     p.dn_stile = mx_tile_scale_bytes(L.inter);
-    // h terms: |h| <= (limit + 1) * limit after the clamps; scale it into [64, 128) at most
-    const float hmax = (L.swiglu_limit + 1.0f) * L.swiglu_limit;
-    int e = 0;
-    if (hmax > 0.0f && hmax < 1e30f) frexpf(hmax, &e);  // hmax < 2^e
-    e = e < -100 ? -100 : (e > 100 ? 100 : e);
-    p.h_scale = ldexpf(1.0f, 7 - e);
-    p.h_inv = ldexpf(1.0f, e - 7);
 
-    const size_t lds_a = 3 * 128 * (size_t)ma;
-    const size_t tpb = (128 * (size_t)mb + 1023) / 1024 * 1024;
-    const size_t lds_b = MISC_LDS + WAVES * 2 * tpb + 128 * (size_t)mb;
+    const size_t lds_a = 3 * 128 * (size_t)ma + ASC_BYTES;
+    const size_t lds_b = MISC_LDS + (2 * WAVES + 1) * 128 * (size_t)mb;
     void* args[] = {&p};
     TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / (8 * GU_WAVES)))), dim3(64 * GU_WAVES), args,
                                   lds_a, st));
