@@ -567,6 +567,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--decode-form", choices=["one", "two"], default="two",
+                    help="workload 3: the tiled decode in one launch (down waits for gate_up in-kernel) or two")
     ap.add_argument("--checkpoint-order", action="store_true",
                     help="workload 3: keep the experts in the checkpoint order (the slower row-major kernel)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -598,6 +600,7 @@ def main() -> int:
         return run_prefill(args, dev)
     K, W = args.steps, args.warmup
     n_layers = args.layers
+    ops.set_decode_options(0 if args.decode_form == "one" else 1)
     if args.copy_calibration:
         copy_calibration(dev)
     if args.workload in (1, 2):
@@ -672,6 +675,8 @@ def main() -> int:
             "bytes_per_step": nbytes,
             "layers_rotated": n_layers,
             "pool_layout": "mxfp4 16-row mfma tiles" if wl.tiled else "checkpoint order",
+            "decode_form": (args.decode_form + " launch" + ("" if args.decode_form == "one" else "es")) if wl.tiled
+            else None,
             "graph": not args.no_graph,
         },
         "roofline": {

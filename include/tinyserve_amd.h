@@ -147,15 +147,19 @@ int tsa_route_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, i
 int tsa_router_logits(const void* x, int x_dtype, int64_t T, int64_t H, const void* w, int w_dtype,
                       const void* bias, int bias_dtype, int64_t E, void* out, int out_dtype, void* stream);
 
-/* Workspace bytes tsa_moe_decode needs for T tokens with top-k experts. */
+/* Workspace bytes tsa_moe_decode needs for T tokens with top-k experts. The workspace
+ * starts with a 32 KiB sync area, the only part that carries state from one call to the
+ * next (the one-launch MXFP4 decode's call counter and workgroup flags): before the first
+ * call on a workspace every 32-bit word of it must hold one value (zero the workspace, or
+ * fill it with any one byte); the library keeps it consistent after that. */
 int tsa_moe_decode_workspace_size(const tsa_expert_layout* layout, int64_t T, int k, int64_t* bytes);
 
 /* Fused top-k expert FFN over resident packed slots:
  *   y[t] = sum_j weights[t, j] * FFN(pool + slots[t, j] * slot_bytes, x[t]),
  * skipping slots < 0 (they contribute zero). slots [T, k] int32 and weights [T, k] f32
  * stay on the device (no host sync). y is overwritten. The workspace
- * (tsa_moe_decode_workspace_size bytes) needs no initialisation: no kernel keeps state in
- * it from one call to the next. Calls that share a workspace must be ordered (one stream).
+ * (tsa_moe_decode_workspace_size bytes) needs its sync area cleared once before the first
+ * call (see there). Calls that share a workspace must be ordered (one stream).
  * Replaces fast_expert_forward (tinyserve/csrc/expert_loop.cpp:41-123) and the per-expert
  * loops of ExpertPipeline._execute_layer_experts_native / _forward_cache_hits
  * (tinyserve/expert_pipeline.py:241-285,416-496) over GGMLExpertForward
@@ -189,6 +193,21 @@ int tsa_moe_decode_routed_noalloc(const tsa_expert_layout* layout, const void* p
                                   const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype,
                                   int mode, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
                                   int32_t* idx_out, float* w_out, void* stream);
+
+/* Process-wide options of the tiled MXFP4 decode. tiled_form 1 (the default): two launches
+ * ordered by the stream; 0: one launch (top-k <= 4, inter a multiple of 64), whose down
+ * workgroups wait (bounded) for the gate_up workgroups of their token. wait_limit: polls a
+ * one-launch wait makes before it gives up (default 262144, about a quarter second; 0 gives
+ * up at once, for tests of the failure path). A wait that gives up writes NaN for the outputs
+ * of its workgroup and poisons the workspace's sync area: later calls on it write NaN until
+ * it is cleared.
+ * No counterpart in the reference (its decode is one host loop over experts). */
+int tsa_set_decode_options(int tiled_form, uint32_t wait_limit);
+
+/* Whether a decode workspace is poisoned (a one-launch wait gave up): copies its call
+ * counter to the host, synchronising the stream. Clearing the workspace's sync area (see
+ * tsa_moe_decode_workspace_size) heals it. No counterpart in the reference. */
+int tsa_moe_decode_workspace_status(const void* workspace, int64_t workspace_bytes, int* poisoned, void* stream);
 
 /* Expert-major grouping of the (token, j) assignments idx [T, k] (int32 expert ids in
  * [0, E), ids < 0 ignored): counts [E], offsets [E+1] (exclusive scan), perm [T*k]

@@ -52,8 +52,32 @@ def bf16_dev(bits: np.ndarray, device: str = "cuda") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).copy()).view(torch.bfloat16).to(device)
 
 
-def tiled_h(ws: torch.Tensor, pairs: int, inter: int) -> np.ndarray:
-    """The intermediate h [pairs, inter] (bf16) the tiled decode wrote at the start of its
-    workspace, as float32."""
-    raw = ws[: pairs * 2 * inter].cpu().numpy().view(np.uint16).reshape(pairs, inter)
-    return (raw.astype(np.uint32) << 16).view(np.float32)
+DECODE_SYNC_BYTES = 32 << 10  # the decode workspace's leading sync area
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    """OCP fp8 e4m3 (bias 7, no infinities, 0x7F / 0xFF NaN) -> float32, exact."""
+    c = np.asarray(codes, dtype=np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e, m = (c >> 3) & 15, c & 7
+    v = sign * np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10))
+    v[(c & 0x7F) == 0x7F] = np.nan
+    return v.astype(np.float32)
+
+
+def tiled_h(ws: torch.Tensor, pairs: int, inter: int, one_launch: bool = False) -> np.ndarray:
+    """The intermediate h [pairs, inter] the tiled decode wrote to its workspace (right after
+    the sync area), as float32. Two launches: bf16 [pairs][inter]. One launch: per pair the
+    down dot's operands, hi and lo fp8 terms [inter] each and the A-scale table (block b's
+    e8m0 byte at 4 (4 (b / 16) + b % 4) + (b % 16) / 4), padded to 256 bytes."""
+    o = DECODE_SYNC_BYTES
+    if not one_launch:
+        raw = ws[o : o + pairs * 2 * inter].cpu().numpy().view(np.uint16).reshape(pairs, inter)
+        return (raw.astype(np.uint32) << 16).view(np.float32)
+    pb = (2 * inter + 96 + 255) // 256 * 256
+    raw = ws[o : o + pairs * pb].cpu().numpy().view(np.uint8).reshape(pairs, pb)
+    b = np.arange(inter // 32)
+    tb = 4 * (4 * (b // 16) + b % 4) + (b % 16) // 4
+    scale = np.exp2(raw[:, 2 * inter + tb].astype(np.float64) - 127.0)  # [pairs, blocks]
+    v = e4m3_to_f32(raw[:, :inter]).astype(np.float64) + e4m3_to_f32(raw[:, inter : 2 * inter])
+    return (v * np.repeat(scale, 32, axis=1)).astype(np.float32)

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import expert as oex
-from tests.helpers import assert_close_bf16, bf16_dev, to_f32
+from tests.helpers import DECODE_SYNC_BYTES, assert_close_bf16, bf16_dev, to_f32
 from tinyserve_amd import ops, synth
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout
 
@@ -163,7 +163,8 @@ def test_fused_decode_intermediate_and_output(H, E, k, T, routed):
                            bf16_dev(x_bits), workspace=ws)
     torch.cuda.synchronize()
     xf = synth.bf16_to_f32(x_bits)
-    h_gpu = ws[: T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
+    o = DECODE_SYNC_BYTES  # h follows the workspace's sync area
+    h_gpu = ws[o : o + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
     for t in range(T):
         for j in range(k):
             e = experts[idx[t, j]]

@@ -14,6 +14,21 @@ from tinyserve_amd.expert_forward import mxfp4_expert_layout
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture
+def one_launch():
+    ops.set_decode_options(0)
+    yield
+    ops.set_decode_options()
+
+
+@pytest.fixture(params=[0, 1], ids=["one_launch", "two_launches"])
+def form(request):
+    """The tiled decode's form (tsa_set_decode_options), restored to the default after."""
+    ops.set_decode_options(request.param)
+    yield request.param
+    ops.set_decode_options()
+
+
 @pytest.mark.parametrize("N,K", [(16, 32), (64, 256), (5760, 2880), (48, 160), (2880, 2880), (32, 4096)])
 def test_tile_repack_matches_host_packer(N, K):
     rng = np.random.default_rng(N + K)
@@ -43,7 +58,7 @@ def _ref(experts, x, idx, w):
     (256, 128, 6, 2, 1, False), (512, 384, 8, 4, 3, True), (256, 256, 4, 1, 2, False), (1024, 512, 5, 2, 4, True),
     (2048, 2048, 4, 4, 1, True), (512, 1024, 20, 6, 3, False), (256, 128, 8, 3, 7, True), (768, 256, 16, 16, 2, False),
 ])
-def test_tiled_decode_vs_oracle(H, I, E, k, T, routed):
+def test_tiled_decode_vs_oracle(H, I, E, k, T, routed, form):
     """Output and the published bf16 intermediate h (T > 4 runs in chunks of 4 tokens)."""
     rng, L, experts, pool = _setup(H, I, E, seed=H + 3 * I + E + k + T)
     x_bits = synth.bf16_normal(rng, (T, H))
@@ -66,7 +81,7 @@ def test_tiled_decode_vs_oracle(H, I, E, k, T, routed):
     # h of the last launch's tokens (the chunk starting at 4 * floor((T-1)/4))
     t0 = 4 * ((T - 1) // 4)
     tc = T - t0
-    h = tiled_h(ws, tc * k, I).reshape(tc, k, I)
+    h = tiled_h(ws, tc * k, I, one_launch=form == 0 and k <= 4).reshape(tc, k, I)
     for t in range(tc):
         for j in range(k):
             e = experts[idx[t0 + t, j]]
@@ -117,7 +132,7 @@ def test_tiled_pool_from_device_repack():
     assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w), "device-repacked pool")
 
 
-def test_tiled_decode_workload3_full_routed():
+def test_tiled_decode_workload3_full_routed(form):
     """GPT-OSS-20B shapes (hidden = inter = 2880, 32 experts, top-4), routed in the launch."""
     wl = synth.workload(3)
     H, I, E = wl["hidden"], wl["inter"], wl["E"]
@@ -133,7 +148,7 @@ def test_tiled_decode_workload3_full_routed():
 
 
 @pytest.mark.parametrize("T", [1, 3])
-def test_tiled_routed_repeats_and_missing_slots(T):
+def test_tiled_routed_repeats_and_missing_slots(T, form):
     """12 back-to-back launches on one workspace (counters must return to zero), with
     experts 2 and 5 not resident (expert_slot -1 contributes zero)."""
     H, I, E, k = 512, 256, 8, 4
@@ -193,7 +208,7 @@ def test_tiled_rejects_non_bf16_activations():
 
 
 @pytest.mark.parametrize("H,I,E,k,T", [(2880, 2880, 8, 4, 1), (512, 1024, 6, 3, 3)])
-def test_tiled_decode_small_h(H, I, E, k, T):
+def test_tiled_decode_small_h(H, I, E, k, T, form):
     """Experts with e8m0 block scales 2^-14 .. 2^-10 and no biases: |gate_up| ~ 0.04, so
     |h| ~ 0.01 - 0.05 and y carries h's precision alone. Output and h against the oracle."""
     rng = np.random.default_rng(H + I + T)
@@ -211,7 +226,7 @@ def test_tiled_decode_small_h(H, I, E, k, T):
     idx, w = oex.route_topk_then_softmax(logits, k)
     assert np.array_equal(gidx.cpu().numpy(), idx)
     xf = synth.bf16_to_f32(x_bits)
-    h = tiled_h(ws, T * k, I).reshape(T, k, I)
+    h = tiled_h(ws, T * k, I, one_launch=form == 0 and k <= 4).reshape(T, k, I)
     h_rms = []
     for t in range(T):
         for j in range(k):
@@ -224,7 +239,7 @@ def test_tiled_decode_small_h(H, I, E, k, T):
 
 
 @pytest.mark.parametrize("routed", [True, False])
-def test_tiled_decode_outlier_channel(routed):
+def test_tiled_decode_outlier_channel(routed, form):
     """x with one channel 1000x the others (a different channel per token): each 32-value
     block of x has its own scale, so the other channels keep their bf16 precision."""
     H, I, E, k, T = 2880, 2880, 6, 4, 2
@@ -261,3 +276,92 @@ def test_tiled_decode_outlier_channel(routed):
             full = xf[t] @ wgu.T
             small = xs[t] @ wgu.T
             assert np.abs(small).max() > 0.02 * np.abs(full).max(), "the small channels must matter"
+
+
+def test_one_launch_wait_gives_up_then_workspace_heals():
+    """A wait limit of 0 makes every down wave of the one-launch form give up at once (forced
+    from the host; every workgroup still exits): the outputs are NaN and the workspace is
+    poisoned, so later calls write NaN too, until its sync area is cleared."""
+    H, I, E, k = 512, 256, 6, 4
+    rng, L, experts, pool = _setup(H, I, E, seed=91)
+    es = torch.arange(E, dtype=torch.int32, device="cuda")
+    ws = ops.moe_decode_workspace(L, 1, k, "cuda")
+
+    def call():
+        logits = rng.normal(size=(1, E)).astype(np.float32)
+        x_bits = synth.bf16_normal(rng, (1, H))
+        y = ops.moe_decode_routed(L, pool, es, torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k, workspace=ws)
+        idx, w = oex.route_topk_then_softmax(logits, k)
+        return y, _ref(experts, synth.bf16_to_f32(x_bits), idx, w)
+
+    try:
+        ops.set_decode_options(0, 0)
+        y, _ = call()
+        torch.cuda.synchronize()
+        assert torch.isnan(y.float()).all(), "a wait that gave up must leave NaN outputs"
+        assert ops.decode_workspace_poisoned(ws)
+        ops.set_decode_options(0)  # one launch, default wait limit
+        y, _ = call()
+        torch.cuda.synchronize()
+        assert torch.isnan(y.float()).all(), "a poisoned workspace must keep writing NaN"
+        assert ops.decode_workspace_poisoned(ws)
+        ws.zero_()
+        for _ in range(3):
+            y, ref = call()
+            torch.cuda.synchronize()
+            assert_close_bf16(y, ref, "after clearing the sync area")
+        assert not ops.decode_workspace_poisoned(ws)
+    finally:
+        ops.set_decode_options()
+
+
+@pytest.mark.parametrize("routed", [True, False])
+def test_one_launch_graph_replays(routed, one_launch):
+    """One decode call captured in a HIP graph and replayed with new inputs each time (same
+    kernel arguments, so the workspace's call counter alone tells the calls apart); eager
+    calls on the same workspace in between. Every result against the oracle."""
+    H, I, E, k = 512, 512, 8, 4
+    rng, L, experts, pool = _setup(H, I, E, seed=123 + routed)
+    es = torch.arange(E, dtype=torch.int32, device="cuda")
+    ws = ops.moe_decode_workspace(L, 1, k, "cuda")
+    x = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+    logits = torch.empty((1, E), dtype=torch.float32, device="cuda")
+    slots = torch.empty((1, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((1, k), dtype=torch.float32, device="cuda")
+    y = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+
+    def run():
+        if routed:
+            ops.moe_decode_routed(L, pool, es, logits, x, k, workspace=ws, out=y)
+        else:
+            ops.moe_decode(L, pool, slots, wts, x, workspace=ws, out=y)
+
+    def fill():
+        lg = rng.normal(size=(1, E)).astype(np.float32)
+        xb = synth.bf16_normal(rng, (1, H))
+        idx, w = oex.route_topk_then_softmax(lg, k)
+        x.copy_(bf16_dev(xb))
+        logits.copy_(torch.from_numpy(lg))
+        slots.copy_(torch.from_numpy(idx.astype(np.int32)))
+        wts.copy_(torch.from_numpy(w))
+        return _ref(experts, synth.bf16_to_f32(xb), idx, w)
+
+    fill()
+    run()  # warm up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            run()
+    torch.cuda.synchronize()
+    for i in range(6):
+        ref = fill()
+        torch.cuda.synchronize()
+        if i % 3 == 2:
+            run()  # an eager call between replays
+        else:
+            g.replay()
+        torch.cuda.synchronize()
+        assert_close_bf16(y, ref, f"replay {i}")
+    assert not ops.decode_workspace_poisoned(ws)

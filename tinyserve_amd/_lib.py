@@ -82,6 +82,8 @@ SIGNATURES = {
                                      _P, _I64, _P]),
     "tsa_moe_decode_routed_noalloc": (_I32, [_LP, _P, _I64, _P, _I64, _P, _I32, _I32, _I64, _I32, _P, _I32, _P, _I32,
                                              _P, _P, _P]),
+    "tsa_set_decode_options": (_I32, [_I32, ctypes.c_uint32]),
+    "tsa_moe_decode_workspace_status": (_I32, [_P, _I64, ctypes.POINTER(_I32), _P]),
     "tsa_group_by_expert": (_I32, [_P, _I64, _I32, _I64, _P, _P, _P, _P]),
     "tsa_moe_prefill_workspace_size": (_I32, [_LP, _I64, _I32, _I64, ctypes.POINTER(_I64)]),
     "tsa_moe_prefill": (_I32, [_LP, _P, _I64, _P, _I64, _P, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I64, _P]),

@@ -13,6 +13,7 @@
 // (weighted top-k accumulation).
 #include "rowdot.h"
 
+#include <atomic>
 #include <mutex>
 
 namespace tsa {
@@ -214,20 +215,28 @@ int64_t mx_tile_scale_bytes(int64_t K);
 const char* mxt_unsupported(const tsa_expert_layout& L);
 int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
                const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E,
-               int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype, uint8_t* ws,
-               int64_t ws_bytes, hipStream_t st);
+               int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype, uint8_t* sync,
+               uint8_t* ws, int64_t ws_bytes, hipStream_t st);
 
-// Workspace: the intermediate h of every path (float [T, k, I] at most), then int32 slots /
-// ids and float weights [T, k] for routed calls. No kernel keeps state in it between
-// calls, so it needs no initialisation.
+// Workspace: the sync area of the one-launch MXFP4 decode (MXT_SYNC_BYTES), then the
+// intermediate h of every path (float [T, k, I] at most), then int32 slots / ids and float
+// weights [T, k] for routed calls. Only the sync area carries state from one call to the
+// next; it needs one value in every 32-bit word before the first call (zero it).
 static int64_t h_region(const tsa_expert_layout& L, int64_t T, int k) {
     const int64_t v1 = (T * k * L.inter * 4 + 255) / 256 * 256;
     const int64_t fu = mx_fused_ws_bytes(L, T, k), ti = mxt_ws_bytes(L, T, k);
     return v1 > fu ? (v1 > ti ? v1 : ti) : (fu > ti ? fu : ti);
 }
 static int64_t ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
-    return h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
+    return MXT_SYNC_BYTES + h_region(L, T, k) + 3 * ((T * k * 4 + 255) / 256 * 256);
 }
+
+namespace {
+std::atomic<int> g_mxt_form{1};
+std::atomic<uint32_t> g_mxt_wait_limit{1u << 18};
+}  // namespace
+int mxt_form() { return g_mxt_form.load(std::memory_order_relaxed); }
+uint32_t mxt_wait_limit() { return g_mxt_wait_limit.load(std::memory_order_relaxed); }
 
 int validate_layout(const tsa_expert_layout* L) {
     TSA_REQUIRE(L != nullptr, TSA_ERR_INVALID_ARG, "layout is null");
@@ -307,13 +316,13 @@ __global__ void __launch_bounds__(256) tsa_map_slots_kernel(const int32_t* __res
     slots[a] = (e >= 0 && e < E) ? expert_slot[e] : -1;
 }
 
-// Tiled MXFP4 layouts: the MFMA launch pair over chunks of up to 4 tokens (stream-ordered
-// on the shared workspace).
+// Tiled MXFP4 layouts: the MFMA decode over chunks of up to 4 tokens (stream-ordered on
+// the shared workspace).
 static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
                         const float* weights, const void* logits, int logits_dtype, int mode,
                         const int32_t* expert_slot, int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k,
-                        const void* x, int x_dtype, void* y, int y_dtype, uint8_t* ws, int64_t ws_bytes,
-                        hipStream_t st) {
+                        const void* x, int x_dtype, void* y, int y_dtype, uint8_t* sync, uint8_t* ws,
+                        int64_t ws_bytes, hipStream_t st) {
     TSA_REQUIRE(x_dtype == TSA_BF16, TSA_ERR_INVALID_ARG, "tiled MXFP4 experts take bf16 activations (got dtype %d)",
                 x_dtype);
     TSA_REQUIRE(k <= 16, TSA_ERR_SHAPE, "tiled MXFP4 decode supports top-k <= 16 (got %d)", k);
@@ -324,7 +333,7 @@ static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n
         int rc = mxt_decode(L, pl, n_slots, slots ? slots + t0 * k : nullptr, weights ? weights + t0 * k : nullptr, lg,
                             logits_dtype, mode, expert_slot, E, idx_out ? idx_out + t0 * k : nullptr,
                             w_out ? w_out + t0 * k : nullptr, tc, k, static_cast<const uint16_t*>(x) + t0 * H,
-                            static_cast<uint8_t*>(y) + t0 * H * ys, y_dtype, ws, ws_bytes, st);
+                            static_cast<uint8_t*>(y) + t0 * H * ys, y_dtype, sync, ws, ws_bytes, st);
         if (rc) return rc;
     }
     return TSA_OK;
@@ -357,10 +366,12 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
                 (long long)ws_bytes(L, T, k));
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint8_t* sync = static_cast<uint8_t*>(workspace);
+    uint8_t* ws = sync + MXT_SYNC_BYTES;
+    const int64_t wsb = workspace_bytes - MXT_SYNC_BYTES;
     if (L.mx_tiled)
         return tiled_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x,
-                            x_dtype, y, y_dtype, ws, workspace_bytes, st);
+                            x_dtype, y, y_dtype, sync, ws, wsb, st);
     if (T * k > 65535) {  // the other paths launch one grid row per assignment: token chunks
         const int64_t tc = 65535 / k;
         for (int64_t t0 = 0; t0 < T; t0 += tc) {
@@ -374,7 +385,7 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
         return TSA_OK;
     }
     rc = mx_fused_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype,
-                         y, y_dtype, ws, workspace_bytes, st);
+                         y, y_dtype, ws, wsb, st);
     if (rc <= 0) return rc;
     return two_launch_decode(L, pl, n_slots, slots, weights, T, k, x, x_dtype, y, y_dtype, ws, st);
 }
@@ -449,18 +460,35 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
                 (long long)workspace_bytes, (long long)need);
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint8_t* sync = static_cast<uint8_t*>(workspace);
+    uint8_t* ws = sync + MXT_SYNC_BYTES;
+    const int64_t wsb = workspace_bytes - MXT_SYNC_BYTES;
     if (L.mx_tiled && E <= 256)
         return tiled_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
-                            w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+                            w_out, T, k, x, x_dtype, y, y_dtype, sync, ws, wsb, st);
+    if (!L.mx_tiled && T * k > 65535) {  // the row-per-assignment paths: token chunks, routed one by one
+        const int64_t tc = 65535 / k;
+        for (int64_t t0 = 0; t0 < T; t0 += tc) {
+            const int64_t n = T - t0 < tc ? T - t0 : tc;
+            rc = tsa_moe_decode_routed(layout, pool, n_slots, expert_slot, E,
+                                       static_cast<const uint8_t*>(logits) + t0 * E * dtype_size(logits_dtype),
+                                       logits_dtype, mode, n, k,
+                                       static_cast<const uint8_t*>(x) + t0 * L.hidden * dtype_size(x_dtype), x_dtype,
+                                       static_cast<uint8_t*>(y) + t0 * L.hidden * dtype_size(y_dtype), y_dtype,
+                                       idx_out ? idx_out + t0 * k : nullptr, w_out ? w_out + t0 * k : nullptr,
+                                       workspace, workspace_bytes, stream);
+            if (rc) return rc;
+        }
+        return TSA_OK;
+    }
     if (!L.mx_tiled) {
         rc = mx_fused_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
-                             w_out, T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+                             w_out, T, k, x, x_dtype, y, y_dtype, ws, wsb, st);
         if (rc <= 0) return rc;
     }
     if (use_gq(L, pl, T, k) && E <= 256 && T <= 4)
         return gq_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out, w_out,
-                         T, k, x, x_dtype, y, y_dtype, ws, workspace_bytes, st);
+                         T, k, x, x_dtype, y, y_dtype, ws, wsb, st);
     // separate routing, slot mapping and the two-launch decode
     const int64_t tk = (T * k * 4 + 255) / 256 * 256;
     uint8_t* extra = ws + h_region(L, T, k);
@@ -474,14 +502,37 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
     TSA_LAUNCH_CHECK();
     if (L.mx_tiled)
         return tiled_decode(L, pl, n_slots, slots, w, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype, y,
-                            y_dtype, ws, workspace_bytes, st);
+                            y_dtype, sync, ws, wsb, st);
     return two_launch_decode(L, pl, n_slots, slots, w, T, k, x, x_dtype, y, y_dtype, ws, st);
+}
+
+extern "C" int tsa_set_decode_options(int tiled_form, uint32_t wait_limit) {
+    clear_error();
+    TSA_REQUIRE(tiled_form == 0 || tiled_form == 1, TSA_ERR_INVALID_ARG, "tiled_form must be 0 or 1 (got %d)",
+                tiled_form);
+    g_mxt_form.store(tiled_form, std::memory_order_relaxed);
+    g_mxt_wait_limit.store(wait_limit, std::memory_order_relaxed);
+    return TSA_OK;
+}
+
+extern "C" int tsa_moe_decode_workspace_status(const void* workspace, int64_t workspace_bytes, int* poisoned,
+                                               void* stream) {
+    clear_error();
+    TSA_REQUIRE(workspace && poisoned && workspace_bytes >= MXT_SYNC_BYTES, TSA_ERR_INVALID_ARG,
+                "need a decode workspace (at least %lld bytes) and an output", (long long)MXT_SYNC_BYTES);
+    uint32_t gen = 0;
+    hipStream_t st = as_stream(stream);
+    TSA_HIP_CHECK(hipMemcpyAsync(&gen, workspace, 4, hipMemcpyDeviceToHost, st));
+    TSA_HIP_CHECK(hipStreamSynchronize(st));
+    *poisoned = gen == MXT_GEN_POISON;
+    return TSA_OK;
 }
 
 // ---- allocation-free routed decode: the workspace is a file-scope device array, one per
 // GPU (held until the process ends), whose address is looked up once per device with that
 // device current. Calls on one GPU share it, so calls that overlap on one GPU race (order
-// them on one stream); every call fully rewrites what it reads, so nothing needs clearing.
+// them on one stream). Only its sync area carries state between calls; being zero at load,
+// it needs no clearing.
 static constexpr int64_t kNoAllocScratchBytes = 8ll << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 

@@ -70,6 +70,10 @@ struct MxtParams {
     int y_dtype;
     uint16_t* h;  // [T k][I] bf16
     int64_t gu_tile, gu_stile, dn_tile, dn_stile;  // bytes per 16-row tile: blocks, scale words
+    struct MxtSync* sync;  // one-launch form: the workspace's sync area
+    uint8_t* hterm;        // one-launch form: h as the down dot's terms, pair_term_bytes(I) per pair
+    uint32_t wait_limit;   // one-launch form: polls before a wait gives up
+    int n_gu;              // one-launch form: workgroups [0, n_gu) run gate_up
 };
 
 // A wave's 16-row tile: MM pieces of 1 KB and the scale words (byte m%4 of word m/4) as
@@ -117,6 +121,15 @@ __device__ __forceinline__ void tile_load(Tile<MM>& tl, const uint8_t* blocks, i
     }
 }
 
+// The tile's B-scale words moved to LDS (word g of lane l at st + 4 (64 g + l)), freeing their
+// registers for the dot; waits for the scale loads only (the pieces, issued after them, stay
+// in flight).
+template <int MM>
+__device__ __forceinline__ void tile_stash(const Tile<MM>& tl, uint8_t* st, int lane) {
+#pragma unroll
+    for (int g = 0; g < Tile<MM>::MS; ++g) *reinterpret_cast<uint32_t*>(st + 4 * (64 * g + lane)) = tl.sc[g];
+}
+
 // The bias of row r as one dword load bounded to the n-element bias vector (n * element
 // size is a multiple of 4 here; a 2-byte element is the half of its dword that r & 1
 // selects). A zero-size bound (no bias) reads 0. One register, so no reuse of a pending
@@ -147,7 +160,7 @@ __device__ __forceinline__ v4f mfma_fp8_fp4(const v8i& A, const v8i& B, const v4
 // is term r over the piece's 128 K (rows 2..15 zero), B is the piece as loaded, and the block
 // scales of both operands are applied by the instruction: lane 16q + i holds the scale word
 // of (row i, blocks 4m' + q), so byte m % 4 of its word m / 4 is exactly its B scale for
-// piece m, and byte m % 4 of asc[m / 4] (a_scales) is the A scale of block q of piece m. The
+// piece m, and byte m % 4 of the lane's word of the A-scale table is the A scale of block q of piece m. The
 // MFMA accumulates across pieces. src: the lane's A-operand source (a_source). The A operands
 // of the next two pieces are read ahead of each MFMA (sched barriers keep them there: left
 // alone the scheduler moves the reads next to their use and the MFMAs wait for LDS, and
@@ -159,11 +172,18 @@ typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
 __device__ __forceinline__ u32x4 lds16(const uint8_t* p) {
     return *(lds_u32x4*)(p);
 }
-template <int MM>
-__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src, const uint32_t (&asc)[Tile<MM>::MS]) {
-    constexpr int PD = 2;
+typedef __attribute__((address_space(3))) const volatile uint32_t lds_u32;
+template <int MM, int PD = 2>
+__device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src, const uint8_t* table, int lane,
+                                         const uint8_t* bst = nullptr) {
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     u32x4 lo[PD + 1], hi[PD + 1];
+    // the lane's A-scale word of pieces 4g .. 4g + 3 (the table's layout above), read one group
+    // ahead; likewise its B-scale word from the tile's stash (tile_stash) when there is one
+    const uint8_t* aw = table + 4 * (lane >> 4);
+    uint32_t asc_cur = *(lds_u32*)(aw), asc_next = MM > 4 ? *(lds_u32*)(aw + 16) : 0u;
+    const uint8_t* bw = bst + 4 * lane;
+    uint32_t bsc_cur = bst ? *(lds_u32*)(bw) : 0u, bsc_next = bst && MM > 4 ? *(lds_u32*)(bw + 256) : 0u;
 #pragma unroll
     for (int i = 0; i <= PD && i < MM; ++i) {
         lo[i] = lds16(src + 128 * i);
@@ -175,8 +195,17 @@ __device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src
         const v8i A = {(int)lo[b][0], (int)lo[b][1], (int)lo[b][2], (int)lo[b][3],
                        (int)hi[b][0], (int)hi[b][1], (int)hi[b][2], (int)hi[b][3]};
         const v8i B = {(int)tl.q[m][0], (int)tl.q[m][1], (int)tl.q[m][2], (int)tl.q[m][3], 0, 0, 0, 0};
-        const int sb = m / 4 < tl.w ? (int)tl.sc[m / 4] : 0x7F7F7F7F;  // past the row end: any finite scale
-        const int sa = (int)asc[m / 4];
+        if (m % 4 == 0 && m > 0) {
+            asc_cur = asc_next;
+            if (m + 4 < MM) asc_next = *(lds_u32*)(aw + 16 * (m / 4 + 1));
+            if (bst) {
+                bsc_cur = bsc_next;
+                if (m + 4 < MM) bsc_next = *(lds_u32*)(bw + 256 * (m / 4 + 1));
+            }
+        }
+        // past the row end: any finite scale
+        const int sb = m / 4 < tl.w ? (int)(bst ? bsc_cur : tl.sc[m / 4]) : 0x7F7F7F7F;
+        const int sa = (int)asc_cur;
         switch (m & 3) {
             case 0: acc = mfma_fp8_fp4<0>(A, B, acc, sa, sb); break;
             case 1: acc = mfma_fp8_fp4<1>(A, B, acc, sa, sb); break;
@@ -212,14 +241,8 @@ __device__ __forceinline__ void fp8_terms(float v0, float v1, uint32_t& hi2, uin
 
 // A vector's A-scale table: one e8m0 byte per 32-value block b, at byte 4 (4 (b / 16) + b % 4)
 // + (b % 16) / 4, so that dword 4g + q holds in byte j the scale of block 16g + 4j + q, which
-// is block q of piece 4g + j: lane 16q + r reads dword 4g + q for pieces 4g .. 4g + 3.
-// All lanes read a word (rows 2..15 of A are zero; every table byte is a finite scale).
-template <int MS>
-__device__ __forceinline__ void a_scales(const uint8_t* table, int lane, uint32_t (&asc)[MS]) {
-    typedef __attribute__((address_space(3))) const uint32_t lds_u32;
-#pragma unroll
-    for (int g = 0; g < MS; ++g) asc[g] = *(lds_u32*)(table + 4 * (4 * g + (lane >> 4)));
-}
+// is block q of piece 4g + j: lane 16q + r reads dword 4g + q for pieces 4g .. 4g + 3 (all
+// lanes read a word: rows 2..15 of A are zero, and every table byte is a finite scale).
 
 // Block-scaled fp8 terms of chunk set i of a bf16 vector: lane l holds chunk c = l + 64 i (8
 // values, zero past the vector's end), so a lane quad holds one 32-value block, block
@@ -255,27 +278,48 @@ __device__ __forceinline__ void lds_zero(uint8_t* a, int from, int to, int me, i
     for (int o = from + 16 * me; o < to; o += 16 * nthr) *reinterpret_cast<u32x4*>(a + o) = u32x4{0u, 0u, 0u, 0u};
 }
 
-constexpr int GU_WAVES = 2;  // waves per gate_up workgroup (one 16-row tile each)
+constexpr int GU_WAVES = 2;  // waves per workgroup of the gate_up launch (one 16-row tile each)
 
-// ---- launch 1: gate_up tiles of one (token, expert) pair, SwiGLU, h (bf16) to the workspace.
-// Workgroup b: pair b % (T k), 32-row block b / (T k) (pair-major, so neighbouring
-// workgroups stream different experts). Two waves per workgroup: for GPT-OSS-20B shapes the
-// 720 workgroups spread over the 256 CUs more evenly than 360 four-wave ones would, which
-// shortens the weight stream (measured 6.2 against 6.8 us for the stream alone).
+// The token's routing from its logits (all k rounds): lane r < k ends with the r-th selected
+// expert id and slot and its weight (softmax over the k selected logits, or the unnormalised
+// mode's softmax over all E).
+template <class P>
+__device__ float route_weights(const P& p, int lane, const float lg[4], const int es[4], int k, int& mysel,
+                               int& myslot) {
+    uint32_t myk;
+    select_topk(p, lane, lg, es, k, myk, mysel, myslot);
+    const float myval = route_key_value(myk);
+    const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));
+    if (p.route_mode == TSA_ROUTE_SOFTMAX_TOPK) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j < p.E) sum += __expf(lg[j] - top);
+        const float z = wave_sum_u(sum);
+        return lane < k ? __expf(myval - top) / z : 0.0f;
+    }
+    const float ex = lane < k ? __expf(myval - top) : 0.0f;
+    return ex / row16_sum(ex);
+}
+
+// ---- launch 1 of the two-launch form: workgroup b of NW waves multiplies 16 NW gate_up rows
+// of one (token, expert) pair by x of the token; bias, clamped SwiGLU, h rounded to bf16 into
+// the workspace. Pair b % (T k), row block b / (T k) (pair-major, so neighbouring workgroups
+// stream different experts).
 //
 // Each wave selects the token's experts itself and issues its tile's loads as soon as it
-// knows the slot. Each wave also loads all of x; in the shadow of the tile loads the two
-// waves convert alternate 512-value chunk sets of x into the shared block-scaled terms and
-// meet at the workgroup's only barrier before the dot.
-template <int MM>
-__global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
+// knows the slot. Each wave also loads all of x; in the shadow of the tile loads the waves
+// convert interleaved 512-value chunk sets of x into the shared block-scaled terms and meet
+// at the workgroup's barrier before the dot.
+template <int MM, int NW>
+__device__ __forceinline__ void gate_up_body(const MxtParams& p, int b) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = 128 * MM;  // padded vector length
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int pairs = p.T * k;
-    const int kb = (int)blockIdx.x / pairs, pr = (int)blockIdx.x % pairs, t = pr / k, jj = pr % k;
+    const int kb = b / pairs, pr = b % pairs, t = pr / k, jj = pr % k;
     uint8_t* vec = smem;  // x terms [2][KP], a zero area [KP], then x's A-scale table
     uint8_t* zero = vec + 2 * KP;
     uint8_t* table = zero + KP;
@@ -292,9 +336,9 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
     float lg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int es[4] = {0, 0, 0, 0};
     int64_t slot = -1;
-    uint32_t myk = 0u;
     int mysel = -1, myslot = -1;
     if (routed) {
+        uint32_t myk;
 #pragma unroll
         for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
         load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
@@ -304,24 +348,9 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
         slot = uniform(p.sel_slot[pr]);
     }
 
-    // the token's first workgroup publishes the selection (all k rounds): softmax over the k
-    // selected logits, or (unnormalised mode) over all E
+    // the token's first workgroup publishes the selection (all k rounds)
     auto publish = [&]() {
-        select_topk(p, lane, lg, es, k, myk, mysel, myslot);
-        const float myval = route_key_value(myk);
-        const float top = route_key_value((uint32_t)__builtin_amdgcn_readfirstlane((int)myk));
-        float w;
-        if (p.route_mode == TSA_ROUTE_SOFTMAX_TOPK) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (lane + 64 * j < p.E) sum += __expf(lg[j] - top);
-            const float z = wave_sum_u(sum);
-            w = lane < k ? __expf(myval - top) / z : 0.0f;
-        } else {
-            const float ex = lane < k ? __expf(myval - top) : 0.0f;
-            w = ex / row16_sum(ex);
-        }
+        const float w = route_weights(p, lane, lg, es, k, mysel, myslot);
         if (lane < k) {
             p.sel_slot[t * k + lane] = myslot;
             p.sel_w[t * k + lane] = w;
@@ -339,7 +368,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
     }
 
     // ---- the wave's gate_up tile: rows row0 .. row0 + 15 of the pair's expert, after its bias
-    const int64_t row0 = (int64_t)kb * 16 * GU_WAVES + 16 * wave;
+    const int64_t row0 = (int64_t)kb * 16 * NW + 16 * wave;
     const uint8_t* base = p.pool + slot * L.slot_bytes;
     const bool hbias = L.gate_bias_off >= 0;
     const int64_t brow = row0 + (lane & 15);
@@ -349,16 +378,14 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
                   base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
     if (publisher) publish();  // while the tile streams in
 
-    // ---- x as block-scaled terms (chunk sets i = wave, wave + 2, ...; past H they are zero)
+    // ---- x as block-scaled terms (chunk sets i = wave, wave + NW, ...; past H they are zero)
 #pragma unroll
     for (int i = 0; i < VCH; ++i)
-        if (i % GU_WAVES == wave) chunk_terms(xr[i], i, lane, vec, KP, table);
-    lds_zero(zero, 0, KP, tid, 64 * GU_WAVES);
-    __syncthreads();  // every pair is live or dead for both waves: both get here or neither
+        if (i % NW == wave) chunk_terms(xr[i], i, lane, vec, KP, table);
+    lds_zero(zero, 0, KP, tid, 64 * NW);
+    __syncthreads();  // every pair is live or dead for all waves: all get here or none
 
-    uint32_t asc[Tile<MM>::MS];
-    a_scales(table, lane, asc);
-    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane), asc);
+    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane), table, lane);
     const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
     const float tot = a + bias;  // lanes 0..15: row row0 + lane
     // rows alternate gate, up: lane 2r holds h[row0 / 2 + r]; lanes 0, 4, 8, 12 store two
@@ -371,8 +398,16 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
             ((uint32_t)hb & 0xFFFFu) | ((uint32_t)hb2 << 16);
 }
 
-// ---- launch 2: down tiles of every selected expert of one token, weighted sum in a fixed
-// order. Workgroup b: token b / (H / 16), output rows 16 (b % (H / 16)) .. + 15.
+template <int MM>
+__global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
+    gate_up_body<MM, GU_WAVES>(p, (int)blockIdx.x);
+}
+
+// ---- launch 2 of the two-launch form: workgroup d (token d / (H / 16), output rows
+// 16 (d % (H / 16)) .. + 15) runs the down tiles of every selected expert of its token, wave
+// j = expert j (further experts take further rounds), and sums the waves' weighted rows in a
+// fixed order in LDS (one writer per output, deterministic). Each wave turns its pair's h
+// into block-scaled terms while its tile streams in.
 template <int MM>
 __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -381,8 +416,9 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int RB = H / 16;
-    const int t = (int)blockIdx.x / RB;
-    const int64_t n0 = (int64_t)((int)blockIdx.x % RB) * 16;
+    const int d = (int)blockIdx.x;
+    const int t = d / RB;
+    const int64_t n0 = (int64_t)(d % RB) * 16;
     float* s_y = reinterpret_cast<float*>(smem);             // [WAVES][16]
     uint8_t* table = smem + 64 * WAVES + ASC_BYTES * wave;  // this wave's h A-scale table
     uint8_t* hs = smem + MISC_LDS + wave * 2 * KP;          // this wave's h terms [2][KP]
@@ -424,9 +460,7 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
 #pragma unroll
         for (int i = 0; i < VCH; ++i) chunk_terms(hr[i], i, lane, hs, KP, table);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own terms and table are in LDS
-        uint32_t asc[Tile<MM>::MS];
-        a_scales(table, lane, asc);
-        const float a = tile_dot<MM>(tl, a_source(hs, zero, KP, lane), asc);
+        const float a = tile_dot<MM>(tl, a_source(hs, zero, KP, lane), table, lane);
         const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
         yv += w * (a + bias);
     }
@@ -440,11 +474,378 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     }
 }
 
-const void* kernel_for_mm(int MM, bool down) {
-#define TSA_MXT_CASE(M)                                                                  \
-    case M:                                                                              \
-        return down ? reinterpret_cast<const void*>(&mxt_down_kernel<M>)                 \
-                    : reinterpret_cast<const void*>(&mxt_gate_up_kernel<M>);
+// =====================================================================================
+// The one-launch form (k <= 4 experts per token, inter a multiple of 64). Workgroups of 8
+// waves (two per SIMD, so they pack four to a CU): workgroups [0, n_gu) run gate_up (128 rows
+// of one pair, eight 16-row tiles: two 32-value blocks of h), the rest run down (16 output
+// rows of one token: waves 0..3 compute, wave j on expert j; waves 4..7 are helpers, helper
+// 4 + j fetching pair j's h). Down workgroups come after every gate_up workgroup in dispatch
+// order, so a waiting workgroup's producers have all been dispatched: they run whether or not
+// the whole grid is resident.
+//
+// Hand-over. A gate_up workgroup writes its blocks of h as the down dot's operands: the two
+// fp8 terms of each value and the block's A-scale byte (at its place in the down wave's scale
+// table), at agent scope (sc1: coherent across the XCDs' L2 caches). A sync area at the
+// start of the workspace holds a call counter (gen) and one flag per workgroup. One wave of
+// each workgroup reads gen = g when it starts; a gate_up workgroup sets its flag to next(g)
+// once its stores are complete, a down workgroup sets its flag to next(g) as soon as it has
+// read g. Each down helper waits for the flags of its pair and copies the pair's terms into
+// LDS while the compute waves' tiles stream in (a helper has no tile loads in flight, so its
+// polls return at once; a compute wave's poll would wait behind its tile). The last down
+// workgroup first waits for every flag of the call (so every workgroup has read g) and
+// advances gen to next(g): a flag never holds next(g) before the call writes it, provided
+// every word of the area held one value before the first call (zero it, or fill it with any
+// one byte). Waits are bounded: a helper that gives up makes its workgroup write NaN and sets
+// gen to GEN_POISON, after which every call on the workspace writes NaN until the area is
+// cleared again.
+constexpr int F_WAVES = 2 * WAVES;          // eight waves per workgroup
+constexpr int F_MISC = 1024;                // slots, weights, block maxima, status, weighted rows
+constexpr uint32_t GEN_POISON = MXT_GEN_POISON;
+struct MxtSync {
+    uint32_t gen;
+    uint32_t pad[63];
+    uint32_t gflag[MXT_SYNC_GFLAGS];  // gate_up workgroup (pair pr, block pair m): pr * (I / 64) + m
+    uint32_t dflag[MXT_SYNC_DFLAGS];  // down workgroup (token t, row block rb): t * (H / 16) + rb
+    uint32_t relay[MAXT][8][32];      // per token and XCD (one 128-byte line each): its pairs are complete
+};
+static_assert(sizeof(MxtSync) <= MXT_SYNC_BYTES, "sync area");
+
+// The terms of one pair in the workspace: hi [I] bytes, lo [I] bytes, then the A-scale table
+// (ASC_BYTES, in the A-scale table's order), padded to 256 bytes.
+__host__ __device__ __forceinline__ int64_t pair_term_bytes(int64_t I) { return (2 * I + ASC_BYTES + 255) / 256 * 256; }
+
+__device__ __forceinline__ uint32_t next_gen(uint32_t g) { return g + 1 == GEN_POISON ? g + 2 : g + 1; }
+__device__ __forceinline__ uint32_t load_agent(const uint32_t* a) {
+    return __hip_atomic_load(const_cast<uint32_t*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t* a, uint32_t v) {
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void poison(MxtSync* s) {
+    __hip_atomic_exchange(&s->gen, GEN_POISON, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Whole-wave bounded wait until words [0, n) of f all equal v: polls (agent-scope loads) with
+// a short sleep between them, at most `limit` times (0: give up at once). True if they did.
+__device__ bool wait_flags(const uint32_t* f, int n, uint32_t v, uint32_t limit, int lane) {
+    for (uint32_t it = 0; it < limit; ++it) {
+        bool ok = true;
+        for (int i = lane; i < n; i += 64) ok = ok && load_agent(f + i) == v;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
+// The down helper's wait for every pair of token t (all flags equal want, bounded). Each round
+// reads the token's relay word for this XCD at XCD scope (sc0: past the CU's L1, an L2 hit, no
+// memory traffic); one round in four, staggered by workgroup, polls the flags themselves at
+// agent scope and, once they are complete, sets the relay for the other workgroups on the XCD
+// (so a flag line is polled by a quarter of the workgroups at a time, not all of them). The
+// relay only ever says what a poll of the flags saw, so its XCD index need not be exact.
+__device__ bool wait_token(const MxtParams& p, int t, uint32_t want, int lane, int d) {
+    const int n = p.k * (int)(p.L.inter / 64);
+    const uint32_t* f = &p.sync->gflag[t * n];
+    const int xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 7;  // HW_REG_XCC_ID
+    const __amdgpu_buffer_rsrc_t rr =
+        __builtin_amdgcn_make_buffer_rsrc(&p.sync->relay[t][xcc][0], (short)0, 4, 0x00020000);
+    for (uint32_t it = 0; it < p.wait_limit; ++it) {
+        if (__builtin_amdgcn_raw_buffer_load_b32(rr, 0, 0, 1) == want) return true;
+        if (((it + (uint32_t)d) & 3) == 0) {
+            bool ok = true;
+            for (int i = lane; i < n; i += 64) ok = ok && load_agent(f + i) == want;
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+                if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(want, rr, 0, 0, 1);
+                return true;
+            }
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
+// 16 bytes per lane at buffer offset voff, at agent scope (sc1), straight into LDS at
+// lds + 16 lane (one 1 KB wave transfer); 4 bytes per lane (256 B) for the dword form.
+// Issued from inline assembly: the caller waits for them with its own s_waitcnt.
+__device__ __forceinline__ void lds_dma16_agent(const __amdgpu_buffer_rsrc_t& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen sc1 lds" ::"v"(voff), "s"(r), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4_agent(const __amdgpu_buffer_rsrc_t& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen sc1 lds" ::"v"(voff), "s"(r), "s"(lds)
+                 : "memory", "m0");
+}
+
+template <int MM>
+__device__ __forceinline__ void fused_gate_up(const MxtParams& p, int b) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int KP = 128 * MM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
+    const int pairs = p.T * k;
+    const int m = b / pairs, pr = b % pairs, t = pr / k, jj = pr % k;
+    const int kb = 2 * m + (wave >> 2);                    // the wave's block of h
+    const int64_t row0 = (int64_t)m * 128 + 16 * wave;     // the wave's 16 gate_up rows
+    float* s_max = reinterpret_cast<float*>(smem + 128);  // [8]
+    uint8_t* vec = smem + F_MISC;                          // x terms [2][KP], zero [KP], x's table
+    uint8_t* zero = vec + 2 * KP;
+    uint8_t* table = zero + KP;
+    uint8_t* stash = table + 128 + wave * (256 * Tile<MM>::MS);  // the wave's B-scale words
+    uint8_t* terms = p.hterm + pr * pair_term_bytes(I);
+    // gen as a plain load: the previous call's update is visible across kernel boundaries, and
+    // agent-scope loads of one word by every workgroup would queue at its memory channel
+    const uint32_t g = wave == 0 ? p.sync->gen : 0u;
+
+    // ---- loads, all issued before any is used: the wave's chunk set of x, then the routing inputs
+    u32x4 xr = u32x4{0u, 0u, 0u, 0u};
+    const int xc = lane + 64 * wave;
+    if (wave < VCH && xc < H / 8) xr = *reinterpret_cast<const u32x4*>(p.x + (int64_t)t * H + 8 * xc);
+    float lg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int es[4] = {0, 0, 0, 0};
+    int64_t slot = -1;
+    int mysel = -1, myslot = -1;
+    if (p.logits) {
+        uint32_t myk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+        load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
+        select_topk(p, lane, lg, es, jj + 1, myk, mysel, myslot);  // the pair's selection is round jj
+        slot = __builtin_amdgcn_readlane(myslot, jj);
+    } else {
+        slot = uniform(p.sel_slot[pr]);
+    }
+    const bool publisher = p.logits && m == 0 && jj == 0 && wave == 0;
+    if (wave == 0 && g == GEN_POISON) slot = -1;  // a poisoned workspace: no work, no flag
+    // every wave reaches B0 (the poisoned check is wave 0's): the slot as wave 0 sees it
+    int* s_live = reinterpret_cast<int*>(smem);
+    if (tid == 0) *s_live = slot >= 0 && slot < p.n_slots;
+    __syncthreads();  // B0
+    if (!uniform(*s_live)) {  // a dead pair: nothing to compute; the flag says g was read
+        if (wave == 0 && lane == 0 && g != GEN_POISON) store_agent(&p.sync->gflag[pr * (I / 64) + m], next_gen(g));
+        if (publisher) {
+            const float w = route_weights(p, lane, lg, es, k, mysel, myslot);
+            if (lane < k && p.idx_out) {
+                p.idx_out[t * k + lane] = mysel;
+                p.w_out[t * k + lane] = w;
+            }
+        }
+        return;
+    }
+    // x's terms and the publication before the tile loads (x arrived with the routing inputs;
+    // done later they would hold registers across the tile)
+    if (wave < VCH) chunk_terms(xr, wave, lane, vec, KP, table);
+    if (publisher) {
+        const float w = route_weights(p, lane, lg, es, k, mysel, myslot);
+        if (lane < k && p.idx_out) {
+            p.idx_out[t * k + lane] = mysel;
+            p.w_out[t * k + lane] = w;
+        }
+    }
+    const uint8_t* base = p.pool + slot * L.slot_bytes;
+    const bool hbias = L.gate_bias_off >= 0;
+    const int64_t brow = row0 + (lane & 15);
+    const uint32_t bw = bias_word(base + (hbias ? L.gate_bias_off : 0), L.bias_dtype, hbias ? 2 * (int64_t)I : 0, brow);
+    Tile<MM> tl;
+    tile_load<MM>(tl, base + L.gate_off + (row0 / 16) * p.gu_tile, p.gu_tile,
+                  base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
+    tile_stash(tl, stash, lane);
+    lds_zero(zero, 0, KP, tid, 64 * F_WAVES);
+    __syncthreads();  // B1: x's terms and the stashes
+    const float a = tile_dot<MM, 1>(tl, a_source(vec, zero, KP, lane), table, lane, stash);
+    const float tot = a + bias_word_value(bw, L.bias_dtype, brow);  // lanes 0..15: row row0 + lane
+    // rows alternate gate, up: lane 2r (r < 8) holds h value 8 (wave % 4) + r of block kb,
+    // rounded to bf16 as the reference's bf16 expert computes it
+    const float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(tot), 0xB1, 0xF, 0xF, false));
+    const float hv = bf16_bits_to_f32(f32_to_bf16_bits(swiglu_oai(L, tot, up)));
+    // the maximum over lanes 0, 2, .., 14: quad_perm [2,3,0,1] (lane 4i then holds its quad's),
+    // then row_ror 4 and 8 (each lane of the first row then holds all four quads')
+    float mx = lane < 16 && (lane & 1) == 0 ? fabsf(hv) : 0.0f;
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4E, 0xF, 0xF, false)));
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x124, 0xF, 0xF, false)));
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x128, 0xF, 0xF, false)));
+    if (lane == 0) s_max[wave] = mx;
+    __syncthreads();  // B2: the waves' maxima
+    const int w0 = wave & ~3;
+    const float bm = fmaxf(fmaxf(s_max[w0], s_max[w0 + 1]), fmaxf(s_max[w0 + 2], s_max[w0 + 3]));
+    // the block's scale as chunk_terms takes it (exponent of the largest |h|, clamped)
+    const uint32_t mb = f32_to_bf16_bits(bm) & 0x7FFFu;
+    const int e = mb ? min(max((int)(mb >> 7) - 127, -120), 127) : 0;
+    const float s = __uint_as_float((uint32_t)(134 - e) << 23);
+    uint32_t hi2, lo2;
+    fp8_terms(hv * s, 0.0f, hi2, lo2);
+    // lanes 0, 2, .., 14 hold the wave's 8 values: gather 4 per dword, stored by lanes 0 and 8
+    const uint32_t hb = (hi2 & 255u) | ((lo2 & 255u) << 8);
+    const uint32_t b1 = (uint32_t)__shfl_down((int)hb, 2), b2 = (uint32_t)__shfl_down((int)hb, 4),
+                   b3 = (uint32_t)__shfl_down((int)hb, 6);
+    if (lane == 0 || lane == 8) {
+        const uint32_t ph = (hb & 255u) | ((b1 & 255u) << 8) | ((b2 & 255u) << 16) | ((b3 & 255u) << 24);
+        const uint32_t pl = (hb >> 8) | ((b1 >> 8) << 8) | ((b2 >> 8) << 16) | ((b3 >> 8) << 24);
+        const int64_t o = (int64_t)kb * 32 + 8 * (wave & 3) + (lane >> 1);
+        store_agent(reinterpret_cast<uint32_t*>(terms + o), ph);
+        store_agent(reinterpret_cast<uint32_t*>(terms + I + o), pl);
+    }
+    // the block's A-scale byte at its place in the A-scale table (by the block's first wave);
+    // the pair's first workgroup also gives the table's blocks past I a finite scale (1.0:
+    // their terms read as zero)
+    const int nb = I / 32;
+    if ((wave & 3) == 0) {
+        for (int b2i = lane; b2i < ASC_BYTES; b2i += 64) {
+            if (b2i == kb || (m == 0 && wave == 0 && b2i >= nb)) {
+                const int tb = 4 * (4 * (b2i / 16) + b2i % 4) + (b2i % 16) / 4;
+                __hip_atomic_store(terms + 2 * I + tb, (uint8_t)(b2i == kb ? 120 + e : 127), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the wave's stores are complete
+    __syncthreads();  // B3
+    if (tid == 0) store_agent(&p.sync->gflag[pr * (I / 64) + m], next_gen(g));
+}
+
+template <int MM>
+__device__ __forceinline__ void fused_down(const MxtParams& p, int d) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int KP = 128 * MM;
+    constexpr int KT = (KP + 1023) / 1024 * 1024;  // bytes per term in LDS (whole 1 KB transfers)
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const tsa_expert_layout& L = p.L;
+    const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
+    const int RB = H / 16;
+    const int t = d / RB;
+    const int64_t n0 = (int64_t)(d % RB) * 16;
+    int* s_slot = reinterpret_cast<int*>(smem);            // [16]
+    float* s_w = reinterpret_cast<float*>(smem + 64);      // [16]
+    int* s_fail = reinterpret_cast<int*>(smem + 128);      // a helper gave up, or the workspace is poisoned
+    uint32_t* s_gen = reinterpret_cast<uint32_t*>(smem + 132);
+    float* s_y = reinterpret_cast<float*>(smem + 256);     // [WAVES][16]
+    uint8_t* tables = smem + 512;                          // [WAVES][128]: the pairs' A-scale tables
+    uint8_t* hs = smem + F_MISC;                           // [WAVES][2][KT]: the pairs' terms
+    uint8_t* zero = hs + WAVES * 2 * KT;                   // [KP]
+    uint8_t* stash = zero + KP + (wave & 3) * (256 * Tile<MM>::MS);  // compute wave's B-scale words
+
+    if (wave >= WAVES) {  // helpers
+        const int j = wave - WAVES;
+        if (j == 0) {  // gen, the routing and the workgroup's flag
+            const uint32_t g = p.sync->gen;  // a plain load, as in the gate_up role
+            if (p.logits) {
+                float lg[4];
+                int es[4], mysel, myslot;
+#pragma unroll
+                for (int jx = 0; jx < 4; ++jx) es[jx] = p.expert_slot[min(lane + 64 * jx, p.E - 1)];
+                load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
+                const float w = route_weights(p, lane, lg, es, k, mysel, myslot);
+                if (lane < k) {
+                    s_slot[lane] = myslot;
+                    s_w[lane] = w;
+                }
+            } else if (lane < k) {
+                s_slot[lane] = p.sel_slot[t * k + lane];
+                s_w[lane] = p.sel_w[t * k + lane];
+            }
+            if (lane == 0) {
+                *s_gen = g;
+                *s_fail = g == GEN_POISON;
+                if (g != GEN_POISON) store_agent(&p.sync->dflag[d], next_gen(g));  // g has been read
+            }
+        }
+        lds_zero(zero, 0, KP, tid - 64 * WAVES, 64 * WAVES);
+        __syncthreads();  // B1: the selection
+        if (j == 0) {  // helper 4: waits for the token's pairs, then copies their terms into LDS
+            const uint32_t g = uniform((int)*s_gen);
+            const uint32_t want = next_gen(g);
+            bool ok = g != GEN_POISON;
+            if (ok && d == p.T * RB - 1) {  // the last workgroup: once every workgroup has read g, advance gen
+                ok = wait_flags(p.sync->dflag, p.T * RB, want, p.wait_limit, lane) &&
+                     wait_flags(p.sync->gflag, p.T * k * (I / 64), want, p.wait_limit, lane);
+                if (lane == 0) {
+                    if (ok)
+                        atomicCAS(&p.sync->gen, g, want);  // agent scope; fails only if a wait gave up meanwhile
+                    else
+                        poison(p.sync);
+                }
+            }
+            if (ok && !wait_token(p, t, want, lane, d)) {
+                ok = false;
+                if (lane == 0) poison(p.sync);
+            }
+            for (int jp = 0; jp < k && ok; ++jp) {
+                const int slot = uniform(s_slot[jp]);
+                if (slot < 0 || slot >= p.n_slots) continue;
+                const uint8_t* src = p.hterm + (t * k + jp) * pair_term_bytes(I);
+                const uint32_t dst = (uint32_t)reinterpret_cast<uintptr_t>(hs + jp * 2 * KT);
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const __amdgpu_buffer_rsrc_t rs =
+                        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src + r * I), (short)0, I, 0x00020000);
+#pragma unroll
+                    for (int i = 0; i < KT / 1024; ++i)
+                        lds_dma16_agent(rs, (uint32_t)(1024 * i + 16 * lane), dst + (uint32_t)(r * KT + 1024 * i));
+                }
+                const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint8_t*>(src + 2 * I), (short)0, ASC_BYTES, 0x00020000);
+                if (lane < 32)
+                    lds_dma4_agent(rt, (uint32_t)(4 * lane), (uint32_t)reinterpret_cast<uintptr_t>(tables + 128 * jp));
+            }
+            if (!ok && lane == 0) *s_fail = 1;
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // the terms are in LDS
+        }
+        __syncthreads();  // B2
+        __syncthreads();  // B3: the weighted rows
+        return;
+    }
+    // compute wave j = wave: its expert's down tile while its helper fetches h
+    __syncthreads();  // B1
+    const int j = wave;
+    const int64_t slot = j < k ? uniform(s_slot[j]) : -1;
+    const float w = j < k ? s_w[j] : 0.0f;
+    const bool live = slot >= 0 && slot < p.n_slots && !uniform(*s_fail);
+    const bool hbias = L.down_bias_off >= 0;
+    const int64_t brow = n0 + (lane & 15);
+    Tile<MM> tl;
+    uint32_t bw = 0;
+    if (live) {
+        const uint8_t* base = p.pool + slot * L.slot_bytes;
+        bw = bias_word(base + (hbias ? L.down_bias_off : 0), L.bias_dtype, hbias ? (int64_t)H : 0, brow);
+        tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
+                      base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
+        tile_stash(tl, stash, lane);
+    }
+    __syncthreads();  // B2
+    float yv = 0.0f;
+    if (uniform(*s_fail)) {
+        yv = __builtin_nanf("");
+    } else if (live) {
+        const float a =
+            tile_dot<MM, 1>(tl, a_source(hs + j * 2 * KT, zero, KT, lane), tables + 128 * j, lane, stash);
+        yv = w * (a + bias_word_value(bw, L.bias_dtype, brow));
+    }
+    if (lane < 16) s_y[wave * 16 + lane] = yv;
+    __syncthreads();  // B3
+    if (wave == 0 && lane < 16) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; ++w2) sum += s_y[w2 * 16 + lane];
+        store_out(p.y, p.y_dtype, (int64_t)t * H + n0 + lane, sum);
+    }
+}
+
+// Both roles take MM = the larger piece count of hidden and inter (pieces past a row's end
+// read zero).
+template <int MM>
+__global__ void __launch_bounds__(64 * F_WAVES) __attribute__((amdgpu_waves_per_eu(4, 4))) mxt_fused_kernel(MxtParams p) {
+    const int b = (int)blockIdx.x;
+    if (b < p.n_gu)
+        fused_gate_up<MM>(p, b);
+    else
+        fused_down<MM>(p, b - p.n_gu);
+}
+
+const void* kernel_for_mm(int MM, int which) {
+#define TSA_MXT_CASE(M)                                                                   \
+    case M:                                                                               \
+        return which == 1 ? reinterpret_cast<const void*>(&mxt_down_kernel<M>)            \
+               : which == 2 ? reinterpret_cast<const void*>(&mxt_fused_kernel<M>)         \
+                           : reinterpret_cast<const void*>(&mxt_gate_up_kernel<M>);
     switch (MM) {
         TSA_MXT_CASE(4)
         TSA_MXT_CASE(8)
@@ -466,10 +867,12 @@ int64_t al256(int64_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
-// Workspace bytes of the tiled decode (after the header): h in bf16, 2 inter bytes per
-// (token, expert) pair, then the routed selection (int32 slots, float weights).
+// Workspace bytes of the tiled decode (after the sync area): h per (token, expert) pair, in
+// bf16 (two launches) or as the down dot's terms (one launch), then the routed selection
+// (int32 slots, float weights).
+static int64_t h_bytes(const tsa_expert_layout& L, int64_t T, int k) { return al256(T * k * pair_term_bytes(L.inter)); }
 int64_t mxt_ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
-    return al256(T * k * 2 * L.inter) + 2 * al256(T * k * 4);
+    return h_bytes(L, T, k) + 2 * al256(T * k * 4);
 }
 
 // Requirements of the tiled path beyond validate_layout: "" if met.
@@ -483,13 +886,14 @@ const char* mxt_unsupported(const tsa_expert_layout& L) {
     return "";
 }
 
-// Enqueue the two launches for T <= 4 tokens, k <= 16 (the caller checked the layout with
-// mxt_unsupported and the pointers' alignment). Unrouted: slots / wts [T, k]; routed:
-// logits [T, E] with E <= 256.
+// Enqueue the decode of T <= 4 tokens, k <= 16 (the caller checked the layout with
+// mxt_unsupported and the pointers' alignment): one launch (mxt_form() 0, sync = the
+// workspace's sync area) or two. Unrouted: slots / wts [T, k]; routed: logits [T, E] with
+// E <= 256.
 int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, const int32_t* slots,
                const float* wts, const void* logits, int logits_dtype, int mode, const int32_t* expert_slot, int64_t E,
-               int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype, uint8_t* ws,
-               int64_t ws_bytes, hipStream_t st) {
+               int32_t* idx_out, float* w_out, int64_t T, int k, const void* x, void* y, int y_dtype, uint8_t* sync,
+               uint8_t* ws, int64_t ws_bytes, hipStream_t st) {
     TSA_REQUIRE(T >= 1 && T <= MAXT && k >= 1 && k <= MAXK, TSA_ERR_SHAPE, "tiled decode launch: T %lld, k %d",
                 (long long)T, k);
     TSA_REQUIRE(!logits || E <= 256, TSA_ERR_SHAPE, "fused routing supports E <= 256 (got %lld)", (long long)E);
@@ -497,16 +901,16 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     TSA_REQUIRE(L.hidden % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0, TSA_ERR_INVALID_ARG,
                 "tiled decode needs 16-byte aligned activations");
     const int ma = pick_mm(mx_tile_groups(L.hidden)), mb = pick_mm(mx_tile_groups(L.inter));
-    const void* ka = kernel_for_mm(ma, false);
-    const void* kd = kernel_for_mm(mb, true);
-    TSA_REQUIRE(ka && kd && L.hidden <= 3072, TSA_ERR_SHAPE, "tiled decode: unsupported sizes");
+    const void* ka = kernel_for_mm(ma, 0);
+    const void* kd = kernel_for_mm(mb, 1);
+    TSA_REQUIRE(ka && kd && L.hidden <= 3072 && L.inter <= 3072, TSA_ERR_SHAPE, "tiled decode: unsupported sizes");
 
     MxtParams p{};
     p.L = L;
     p.pool = pool;
     p.n_slots = n_slots;
     uint8_t* h = ws;
-    const int64_t hb = al256(T * k * 2 * L.inter);
+    const int64_t hb = h_bytes(L, T, k);
     if (logits) {
         p.sel_slot = reinterpret_cast<int32_t*>(h + hb);
         p.sel_w = reinterpret_cast<float*>(h + hb + al256(T * k * 4));
@@ -532,9 +936,23 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     p.dn_tile = 8 * L.inter;
     p.dn_stile = mx_tile_scale_bytes(L.inter);
 
+    void* args[] = {&p};
+    const int64_t n_gu = T * k * (L.inter / 64), n_dn = T * (L.hidden / 16);
+    if (sync && mxt_form() == 0 && k <= WAVES && L.inter % 64 == 0 && n_gu <= MXT_SYNC_GFLAGS &&
+        n_dn <= MXT_SYNC_DFLAGS) {
+        const int mm = ma > mb ? ma : mb;
+        p.sync = reinterpret_cast<MxtSync*>(sync);
+        p.hterm = h;
+        p.wait_limit = mxt_wait_limit();
+        p.n_gu = (int)n_gu;
+        const size_t kp = 128 * (size_t)mm, kt = (kp + 1023) / 1024 * 1024, sb = 256 * (size_t)((mm + 3) / 4);
+        const size_t la = F_MISC + 3 * kp + 128 + F_WAVES * sb, lb = F_MISC + 2 * WAVES * kt + kp + WAVES * sb;
+        TSA_HIP_CHECK(hipLaunchKernel(kernel_for_mm(mm, 2), dim3((unsigned)(n_gu + n_dn)), dim3(64 * F_WAVES), args,
+                                      la > lb ? la : lb, st));
+        return TSA_OK;
+    }
     const size_t lds_a = 3 * 128 * (size_t)ma + ASC_BYTES;
     const size_t lds_b = MISC_LDS + (2 * WAVES + 1) * 128 * (size_t)mb;
-    void* args[] = {&p};
     TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / (8 * GU_WAVES)))), dim3(64 * GU_WAVES), args,
                                   lds_a, st));
     TSA_HIP_CHECK(hipLaunchKernel(kd, dim3((unsigned)(T * (L.hidden / 16))), dim3(256), args, lds_b, st));

@@ -53,6 +53,19 @@ inline bool gguf_geometry(int type, int* block_elems, int* type_size) {
 
 int num_cus();  // compute units of the current device (cached per device)
 
+// The MoE decode workspace starts with a sync area of MXT_SYNC_BYTES, used only by the
+// one-launch MXFP4 decode (moe_decode_mxt.hip): a call counter and one flag per workgroup of
+// a launch (at most MXT_SYNC_GFLAGS gate_up and MXT_SYNC_DFLAGS down workgroups: T <= 4,
+// k <= 16, inter, hidden <= 3072). The other decode paths start after it.
+constexpr int64_t MXT_SYNC_BYTES = 32 << 10;
+constexpr int MXT_SYNC_GFLAGS = 4 * 16 * 96;
+constexpr int MXT_SYNC_DFLAGS = 4 * 192;
+constexpr uint32_t MXT_GEN_POISON = 0x7E7E7E7Eu;  // the call counter after a wait gave up
+// Process-wide settings of the tiled MXFP4 decode (tsa_set_decode_options): its form (0 one
+// launch, 1 two launches) and how many polls a one-launch wait makes before it gives up.
+int mxt_form();
+uint32_t mxt_wait_limit();
+
 
 // ---------------------------------------------------------------- device helpers
 // IEEE binary16 bits -> float by v_cvt_f32_f16: exact for every half, subnormals included

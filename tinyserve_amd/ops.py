@@ -173,10 +173,25 @@ def _n_slots(pool: torch.Tensor, layout: _lib.ExpertLayout) -> int:
 
 
 def moe_decode_workspace(layout: _lib.ExpertLayout, T: int, k: int, device) -> torch.Tensor:
-    """Decode workspace (uninitialised: the decode keeps no state in it between calls)."""
+    """Decode workspace, zeroed: its leading sync area (the one-launch MXFP4 decode's call
+    counter and workgroup flags) must hold one value in every word before the first call."""
     n = ctypes.c_int64()
     _lib.check(_lib.load().tsa_moe_decode_workspace_size(ctypes.byref(layout), int(T), int(k), ctypes.byref(n)))
-    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+    return torch.zeros(max(n.value, 1), dtype=torch.uint8, device=device)
+
+
+def set_decode_options(tiled_form: int = 1, wait_limit: int = 1 << 18) -> None:
+    """Process-wide: the tiled MXFP4 decode in two launches (1, the default) or one (0), and
+    the polls a one-launch wait makes before it gives up (tsa_set_decode_options)."""
+    _lib.check(_lib.load().tsa_set_decode_options(int(tiled_form), int(wait_limit)))
+
+
+def decode_workspace_poisoned(workspace: torch.Tensor) -> bool:
+    """True if a one-launch wait gave up on this workspace (synchronises the current stream)."""
+    out = ctypes.c_int()
+    _lib.check(_lib.load().tsa_moe_decode_workspace_status(workspace.data_ptr(), workspace.numel(), ctypes.byref(out),
+                                                           _lib.stream_handle(workspace.device)))
+    return bool(out.value)
 
 
 def moe_decode(layout: _lib.ExpertLayout, pool: torch.Tensor, slots: torch.Tensor, weights: torch.Tensor,
