@@ -168,3 +168,24 @@ def test_batcher_loop_for_unquantised_experts():
             torch.testing.assert_close(y, ref, rtol=1e-5, atol=1e-5)
     assert cache.hits > 0 and cache.misses > 0
     assert b.batch_execute([], 0) == []
+
+
+@pytest.mark.parametrize("in_out", [True, False])
+def test_inline_forward_square_down(in_out):
+    """hidden == inter (GPT-OSS: 2880 both): the down matrix is square, so its orientation
+    comes from gate_up's. [in, out] storage (HF GPT-OSS: gate_up [H, 2I], down [I, H]) and
+    [out, in] storage (F.linear's) both give x @ W against a direct matmul."""
+    H = I = 16
+    torch.manual_seed(3)
+    wgu = torch.randn(2 * I, H) / H ** 0.5  # [out, in]
+    wdn = torch.randn(H, I) / I ** 0.5
+    shapes = {"gate_up_proj": (H, 2 * I) if in_out else (2 * I, H), "down_proj": (I, H) if in_out else (H, I)}
+    lay = TensorLayout({n: (s, torch.float32) for n, s in shapes.items()})
+    packed = torch.empty(lay.total_bytes, dtype=torch.uint8)
+    pack_tensors(packed, lay, {"gate_up_proj": wgu.T.contiguous() if in_out else wgu,
+                               "down_proj": wdn.T.contiguous() if in_out else wdn})
+    h = torch.randn(3, H)
+    g, u = (h @ wgu.T).chunk(2, dim=-1)
+    ref = (torch.nn.functional.silu(g) * u) @ wdn.T
+    inline = _build_inline_forward(lay, nn.SiLU())
+    torch.testing.assert_close(inline(packed, h), ref)

@@ -252,24 +252,26 @@ def _build_inline_forward(layout: TensorLayout, act_fn):
     """``(packed, h) -> y`` for an unquantised fused-expert slot (``gate_up_proj`` and
     ``down_proj`` as bf16/fp16/fp32 matrices, biases optional) with F.linear; None for
     quantised slots (MXFP4 has _build_mxfp4_inline_forward, GGUF has GGMLExpertForward).
-    A matrix stored [in, out] is transposed as the reference's template does (the hidden
-    size is the dimension gate_up and down share). act_fn None: the GPT-OSS clamped SwiGLU on
-    interleaved (gate, up) columns; otherwise act_fn(gate) * up on the two halves."""
+    A matrix stored [in, out] is transposed as the reference's template does
+    (tinyserve/expert_forward.py:131-149): gate_up maps hidden = min(shape) to 2 inter, so it
+    is transposed when its first dimension is hidden; down maps inter = max(gate_up) / 2 to
+    hidden, so it is transposed when its first dimension is inter. A square down matrix
+    (hidden == inter, as in GPT-OSS) takes gate_up's orientation: the reference transposes
+    it always, which is the same for checkpoints that store both [in, out] (HF GPT-OSS), and
+    right also for ones that store both [out, in]. act_fn None: the GPT-OSS clamped SwiGLU
+    on interleaved (gate, up) columns; otherwise act_fn(gate) * up on the two halves."""
     specs = layout.specs
     if "gate_up_proj" not in specs or "down_proj" not in specs or "gate_up_proj_scales" in specs:
         return None
     gu_shape, gu_dtype = specs["gate_up_proj"]
     dn_shape, _ = specs["down_proj"]
-    if gu_dtype not in (torch.bfloat16, torch.float16, torch.float32) or len(gu_shape) != 2:
+    if gu_dtype not in (torch.bfloat16, torch.float16, torch.float32) or len(gu_shape) != 2 or len(dn_shape) != 2:
         return None
-    common = set(gu_shape) & set(dn_shape)
-    if len(dn_shape) != 2 or len(common) != 1:
+    hidden, gated = min(gu_shape), max(gu_shape) // 2
+    if set(dn_shape) != {hidden, gated}:
         return None
-    hidden = common.pop()
-    inter = dn_shape[1] if dn_shape[0] == hidden else dn_shape[0]
-    # square matrices are taken as [out, in], F.linear's layout
-    gu_transposed = gu_shape[0] == hidden and gu_shape[1] != hidden
-    dn_transposed = dn_shape[0] == inter and dn_shape[1] != inter
+    gu_transposed = gu_shape[0] == hidden
+    dn_transposed = gu_transposed if dn_shape[0] == dn_shape[1] else dn_shape[0] == gated
     has_bias = "gate_up_proj_bias" in specs and "down_proj_bias" in specs
 
     def view(packed, name):

@@ -18,9 +18,12 @@ call over the cache's slot pool, with the expert -> slot lookup done on the devi
 ``tsa_moe_decode_routed`` call (the routing runs inside the decode kernels).
 
 ``install_offloaded_forward`` replaces a MoE block's forward as the reference's hook does
-(tinyserve/_model_hooks.py:479-568): the block's router linear, then the experts through
-the pipeline, with the block's shared expert (if any) on ``pipeline.shared_stream`` joined
-by an event.
+(tinyserve/_model_hooks.py:479-568), with the reference's routing modes: router logits (an
+``nn.Linear`` router on the router kernel) routed inside the decode kernels or by the device
+top-k, or the model's own router's result (``router_native``); then the experts through the
+pipeline, with the block's shared expert (if any) on ``pipeline.shared_stream`` joined by an
+event. ``execute_batched_experts`` and ``schedule_prefetch`` complete the interface the
+reference's hook and batcher call.
 """
 from __future__ import annotations
 
@@ -159,27 +162,95 @@ class ExpertPipeline:
         return res.view(hidden_states.shape)
 
 
-_ROUTE_ORDERS = {"topk_then_softmax": "topk_then_softmax", "softmax_then_topk": "softmax_then_topk"}
+    # ---- the rest of the reference's pipeline interface
+    def execute_batched_experts(self, items, layer_idx: int) -> list[torch.Tensor]:
+        """Expert-level batching over several requests (tinyserve/expert_pipeline.py:706-719):
+        delegates to ExpertBatcher, which runs one grouped call for the whole batch."""
+        from .expert_batcher import ExpertBatcher
+
+        return ExpertBatcher(self).batch_execute(items, layer_idx)
+
+    def schedule_prefetch(self, layer_idx: int, expert_ids=None) -> None:
+        """The reference's prefetch of predicted experts (tinyserve/expert_pipeline.py:721-):
+        with every expert resident it only makes sure the layer's experts have slots; the
+        predicted ids (a list or a device tensor) are not read, so nothing synchronises."""
+        if self.cache is not None:
+            self.ensure_resident(layer_idx)
+
+
+_SOFTMAX_ORDERS = ("topk_then_softmax", "softmax_then_topk", "router_native")
+
+
+def _native_route(result, top_k: int, dtype: torch.dtype):
+    """(top_idx, weights, logits or None) from what a model's own router returned, as
+    tinyserve/_model_hooks.py:429-455 reads it: a tensor of logits (sigmoid, then top-k of
+    the sigmoid values), a (logits, weights, indices) triple (HF GPT-OSS / Qwen3-MoE
+    routers), or a pair (full weights and indices, or indices and weights). All of it runs
+    on the router's device; weights come back in ``dtype``."""
+    if isinstance(result, torch.Tensor):
+        w, idx = torch.topk(torch.sigmoid(result), top_k, dim=-1)
+        return idx, w.to(dtype), None
+    if len(result) == 3:
+        logits, w, idx = result
+        return idx, w.to(dtype), logits
+    first, second = result
+    if second.dtype in (torch.int32, torch.int64):
+        w_full, idx = first, second
+        w = w_full.gather(-1, idx) if w_full.shape[-1] > top_k else w_full
+    else:
+        idx, w = first, second
+    return idx, w.to(dtype), None
+
+
+def _router_linear(router: nn.Module):
+    """The router's (weight, bias) if it is a plain nn.Linear the router kernel can run
+    (tsa_router_logits: bf16 / fp16 / fp32 weights on the GPU, in_features a multiple of 8),
+    else None (the model's module is called)."""
+    if type(router) is not nn.Linear or router.weight.device.type != "cuda":
+        return None
+    if router.weight.dtype not in (torch.bfloat16, torch.float16, torch.float32) or router.in_features % 8:
+        return None
+    return router.weight, router.bias
 
 
 def install_offloaded_forward(moe_block: nn.Module, pipeline: ExpertPipeline, layer_idx: int, router_attr: str,
                               top_k: int, returns_router_logits: bool = False,
-                              softmax_order: str = "topk_then_softmax", routed_decode_tokens: int = 4) -> None:
-    """Replace ``moe_block.forward`` (tinyserve/_model_hooks.py:479-568): router linear
-    (``getattr(moe_block, router_attr)``), then for up to ``routed_decode_tokens`` tokens one
-    routed decode call (routing inside the kernels), for longer inputs the device router
-    plus one batched prefill call; the block's ``shared_experts`` / ``shared_expert`` runs
-    on ``pipeline.shared_stream`` and is joined with an event. ``softmax_order``:
-    ``"topk_then_softmax"`` (GPT-OSS) or ``"softmax_then_topk"`` (renormalised, Qwen3-MoE)."""
-    if softmax_order not in _ROUTE_ORDERS:
-        raise ValueError(f"unsupported softmax_order {softmax_order!r}")
-    mode = _ROUTE_ORDERS[softmax_order]
+                              softmax_order: str = "topk_then_softmax", next_pipeline=None, next_route=None,
+                              next_fate_fn=None, adaptive_fate: bool = True, is_first_layer: bool = False,
+                              all_pipelines=None, routed_decode_tokens: int = 4) -> None:
+    """Replace ``moe_block.forward`` (tinyserve/_model_hooks.py:479-568) with the same
+    arguments.
+
+    Routing (tinyserve/_model_hooks.py:424-476): ``"topk_then_softmax"`` (GPT-OSS) and
+    ``"softmax_then_topk"`` (renormalised unless the block's ``norm_topk_prob`` is False)
+    start from router logits: an ``nn.Linear`` router runs on the router kernel
+    (tsa_router_logits), any other router module is called; up to ``routed_decode_tokens``
+    tokens then take one routed decode call (top-k and softmax inside the decode kernels),
+    longer inputs the device top-k and one batched prefill call. ``"router_native"`` calls the
+    model's router and reads its result as the reference does (``_native_route``), then runs
+    the decode or prefill call on those experts and weights (weights in the hidden dtype, as
+    the reference passes them).
+
+    The block's ``shared_experts`` / ``shared_expert`` runs on ``pipeline.shared_stream``,
+    joined by an event. For one-token decode with ``next_pipeline`` and a ``next_route`` /
+    ``next_fate_fn`` given, ``next_pipeline.schedule_prefetch(layer_idx + 1, ...)`` is called
+    as the reference calls it, and likewise ``all_pipelines[layer_idx + hop]`` for hops 2 and 3;
+    with every expert resident these only check residency. ``returns_router_logits`` returns
+    ``(out, logits)``, logits None when a native router gives none."""
+    if softmax_order not in _SOFTMAX_ORDERS:
+        raise ValueError(f"unsupported softmax_order {softmax_order!r}; expected one of {_SOFTMAX_ORDERS}")
+    renormalize = getattr(moe_block, "norm_topk_prob", True)
+    mode = ("topk_then_softmax" if softmax_order == "topk_then_softmax" else
+            "softmax_then_topk" if renormalize else "softmax_then_topk_no_renorm")
     router = getattr(moe_block, router_attr)
+    linear = _router_linear(router) if softmax_order != "router_native" else None
     shared = getattr(moe_block, "shared_experts", None) or getattr(moe_block, "shared_expert", None)
+    prefetch_fn = next_fate_fn if next_fate_fn is not None else next_route
 
     def offloaded_forward(hidden_states: torch.Tensor, **_kwargs):
         hidden = hidden_states.shape[-1]
         flat = hidden_states.reshape(-1, hidden)
+        T = flat.shape[0]
         shared_out = shared_event = None
         main = torch.cuda.current_stream(flat.device)
         if shared is not None:
@@ -192,16 +263,29 @@ def install_offloaded_forward(moe_block: nn.Module, pipeline: ExpertPipeline, la
             # tensors crossing streams: keep their memory until both streams are done with it
             flat.record_stream(side)
             shared_out.record_stream(main)
-        logits = router(flat)
-        if flat.shape[0] <= routed_decode_tokens:
-            out = pipeline.execute_layer_logits(flat, layer_idx, logits, top_k, mode)
+        if softmax_order == "router_native":
+            idx, w, logits = _native_route(router(flat), top_k, flat.dtype)
+            if T <= routed_decode_tokens:
+                out = pipeline.execute_layer_experts(flat, layer_idx, idx, w)
+            else:
+                out = pipeline.execute_layer_experts_batched(flat, layer_idx, idx, w)
         else:
-            idx, w = ops.route_topk(logits.float(), top_k, mode)
-            out = pipeline.execute_layer_experts_batched(flat, layer_idx, idx, w)
+            logits = ops.router_logits(flat, *linear) if linear is not None else router(flat)
+            if T <= routed_decode_tokens:
+                out = pipeline.execute_layer_logits(flat, layer_idx, logits, top_k, mode)
+            else:
+                idx, w = ops.route_topk(logits.float(), top_k, mode)
+                out = pipeline.execute_layer_experts_batched(flat, layer_idx, idx, w.to(flat.dtype))
         out = out.to(flat.dtype)
         if shared_event is not None:
             main.wait_event(shared_event)
             out = out + shared_out
+        if T == 1 and next_pipeline is not None and prefetch_fn is not None:
+            next_pipeline.schedule_prefetch(layer_idx + 1, None)
+        if T == 1 and all_pipelines is not None:
+            for hop in (2, 3):
+                if layer_idx + hop < len(all_pipelines):
+                    all_pipelines[layer_idx + hop].schedule_prefetch(layer_idx + hop, None)
         out = out.view(hidden_states.shape)
         return (out, logits) if returns_router_logits else out
 
