@@ -30,7 +30,11 @@ Qwen3-30B-A3B-shaped Q5_K/Q6_K MoE layer) the same way, in GB/s of algorithmic b
 dot_scaled_vecmat / _mxfp4_linear) at GPT-OSS-20B's gate_up shape: 5760 x 2880 checkpoint-order
 blocks and scales, bf16 bias and x, batch 1, in GB/s of algorithmic bytes.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5,6,7}]
+--workload 8 is workload 3 from the hidden states: each step runs the GPT-OSS router linear
+(bf16 weight [32, 2880] and bias, tsa_router_logits) and then the routed decode on its logits,
+so it measures the per-layer cost from hidden states to y (router, gate_up, down).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload {1,2,3,4,5,6,7,8}]
 """
 from __future__ import annotations
 
@@ -89,7 +93,8 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 # the experts in checkpoint order).
 STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
-                "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_kernel",)}
+                "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_kernel",),
+                "8": ("router_logits_kernel", "mxt_gate_up_kernel", "mxt_down_kernel")}
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str, key: str, command: str) -> dict:
@@ -138,6 +143,8 @@ class MoEWorkload:
 
     def __init__(self, wl: int, n_layers: int, n_steps: int, dev: torch.device, tiled: bool = True):
         self.wl = wl
+        self.gated = wl == 8  # workload 8: workload 3 from hidden states, through the router linear
+        wl = 3 if self.gated else wl
         base = synth.workload(wl)
         self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
         self.route = base["route"]
@@ -171,6 +178,12 @@ class MoEWorkload:
         self.ws = ops.moe_decode_workspace(self.L, 1, self.k, dev)
         self.expert_slot = torch.arange(self.E, dtype=torch.int32, device=dev)
         self.n_layers = n_layers
+        if self.gated:  # GPT-OSS router per layer: bf16 weight [E, H] and bias, N(0, 1/H) and N(0, 0.02)
+            self.router_w = [(torch.randn((self.E, self.H), device=dev, generator=g) * self.H ** -0.5).to(
+                torch.bfloat16) for _ in range(n_layers)]
+            self.router_b = [(torch.randn(self.E, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+                             for _ in range(n_layers)]
+            self.step_logits = torch.empty((n_steps, self.E), device=dev, dtype=torch.bfloat16)
 
     @staticmethod
     def _fix_scales(p: torch.Tensor, lay, g):
@@ -185,30 +198,39 @@ class MoEWorkload:
                     o, n = lay.offsets[name], lay.sizes[name]
                     b = (torch.randn((p.shape[0], n // 2), device=p.device, generator=g) * 0.02).to(torch.bfloat16)
                     p[:, o : o + n] = b.view(torch.uint8)
-        else:  # GGUF: keep the fp16 super-block scales small and finite
+        else:  # GGUF: keep the fp16 super-block scales small and finite (one strided write per field)
             for name, t in (("gate", 13), ("up", 13), ("down", 14)):
                 o, n = lay.offsets[name], lay.sizes[name]
                 be, ts = synth.QTYPE_SIZES[t]
-                for e in range(p.shape[0]):
-                    blk = p[e, o : o + n].view(-1, ts)
-                    for off in ([0, 2] if t in (12, 13) else [208]):
-                        d = (torch.randn(blk.shape[0], device=p.device, generator=g).abs() * 0.01).to(torch.float16)
-                        blk[:, off : off + 2] = d.view(torch.uint8).view(-1, 2)
+                blk = p[:, o : o + n].view(p.shape[0], -1, ts)  # [experts, super-blocks, bytes]
+                for off in ([0, 2] if t in (12, 13) else [208]):
+                    d = (torch.randn(blk.shape[:2], device=p.device, generator=g).abs() * 0.01).to(torch.float16)
+                    blk[:, :, off : off + 2] = d.view(torch.uint8).view(*blk.shape[:2], 2)
 
     def bytes_per_step(self) -> int:
-        """Algorithmic HBM bytes of one step: k experts' weights + activations + logits."""
+        """Algorithmic HBM bytes of one step: k experts' weights + activations + logits (fp32
+        in; workload 8 reads the bf16 router weight and bias and writes and reads bf16 logits)."""
+        if self.gated:
+            return self.k * self.slot_bytes + 2 * self.H * 2 + self.E * self.H * 2 + self.E * 2 + 2 * self.E * 2
         return self.k * self.slot_bytes + 2 * self.H * 2 + self.E * 4
 
     def step(self, s: int) -> None:
-        """One token through one layer: a single fused launch (routing + experts) on the
-        current stream."""
+        """One token through one layer on the current stream: the routed decode (routing inside
+        its launches) from the step's logits, or (workload 8) from the hidden states through
+        the router linear first (tsa_router_logits)."""
         lib = _lib.load()
         st = torch.cuda.current_stream().cuda_stream
-        pool = self.pools[s % self.n_layers]
-        lg = self.logits[s : s + 1]
+        li = s % self.n_layers
+        pool = self.pools[li]
+        lg, lg_dtype = self.logits[s : s + 1], _lib.F32
+        if self.gated:
+            lg, lg_dtype = self.step_logits[s : s + 1], _lib.BF16
+            _lib.check(lib.tsa_router_logits(self.x[s].data_ptr(), _lib.BF16, 1, self.H, self.router_w[li].data_ptr(),
+                                             _lib.BF16, self.router_b[li].data_ptr(), _lib.BF16, self.E, lg.data_ptr(),
+                                             _lib.BF16, st))
         _lib.check(lib.tsa_moe_decode_routed(
             ctypes.byref(self.L), pool.data_ptr(), pool.shape[0], self.expert_slot.data_ptr(), self.E, lg.data_ptr(),
-            _lib.F32, ops.ROUTE_MODES[self.route], 1, self.k, self.x[s].data_ptr(), _lib.BF16, self.y[s].data_ptr(),
+            lg_dtype, ops.ROUTE_MODES[self.route], 1, self.k, self.x[s].data_ptr(), _lib.BF16, self.y[s].data_ptr(),
             _lib.BF16, self.idx[s].data_ptr(), self.w[s].data_ptr(), self.ws.data_ptr(), self.ws.numel(), st))
 
 
@@ -470,7 +492,8 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
     from oracle import torch_cpu as otc
 
     cores, model = _cpu_host()
-    wl = {6: lambda: synth.workload(4, tokens=GgufPrefillWorkload.TOKENS), 7: dict}.get(wl_id, lambda: synth.workload(wl_id))()
+    wl = {6: lambda: synth.workload(4, tokens=GgufPrefillWorkload.TOKENS), 7: dict,
+          8: lambda: synth.workload(3)}.get(wl_id, lambda: synth.workload(wl_id))()
     if wl_id == 1:
         x = torch.from_numpy(wl["x"]).reshape(1, -1)
         w = otc.as_u8(wl["w"])
@@ -493,12 +516,18 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
         dequant = lambda: otc.mxfp4_dequant(blocks, scales)  # noqa: E731
         matmul = lambda W: x @ W.T + bias  # noqa: E731
         work, unit, what = N * (K // 2 + K // 32) + 2 * N + 2 * K + 2 * N, "GB/s", "MXFP4 5760 x 2880 matvecs"
-    elif wl_id in (3, 4):
+    elif wl_id in (3, 4, 8):
         x = torch.from_numpy(synth.bf16_to_f32(wl["x_bits"][:1]))
-        route = oex.route_topk_then_softmax if wl_id == 3 else oex.route_softmax_then_topk
-        idx, wts = route(wl["logits"][:1], wl["top_k"])
+        route = oex.route_softmax_then_topk if wl_id == 4 else oex.route_topk_then_softmax
+        logits = wl["logits"][:1]
+        if wl_id == 8:  # the router linear from the hidden states (timed with the matmuls)
+            rr = np.random.default_rng(8)
+            wr = torch.from_numpy(synth.bf16_to_f32(synth.bf16_normal(rr, (wl["E"], wl["hidden"]), wl["hidden"] ** -0.5)))
+            br = torch.from_numpy(synth.bf16_to_f32(synth.bf16_normal(rr, (wl["E"],), 0.02)))
+            logits = (x @ wr.T + br).numpy()
+        idx, wts = route(logits, wl["top_k"])
         sel = [otc.torch_expert(wl["experts"][int(e)]) for e in idx[0]]
-        if wl_id == 3:
+        if wl_id != 4:
             dequant = lambda: [otc.mxfp4_expert_weights(e) for e in sel]  # noqa: E731
             ffn = lambda W, e: otc.mxfp4_expert_ffn(x, *W, e["gate_up_bias"], e["down_bias"])  # noqa: E731
         else:
@@ -506,6 +535,10 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
             ffn = lambda W, e: otc.gguf_expert_ffn(x, *W)  # noqa: E731
         matmul = lambda Ws: sum(float(c) * ffn(W, e) for c, W, e in zip(wts[0], Ws, sel))  # noqa: E731
         work = wl["top_k"] * wl["layout"].total_bytes + 2 * wl["hidden"] * 2 + wl["E"] * 4
+        if wl_id == 8:
+            experts_only = matmul
+            matmul = lambda Ws: (x @ wr.T + br, experts_only(Ws))[1]  # noqa: E731
+            work += wl["E"] * wl["hidden"] * 2 + wl["E"] * 2  # router weight and bias; logits bf16 out and in
         unit, what = "GB/s", f"single-token MoE-layer decodes (top-{wl['top_k']} of {wl['E']} experts)"
     else:
         n_tok = 64
@@ -560,7 +593,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
-    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5, 6, 7])
+    ap.add_argument("--workload", type=int, default=3, choices=[1, 2, 3, 4, 5, 6, 7, 8])
     ap.add_argument("--layers-prefill", type=int, default=3, help="workloads 5, 6: distinct layers rotated per step")
     ap.add_argument("--prefill-mfma", choices=["fp6", "bf16"], default="fp6",
                     help="workload 5: the GEMMs' MFMA form (fp4 x fp6 terms, or weights expanded to bf16)")
@@ -615,7 +648,7 @@ def main() -> int:
 
     # warmup (eager), also validates every call
     for s in range(W):
-        wl.step(s % max(len(wl.logits), 1) if args.workload in (3, 4) else s)
+        wl.step(s % max(len(wl.logits), 1) if args.workload in (3, 4, 8) else s)
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream()
@@ -664,6 +697,9 @@ def main() -> int:
                      "with a per-32-value e8m0 block scale (exact for values within 2^9 of their block's maximum) "
                      "on the scaled fp8 x fp4 MFMA, fp32 accumulate; h rounded to bf16 between the launches",
                   4: "gguf q5_k/q6_k weights, bf16 activations, fp32 accumulate",
+                  8: "bf16 router linear (fp32 accumulate, bf16 logits), then as workload 3: mxfp4 weights x bf16 "
+                     "activations as two fp8 e4m3 terms per value with per-32-value e8m0 block scales on the scaled "
+                     "fp8 x fp4 MFMA, fp32 accumulate",
                   7: "mxfp4 weights (e2m1 x e8m0), bf16 activations and bias, fp32 accumulate"}[args.workload],
         "data": f"synthetic: seeded native-format weights, {n_layers} resident layers (or copies) rotated per step",
         "config": {
@@ -671,7 +707,9 @@ def main() -> int:
                          2: "one gguf expert ffn, q4_k gate/up 2880 -> 2880, q6_k down (batch 1)",
                          3: "gpt-oss-20b-shaped mxfp4 moe layer decode (hidden 2880, 32 experts, top-4, batch 1)",
                          4: "qwen3-30b-a3b-shaped gguf moe layer decode (hidden 2048, 128 experts, top-8)",
-                         7: "mxfp4 matvec 5760 x 2880 (gpt-oss-20b gate_up shape, dot_scaled_vecmat, batch 1)"}[args.workload],
+                         7: "mxfp4 matvec 5760 x 2880 (gpt-oss-20b gate_up shape, dot_scaled_vecmat, batch 1)",
+                         8: "gpt-oss-20b-shaped mxfp4 moe layer decode from hidden states: router linear (bias) + "
+                            "top-4 of 32 + experts (hidden 2880, batch 1)"}[args.workload],
             "bytes_per_step": nbytes,
             "layers_rotated": n_layers,
             "pool_layout": "mxfp4 16-row mfma tiles" if wl.tiled else "checkpoint order",

@@ -26,6 +26,9 @@ def _bf16_bits(a: np.ndarray) -> np.ndarray:
 
 @pytest.mark.parametrize("T,H,E,xdt,wdt,bias,odt", [
     (1, 2880, 32, torch.bfloat16, torch.bfloat16, True, torch.bfloat16),    # GPT-OSS router, decode
+    (2, 2880, 32, torch.bfloat16, torch.bfloat16, True, torch.bfloat16),    # decode kernel, two tokens
+    (3, 4104, 20, torch.float32, torch.float32, True, torch.float32),       # decode kernel, two passes over H
+    (4, 72, 5, torch.float16, torch.bfloat16, False, torch.float32),        # decode kernel, H below one pass
     (5, 2048, 128, torch.bfloat16, torch.bfloat16, False, torch.float32),   # Qwen3-MoE router, fp32 logits
     (37, 64, 3, torch.float32, torch.float32, True, torch.float32),         # E not a multiple of 4, ragged T
     (9, 512, 16, torch.float16, torch.bfloat16, True, torch.float16),

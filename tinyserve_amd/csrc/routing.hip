@@ -179,6 +179,92 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const void* __restri
     }
 }
 
+// The same for a decode step (T <= 4 tokens, all in one launch row): latency-bound, so each
+// lane issues every load of its part of the row and of the tokens' x (chunks l, l + 64, ..,
+// CH per pass: one pass for H <= 512 CH) as raw words before it converts any, one memory
+// round trip instead of one per chunk. The dtypes are template arguments (WDT for w, XDT
+// for x): with a runtime dtype branch around each load the compiler waits for it before the
+// next, and the branchy code is fetched cold into the instruction cache on every call. Chunks
+// past H are clamped to a valid address and contribute zero.
+template <int DT>
+__device__ __forceinline__ void raw8(const void* base, int64_t i, uint4& a, uint4& b) {
+    if (DT == TSA_F32) {
+        a = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i);
+        b = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i + 4);
+    } else {
+        a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    }
+}
+template <int DT>
+__device__ __forceinline__ float raw_value(const uint4& a, const uint4& b, int j) {
+    if (DT == TSA_F32) {
+        const uint4& q = j < 4 ? a : b;
+        return __uint_as_float((j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w);
+    }
+    const uint32_t u = (j >> 1) == 0 ? a.x : (j >> 1) == 1 ? a.y : (j >> 1) == 2 ? a.z : a.w;
+    const uint32_t h = (j & 1) ? u >> 16 : u & 0xFFFFu;
+    return DT == TSA_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+template <int NT, int WDT, int XDT>
+__global__ void __launch_bounds__(256) router_logits_decode_kernel(const void* __restrict__ x, int H,
+                                                                   const void* __restrict__ w,
+                                                                   const void* __restrict__ bias, int bdt, int E,
+                                                                   void* __restrict__ out, int odt) {
+    constexpr int CH = 6;
+    const int lane = threadIdx.x & 63;
+    const int e = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (e >= E) return;  // whole waves
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < H; c0 += 512 * CH) {
+        uint4 wa[CH], wb[CH], xa[NT][CH], xb[NT][CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = min(c0 + 8 * lane + 512 * i, H - 8);
+            raw8<WDT>(w, (int64_t)e * H + c, wa[i], wb[i]);
+#pragma unroll
+            for (int r = 0; r < NT; ++r) raw8<XDT>(x, (int64_t)r * H + c, xa[r][i], xb[r][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const float on = c0 + 8 * lane + 512 * i < H ? 1.0f : 0.0f;  // clamped chunks add zero
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float wv = raw_value<WDT>(wa[i], wb[i], j) * on;
+#pragma unroll
+                for (int r = 0; r < NT; ++r) acc[r] = fmaf(raw_value<XDT>(xa[r][i], xb[r][i], j), wv, acc[r]);
+            }
+        }
+    }
+    const float tot = wave_sum_rows<4>(acc, lane);  // lane 16 r: token r
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && r < NT) {
+        const float b = bias ? load_act(bias, bdt, e) : 0.0f;
+        store_out(out, odt, (int64_t)r * E + e, tot + b);
+    }
+}
+
+template <int NT, int WDT>
+void launch_router_decode_w(const void* x, int xdt, int H, const void* w, const void* bias, int bdt, int E, void* out,
+                            int odt, hipStream_t st) {
+    const dim3 g((unsigned)((E + 3) / 4)), b(256);
+    if (xdt == TSA_F32)
+        hipLaunchKernelGGL((router_logits_decode_kernel<NT, WDT, TSA_F32>), g, b, 0, st, x, H, w, bias, bdt, E, out, odt);
+    else if (xdt == TSA_F16)
+        hipLaunchKernelGGL((router_logits_decode_kernel<NT, WDT, TSA_F16>), g, b, 0, st, x, H, w, bias, bdt, E, out, odt);
+    else
+        hipLaunchKernelGGL((router_logits_decode_kernel<NT, WDT, TSA_BF16>), g, b, 0, st, x, H, w, bias, bdt, E, out, odt);
+}
+template <int NT>
+void launch_router_decode(const void* x, int xdt, int H, const void* w, int wdt, const void* bias, int bdt, int E,
+                          void* out, int odt, hipStream_t st) {
+    if (wdt == TSA_F32)
+        launch_router_decode_w<NT, TSA_F32>(x, xdt, H, w, bias, bdt, E, out, odt, st);
+    else if (wdt == TSA_F16)
+        launch_router_decode_w<NT, TSA_F16>(x, xdt, H, w, bias, bdt, E, out, odt, st);
+    else
+        launch_router_decode_w<NT, TSA_BF16>(x, xdt, H, w, bias, bdt, E, out, odt, st);
+}
+
 }  // namespace
 }  // namespace tsa
 
@@ -201,6 +287,17 @@ extern "C" int tsa_router_logits(const void* x, int x_dtype, int64_t T, int64_t 
     TSA_REQUIRE(aligned(x, x_dtype) && aligned(w, w_dtype), TSA_ERR_INVALID_ARG,
                 "x and w must be 16-byte aligned (32 for f32)");
     TSA_REQUIRE(T <= (int64_t)65535 * RT, TSA_ERR_SHAPE, "router: more than %d tokens per call", 65535 * RT);
+    if (T <= 4) {
+        hipStream_t st = as_stream(stream);
+        switch (T) {
+            case 1: launch_router_decode<1>(x, x_dtype, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype, st); break;
+            case 2: launch_router_decode<2>(x, x_dtype, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype, st); break;
+            case 3: launch_router_decode<3>(x, x_dtype, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype, st); break;
+            default: launch_router_decode<4>(x, x_dtype, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype, st); break;
+        }
+        TSA_LAUNCH_CHECK();
+        return TSA_OK;
+    }
     hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)((T + RT - 1) / RT)), dim3(256), 0,
                        as_stream(stream), x, x_dtype, T, (int)H, w, w_dtype, bias, bias_dtype, (int)E, out, out_dtype);
     TSA_LAUNCH_CHECK();
