@@ -186,8 +186,9 @@ class MoEWorkload:
             self.step_logits = torch.empty((n_steps, self.E), device=dev, dtype=torch.bfloat16)
 
     @staticmethod
-    def _fix_scales(p: torch.Tensor, lay, g):
-        """Random bytes are valid MXFP4 nibbles; scales and biases need the workload's ranges."""
+    def _fix_scales(p: torch.Tensor, lay, g, gguf_types=(13, 13, 14)):
+        """Random bytes are valid MXFP4 nibbles; scales and biases need the workload's ranges
+        (GGUF: the ggml types of gate, up and down)."""
         if "gate_up_proj_scales" in lay.offsets:
             for name in ("gate_up_proj_scales", "down_proj_scales"):
                 o, n = lay.offsets[name], lay.sizes[name]
@@ -199,7 +200,7 @@ class MoEWorkload:
                     b = (torch.randn((p.shape[0], n // 2), device=p.device, generator=g) * 0.02).to(torch.bfloat16)
                     p[:, o : o + n] = b.view(torch.uint8)
         else:  # GGUF: keep the fp16 super-block scales small and finite (one strided write per field)
-            for name, t in (("gate", 13), ("up", 13), ("down", 14)):
+            for name, t in zip(("gate", "up", "down"), gguf_types):
                 o, n = lay.offsets[name], lay.sizes[name]
                 be, ts = synth.QTYPE_SIZES[t]
                 blk = p[:, o : o + n].view(p.shape[0], -1, ts)  # [experts, super-blocks, bytes]
@@ -364,25 +365,37 @@ class PrefillWorkload:
 class GgufPrefillWorkload:
     """Workload 6: resident GGUF layers at workload 4's expert shapes (Q5_K gate/up
     2048 -> 768, Q6_K down, 128 experts), router logits and activations of a 1024-token
-    prefill; one step = one layer's whole batched MoE (softmax -> top-8)."""
+    prefill; one step = one layer's whole batched MoE (softmax -> top-8).
+    ``shape="2880"``: workload 2's expert (Q4_K gate/up 2880 -> 2880, Q6_K down; every
+    matrix's rows straddle super-blocks) in 32-expert layers, a 512-token prefill with
+    Zipf-skewed top-4 (top-k -> softmax) routing."""
 
-    TOKENS = 1024
-
-    def __init__(self, n_layers: int, dev: torch.device):
-        base = synth.workload(4, tokens=self.TOKENS)
-        self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
-        lay = base["layout"]
-        self.L = gguf_expert_layout(lay, {"gate": 13, "up": 13, "down": 14},
-                                    {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
+    def __init__(self, n_layers: int, dev: torch.device, shape: str = "qwen3"):
         g = torch.Generator(device=dev)
         g.manual_seed(20261206)
-        self.pools = [torch.from_numpy(base["pool"]).to(dev)]
-        for _ in range(1, n_layers):  # further layers: random codes, super-block scales in range
-            p = torch.randint(0, 256, base["pool"].shape, dtype=torch.uint8, device=dev, generator=g)
-            MoEWorkload._fix_scales(p, lay, g)
+        if shape == "qwen3":
+            base = synth.workload(4, tokens=1024)
+            self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
+            self.types, self.route = (13, 13, 14), "softmax_then_topk"
+            lay = base["layout"]
+            self.pools = [torch.from_numpy(base["pool"]).to(dev)]
+            logits, x_bits = base["logits"], base["x_bits"]
+        else:  # every layer random codes with in-range super-block scales
+            rng = synth.rng_for(6)
+            self.H = self.I = 2880
+            self.E, self.k, T = 32, 4, 512
+            self.types, self.route = (12, 12, 14), "topk_then_softmax"
+            lay = synth.gguf_layout(self.H, self.I, *self.types)
+            self.pools = []
+            logits, x_bits = synth.zipf_logits(rng, T, self.E), synth.bf16_normal(rng, (T, self.H))
+        self.L = gguf_expert_layout(lay, dict(zip(("gate", "up", "down"), self.types)),
+                                    {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
+        while len(self.pools) < n_layers:  # further layers: random codes, super-block scales in range
+            p = torch.randint(0, 256, (self.E, lay.total_bytes), dtype=torch.uint8, device=dev, generator=g)
+            MoEWorkload._fix_scales(p, lay, g, self.types)
             self.pools.append(p)
-        self.logits = torch.from_numpy(base["logits"]).to(dev)
-        self.x = _bf16(base["x_bits"], dev)
+        self.logits = torch.from_numpy(logits).to(dev)
+        self.x = _bf16(x_bits, dev)
         self.T = self.x.shape[0]
         self.y = torch.empty_like(self.x)
         self.idx = torch.empty((self.T, self.k), dtype=torch.int32, device=dev)
@@ -399,7 +412,7 @@ class GgufPrefillWorkload:
         st = torch.cuda.current_stream().cuda_stream
         pool = self.pools[s % self.n_layers]
         _lib.check(lib.tsa_route_topk(self.logits.data_ptr(), _lib.F32, self.T, self.E, self.k,
-                                      ops.ROUTE_MODES["softmax_then_topk"], self.idx.data_ptr(), self.w.data_ptr(), st))
+                                      ops.ROUTE_MODES[self.route], self.idx.data_ptr(), self.w.data_ptr(), st))
         _lib.check(lib.tsa_moe_prefill(
             ctypes.byref(self.L), pool.data_ptr(), pool.shape[0], self.expert_slot.data_ptr(), self.E,
             self.idx.data_ptr(), self.w.data_ptr(), self.T, self.k, self.x.data_ptr(), _lib.BF16, self.y.data_ptr(),
@@ -410,7 +423,7 @@ def run_prefill(args, dev) -> int:
     gguf = args.workload == 6
     fp6 = args.prefill_mfma == "fp6" and not gguf
     if gguf:
-        wl = GgufPrefillWorkload(args.layers_prefill, dev)
+        wl = GgufPrefillWorkload(args.layers_prefill, dev, args.gguf_shape)
     else:
         wl = PrefillWorkload(args.layers_prefill, dev, _lib.PREFILL_FP6 if fp6 else _lib.PREFILL_BF16)
     peak = MFMA_F6F4_ALGO_PEAK_TFLOPS if fp6 else MFMA_BF16_PEAK_TFLOPS
@@ -441,14 +454,18 @@ def run_prefill(args, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("gguf q5_k/q6_k blocks decoded and rounded to bf16 (as the reference's .to(bf16)), bf16 "
-                  "activations, bf16 MFMA, fp32 accumulate" if gguf else
+        "dtype": (f"gguf {'q5_k' if wl.types[0] == 13 else 'q4_k'}/q6_k blocks decoded and rounded to bf16 (as the "
+                  "reference's .to(bf16)), bf16 activations, bf16 MFMA, fp32 accumulate" if gguf else
                   "mxfp4 weights x activations as two fp6 (e2m3) terms with per-32 e8m0 scales (from bf16), "
                   "scaled fp4 x fp6 MFMA, fp32 accumulate" if fp6 else
                   "mxfp4 weights expanded exactly to bf16, bf16 activations, bf16 MFMA, fp32 accumulate"),
-        "data": f"synthetic: seeded workload-{4 if gguf else 5} layer + {args.layers_prefill - 1} random layers "
-                "rotated per step",
-        "config": {"workload": ("qwen3-30b-a3b-shaped gguf moe layer prefill (1024 tokens, hidden 2048, 128 "
+        "data": (f"synthetic: {args.layers_prefill} random q4_k/q6_k layers rotated per step, seeded routing and "
+                 "activations" if gguf and args.gguf_shape == "2880" else
+                 f"synthetic: seeded workload-{4 if gguf else 5} layer + {args.layers_prefill - 1} random layers "
+                 "rotated per step"),
+        "config": {"workload": ("workload-2-expert gguf moe layer prefill (512 tokens, hidden 2880, 32 q4_k/q6_k "
+                                "experts, zipf top-4; rows straddle super-blocks)" if gguf and args.gguf_shape == "2880"
+                                else "qwen3-30b-a3b-shaped gguf moe layer prefill (1024 tokens, hidden 2048, 128 "
                                 "experts, zipf top-8)" if gguf else
                                 "gpt-oss-20b-shaped mxfp4 moe layer prefill (2048 tokens, hidden 2880, 32 experts, "
                                 "zipf top-4)"), "flops_per_step": wl.flops_per_step(), "tokens": wl.T,
@@ -461,7 +478,8 @@ def run_prefill(args, dev) -> int:
                                          "peak = dense bf16 MFMA")},
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.workload)
+        # the 2880-wide GGUF form has no CPU leg: its layers are random codes, not oracle experts
+        line["cpu_baseline"] = None if gguf and args.gguf_shape == "2880" else cpu_baseline(args.workload)
     print(json.dumps(line))
     return 0
 
@@ -492,7 +510,7 @@ def cpu_baseline(wl_id: int, min_runs: int = 20, warmup: int = 3, budget_s: floa
     from oracle import torch_cpu as otc
 
     cores, model = _cpu_host()
-    wl = {6: lambda: synth.workload(4, tokens=GgufPrefillWorkload.TOKENS), 7: dict,
+    wl = {6: lambda: synth.workload(4, tokens=1024), 7: dict,
           8: lambda: synth.workload(3)}.get(wl_id, lambda: synth.workload(wl_id))()
     if wl_id == 1:
         x = torch.from_numpy(wl["x"]).reshape(1, -1)
@@ -600,6 +618,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--gguf-shape", choices=["qwen3", "2880"], default="qwen3",
+                    help="workload 6: workload 4's layer shape (default), or workload 2's 2880-wide Q4_K/Q6_K "
+                         "expert in 32-expert layers (512 tokens, top-4)")
     ap.add_argument("--decode-form", choices=["one", "two"], default="two",
                     help="workload 3: the tiled decode in one launch (down waits for gate_up in-kernel) or two")
     ap.add_argument("--checkpoint-order", action="store_true",

@@ -7,6 +7,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from tinyserve_amd import _lib, synth
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout
@@ -133,3 +134,26 @@ def test_router_logits_argument_checks(lib):
     rc = lib.tsa_router_logits(None, 2, 1, 16, None, 2, None, 2, 4, None, 2, None)
     assert rc == _lib.ERR_INVALID_ARG and b"null pointer" in lib.tsa_last_error()
     assert lib.tsa_router_logits(None, 2, 0, 16, None, 2, None, 2, 4, None, 2, None) == 0
+
+
+def test_pipeline_tiles_checkpoint_mxfp4_on_copy(lib):
+    """The cache layout a device pipeline picks for an MXFP4 store: the tile order for
+    checkpoint-order slots whose shapes the tiled kernels take, nothing for tiled stores,
+    shapes past the tiled limits or a given cache too small for the tiled bytes."""
+    from types import SimpleNamespace
+
+    from tinyserve_amd.expert_pipeline import ExpertPipeline
+
+    pick = ExpertPipeline._mxfp4_tiled_cache_layout
+    for H, I in ((256, 128), (2880, 2880)):
+        ck, tl = synth.mxfp4_layout(H, I), synth.mxfp4_tiled_layout(H, I)
+        got = pick(SimpleNamespace(layout=ck, tiled=False), None, None)
+        assert got is not None and got.specs == tl.specs and got.offsets == tl.offsets
+        assert list(got.specs) == list(ck.specs)
+        assert pick(SimpleNamespace(layout=tl, tiled=True), None, None) is None
+        assert pick(SimpleNamespace(layout=ck, tiled=False), SimpleNamespace(expert_bytes=tl.total_bytes - 1),
+                    None) is None
+        assert pick(SimpleNamespace(layout=ck, tiled=False), SimpleNamespace(expert_bytes=tl.total_bytes),
+                    None) is not None
+    assert pick(SimpleNamespace(layout=synth.mxfp4_layout(4096, 256), tiled=False), None, None) is None
+    assert pick(SimpleNamespace(layout=synth.mxfp4_layout(256, 128), tiled=False), None, torch.nn.SiLU()) is None

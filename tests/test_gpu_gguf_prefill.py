@@ -3,7 +3,8 @@ decoded to bf16 in LDS, bf16 MFMA, combine in j order) against the oracle's fp32
 (ggml_forward.py:117-151 runs the batched expert with bf16 weights; the oracle's fp32 form
 bounds that within the bf16 tolerance), over every block type, ragged and multi-tile
 expert runs, experts that are not resident, repeated experts, a garbage-filled workspace,
-and the decode-kernel path that small calls and unaligned layouts keep
+rows that straddle super-blocks (K % 256 != 0), and the decode-kernel path that small
+calls and unaligned layouts keep
 (expert_pipeline.py:166-239)."""
 from __future__ import annotations
 
@@ -77,7 +78,10 @@ def _assert_elementwise(y, ref, bound, what, rtol=1e-2, sum_frac=4e-3):
 
 
 def _run(L, experts, pool, rng, T, k, E, expert_slot=None, idx=None, out_dtype=None, workspace=None,
-         bf16_path=True):
+         bf16_path=True, grouped=False):
+    """One prefill call against the oracle; ``grouped``: also require that the grouped GEMMs
+    ran (their bf16 weights put 99% of the outputs within 1e-5 of their absolute-product
+    sums from the bf16-path reference; the decode kernels' exact weights land near 1e-3)."""
     H = L.hidden
     x_bits = synth.bf16_normal(rng, (T, H))
     if idx is None:
@@ -96,6 +100,10 @@ def _run(L, experts, pool, rng, T, k, E, expert_slot=None, idx=None, out_dtype=N
     ref = oex.moe_combine_grouped(x, idx, w, ffn)
     yb, bound = _bf16_path_ref(experts, x, idx, w, es)
     _assert_elementwise(y, yb, bound, "element check", sum_frac=4e-3 if bf16_path else 8e-3)
+    if grouped:  # a bf16 y against the reference rounded the same way
+        yr = _rb(yb) if y.dtype == torch.bfloat16 else yb
+        rel = np.abs(y.float().cpu().numpy().astype(np.float64) - yr) / np.maximum(bound, 1e-30)
+        assert np.quantile(rel, 0.99) < 1e-5, f"not the grouped path: p99 {np.quantile(rel, 0.99):.3g}"
     return y, ref
 
 
@@ -104,7 +112,7 @@ def test_gguf_grouped_prefill_types(types):
     rng = np.random.default_rng(100 + sum(types))
     H, I, E, k, T = 512, 256, 16, 4, 40  # 160 assignments: ragged tiles of the 16 experts
     L, experts, pool = _pool(rng, H, I, types, E)
-    y, ref = _run(L, experts, pool, rng, T, k, E)
+    y, ref = _run(L, experts, pool, rng, T, k, E, grouped=True)
     assert_close_bf16(y, ref, f"GGUF grouped prefill, types {types}")
 
 
@@ -159,3 +167,33 @@ def test_gguf_grouped_prefill_q6_q8_unaligned_base():
     L, experts, pool = _pool(rng, H, I, (14, 14, 8), E, pad=6)
     y, ref = _run(L, experts, pool, rng, T, k, E)
     assert_close_bf16(y, ref, "GGUF grouped prefill, Q6_K / Q8_0 at 2-byte offsets")
+
+
+@pytest.mark.parametrize("types,H,I,pad", [
+    ((12, 12, 12), 288, 96, 0),     # 9 and 3 units per row: rows start at every unit of a super-block
+    ((14, 14, 14), 288, 96, 0),
+    ((13, 13, 14), 2880, 320, 0),   # 2880 % 256 = 64: gate/up rows straddle, down rows too (320 % 256)
+    ((14, 14, 14), 320, 2880, 0),
+    ((14, 14, 8), 320, 2880, 6),    # Q6_K / Q8_0 matrices at 2-byte offsets
+    ((8, 8, 8), 288, 96, 0),        # Q8_0: whole blocks per row, the last K piece partial
+    ((12, 12, 8), 2880, 320, 0),
+])
+def test_gguf_grouped_prefill_straddling_rows(types, H, I, pad):
+    """K not a multiple of 256: a K-quant row starts inside a super-block and its K pieces
+    cover two; the last piece of a row is partial (its other values belong to the next row)."""
+    rng = np.random.default_rng(300 + H + I + sum(types) + pad)
+    E, k, T = 8, 4, 40
+    L, experts, pool = _pool(rng, H, I, types, E, pad=pad)
+    y, ref = _run(L, experts, pool, rng, T, k, E, grouped=True)
+    assert_close_bf16(y, ref, f"GGUF grouped prefill, straddling rows, types {types}, H {H}, I {I}")
+
+
+def test_gguf_grouped_prefill_2880_wide_512_tokens():
+    """Workload 2's expert (Q4_K gate/up 2880 -> 2880, Q6_K down) in an 8-expert layer, a
+    512-token prefill with Zipf top-4: 2048 assignments, every row straddling."""
+    rng = np.random.default_rng(2880)
+    H = I = 2880
+    E, k, T = 8, 4, 512
+    L, experts, pool = _pool(rng, H, I, (12, 12, 14), E)
+    y, ref = _run(L, experts, pool, rng, T, k, E, grouped=True)
+    assert_close_bf16(y, ref, "GGUF grouped prefill, 2880-wide, 512 tokens")

@@ -115,12 +115,26 @@ def test_prefill_checkpoint_layout_ignores_workspace_contents():
         ws.fill_(0xFF)
 
 
-@pytest.mark.parametrize("tiled", [False, True])
-def test_pipeline_entry_points_mxfp4(tiled):
-    H, I, E, k = 256, 128, 8, 4
-    rng, store, experts = _mx_store(H, I, E, 2, seed=23, tiled=tiled)
-    p = ExpertPipeline(store, None, "cuda")
-    assert p._inline_fwd is not None and p._cpp_layout_args["layout"].mx_tiled == int(tiled)
+@pytest.mark.parametrize("H,I,E,k,tiled,tile_on_copy", [
+    (256, 128, 8, 4, False, False),  # checkpoint-order slots, kernels on checkpoint order
+    (256, 128, 8, 4, False, True),   # checkpoint-order store, tiled on the copy into the cache
+    (256, 128, 8, 4, True, True),    # a tiled store, copied as it is
+    (2880, 2880, 4, 2, False, True),  # the GPT-OSS expert shape, tiled on the copy
+])
+def test_pipeline_entry_points_mxfp4(H, I, E, k, tiled, tile_on_copy):
+    rng, store, experts = _mx_store(H, I, E, 2, seed=23 + H, tiled=tiled)
+    p = ExpertPipeline(store, None, "cuda", tile_mxfp4=tile_on_copy)
+    want_tiled = tiled or tile_on_copy
+    assert p._inline_fwd is not None and p._cpp_layout_args["layout"].mx_tiled == int(want_tiled)
+    assert p.kernel_layout(0).mx_tiled == int(want_tiled)
+    if tile_on_copy and not tiled:
+        p.ensure_resident(1)
+        # the cache slot holds exactly the bytes the host tiler gives for the same expert
+        tl = synth.mxfp4_tiled_layout(H, I)
+        want = synth.pack_mxfp4_expert_tiled(experts[1][E - 1], tl)
+        assert p.cache.expert_bytes == tl.total_bytes and p.cache_layout.offsets == tl.offsets
+        got = p.cache.get_packed(p.cache.lookup(1, E - 1)).cpu().numpy()
+        assert np.array_equal(got, want)
     for layer in (1, 0):
         for T in (1, 3):
             xb = synth.bf16_normal(rng, (T, H))

@@ -1,5 +1,7 @@
 // Library-level C ABI: version, status strings, per-thread last error, block geometry.
+#include <map>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "tsa_common.h"
@@ -29,6 +31,21 @@ int num_cus() {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
     }
     return cache[dev];
+}
+
+hipError_t ensure_dynamic_lds(const void* fn, int bytes) {
+    if (bytes <= 64 * 1024) return hipSuccess;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, int> set;  // (device, kernel) -> bytes allowed
+    std::lock_guard<std::mutex> lock(mu);
+    int& have = set[{dev, fn}];
+    if (have >= bytes) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) have = bytes;
+    return e;
 }
 
 }  // namespace tsa

@@ -172,8 +172,7 @@ int gq_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_
     p.raw_off = sh.raw_off;
     p.raw_stride = sh.raw_stride;
     const void* fn = mv_kernel(type);
-    if (sh.lds > 64 * 1024)
-        TSA_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh.lds));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fn, (int)sh.lds));
     void* args[] = {&p};
     const dim3 grid((unsigned)((N + sh.nw * sh.rw - 1) / (sh.nw * sh.rw)), (unsigned)T);
     TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(64 * sh.nw), args, sh.lds, st));

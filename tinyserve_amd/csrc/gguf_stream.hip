@@ -702,7 +702,7 @@ int gs_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_
     p.raw_off = (int)(xq + xraw);
     p.raw_stride = (int)raw;
     const void* fn = gs_pick(type);
-    if (lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fn, (int)lds));
     void* args[] = {&p};
     const dim3 grid((unsigned)((N + (int64_t)nw * p.rm - 1) / ((int64_t)nw * p.rm)), (unsigned)T);
     TSA_HIP_CHECK(hipLaunchKernel(fn, grid, dim3(64 * nw), args, lds, st));
@@ -799,7 +799,7 @@ int gs_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     p.raw_off = (int)fixed_a;
     p.raw_stride = (int)sa.raw;
     const void* fa = gs_pick_dec(L.gate_type, true);
-    if (sa.lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fa, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sa.lds));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fa, (int)sa.lds));
     void* args_a[] = {&p};
     TSA_HIP_CHECK(hipLaunchKernel(fa, dim3((unsigned)((I + (int64_t)sa.nw * sa.rm - 1) / ((int64_t)sa.nw * sa.rm)), (unsigned)(T * k)),
                                   dim3(64 * sa.nw), args_a, sa.lds, st));
@@ -821,7 +821,7 @@ int gs_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     q.raw_off = (int)fixed_b;
     q.raw_stride = (int)sb.raw;
     const void* fb = gs_pick_dec(L.down_type, false);
-    if (sb.lds > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fb, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sb.lds));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fb, (int)sb.lds));
     void* args_b[] = {&q};
     TSA_HIP_CHECK(hipLaunchKernel(fb, dim3((unsigned)((H + (int64_t)sb.nw * sb.rm - 1) / ((int64_t)sb.nw * sb.rm)), (unsigned)T),
                                   dim3(64 * sb.nw), args_b, sb.lds, st));

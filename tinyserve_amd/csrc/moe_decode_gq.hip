@@ -396,8 +396,8 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
                 lds_b);
     const void* fa = pick_a(L.gate_type);
     const void* fb = pick_b(L.down_type);
-    if (lds_b > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fb, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
-    if (lds_a > 64 * 1024) TSA_HIP_CHECK(hipFuncSetAttribute(fa, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_a));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fb, (int)lds_b));
+    TSA_HIP_CHECK(ensure_dynamic_lds(fa, (int)lds_a));
     void* args[] = {&p};
     const dim3 ga((unsigned)((L.inter + 4 * p.rw - 1) / (4 * p.rw)), (unsigned)(T * k));
     TSA_HIP_CHECK(hipLaunchKernel(fa, ga, dim3(256), args, lds_a, st));

@@ -171,7 +171,7 @@ static int64_t chunked_ws(const tsa_expert_layout& L, int64_t T, int k) {
 }
 
 // MXFP4 tiled pools with bf16 activations take the grouped MFMA GEMMs, and so do GGUF pools
-// (gf_supported: bf16 activations, dimensions multiples of 256, enough assignments); every
+// (gf_supported: bf16 activations, dimensions multiples of 32, enough assignments); every
 // other call runs the decode kernels over chunks of tokens. The workspace covers the
 // largest form the layout can take (the x dtype is not known here).
 static int64_t prefill_ws(const tsa_expert_layout& L, int64_t T, int k, int64_t E) {

@@ -19,7 +19,12 @@
 // of 256 values (one K-quant super-block of each row, or 8 Q8_0 blocks): the piece's raw
 // blocks for the 128 rows (a 16-byte-aligned window per row) and its activations come in
 // by buffer-to-LDS copies, the activations into one of two tiles as the previous piece
-// starts, the raw blocks into one of three areas two pieces ahead. Wave (wr, kh) owns weight
+// starts, the raw blocks into one of three areas two pieces ahead. Where K is not a
+// multiple of 256 (hidden 2880), a K-quant row starts inside a super-block (GGUF stores a
+// matrix as one run of blocks) and a piece of it covers the end of one super-block and the
+// start of the next: that variant keeps each row's super-blocks in a ring of areas, one new
+// super-block per piece, and decodes every 32-value unit from whichever super-block holds
+// it; the last piece of a row is partial, its units past K zeroed. Wave (wr, kh) owns weight
 // rows 32 wr .. + 31 and K half kh of every piece: each lane decodes the values of its row
 // that it feeds v_mfma_f32_32x32x16_bf16 as the A operand straight into registers (no row
 // is decoded twice, no weight tile goes through LDS), the activations are the B operand
@@ -28,8 +33,6 @@
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/ggml_forward.py:117-151 (bf16 weights, F.linear,
 // act_fn(gate) * up), tinyserve/gguf_dequant_torch.py:118-249 (block formats).
-#include <mutex>
-
 #include "fused_common.h"
 #include "mfma_tile.h"
 
@@ -60,22 +63,32 @@ struct GfEntry {
     int slot, row0, rows, pad;
 };
 
-// Raw bytes of one row's K piece: a K-quant super-block, or 8 Q8_0 blocks.
+// Raw bytes of one row's K piece (a raw group): a K-quant super-block, or 8 Q8_0 blocks.
 template <int TY> struct GfType { static constexpr int PB = TY == 8 ? 272 : TY == 12 ? 144 : TY == 13 ? 176 : 210; };
-template <int TY> constexpr int gf_nch() { return (GfType<TY>::PB + 15 + 15) / 16; }
-// Raw areas: the piece in use and the next two (one ahead for Q8_0, whose windows would not
-// fit three areas beside the activation tiles). One area: the 128 rows' windows.
-template <int TY> constexpr int gf_depth() { return TY == 8 ? 2 : 3; }
-template <int TY> constexpr int gf_raw() { return GF_BN * gf_nch<TY>() * 16; }
-template <int TY> constexpr int gf_lds() {
-    return GF_ROFF + gf_depth<TY>() * gf_raw<TY>() > GF_STAGE ? GF_ROFF + gf_depth<TY>() * gf_raw<TY>() : GF_STAGE;
-}
-static_assert(gf_lds<8>() <= 160 * 1024 && gf_lds<12>() <= 160 * 1024 && gf_lds<13>() <= 160 * 1024 &&
-                  gf_lds<14>() <= 160 * 1024, "LDS per workgroup");
-// Alignment of a row's raw piece in LDS, which keeps its global address modulo 16: the
-// K-quant 4/5-bit super-blocks (144 / 176 bytes) stay 16-aligned, Q6_K / Q8_0 2-aligned
-// (the host requires pool, slot size and offsets to keep that).
+// Alignment of a raw group in LDS, which keeps its global address modulo 16: the K-quant
+// 4/5-bit super-blocks (144 / 176 bytes) stay 16-aligned, Q6_K / Q8_0 2-aligned (the host
+// requires pool, slot size and offsets to keep that).
 template <int TY> constexpr int gf_align() { return TY == 12 || TY == 13 ? 16 : 2; }
+// 16-byte chunks of a group's window: from the boundary at or below the group (up to 14
+// bytes before it when 2-aligned) to its end, rounded up to an odd count: the 32 rows a
+// wave's lanes decode from then sit 4 (mod 8) dwords apart and spread over 16 bank groups
+// (an even count halves that or worse: Q6_K's 14 chunks cost its kernel 8% against 15).
+template <int TY> constexpr int gf_nch() { return ((GfType<TY>::PB + (gf_align<TY>() == 16 ? 0 : 14) + 15) / 16) | 1; }
+// Raw areas, each the 128 rows' windows of one group. Plain: the piece in use and the next
+// two (one ahead for Q8_0, whose windows would not fit three areas beside the activation
+// tiles). Straddling (SD): a piece reads two groups of its row, so one more area (Q6_K:
+// none more fit, so its next group flies for one piece only).
+template <int TY, bool SD> constexpr int gf_areas() { return SD ? (TY == 14 ? 3 : 4) : TY == 8 ? 2 : 3; }
+template <int TY> constexpr int gf_raw() { return GF_BN * gf_nch<TY>() * 16; }
+template <int TY, bool SD> constexpr int gf_lds() {
+    return GF_ROFF + gf_areas<TY, SD>() * gf_raw<TY>() > GF_STAGE ? GF_ROFF + gf_areas<TY, SD>() * gf_raw<TY>()
+                                                                  : GF_STAGE;
+}
+static_assert(gf_lds<8, false>() <= 160 * 1024 && gf_lds<12, false>() <= 160 * 1024 &&
+                  gf_lds<13, false>() <= 160 * 1024 && gf_lds<14, false>() <= 160 * 1024 &&
+                  gf_lds<12, true>() <= 160 * 1024 && gf_lds<13, true>() <= 160 * 1024 &&
+                  gf_lds<14, true>() <= 160 * 1024,
+              "LDS per workgroup");
 
 struct GfGemm {
     const uint8_t* pool;
@@ -104,20 +117,23 @@ __device__ __forceinline__ v4i_t gf_desc(const uint8_t* p, int64_t bytes) {
     return v4i_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)n, 0x00020000};
 }
 
-// Byte offset of weight row `row`'s K piece `p` in its matrix.
+// Byte offset in its matrix of raw group q of weight row `row` (K = 32 KU values per row):
+// Q8_0, blocks 8 q .. 8 q + 7 of the row; a K-quant, super-block q counted from the one the
+// row starts in (the row's first value sits at unit (row KU) % 8 of that super-block).
 template <int TY>
-__device__ __forceinline__ uint32_t gf_piece_byte(int row, int p, int K) {
-    return ((uint32_t)row * (uint32_t)(K / GF_KP) + (uint32_t)p) * (uint32_t)GfType<TY>::PB;
+__device__ __forceinline__ uint32_t gf_group_byte(int row, int q, int KU) {
+    if constexpr (TY == 8) return ((uint32_t)row * (uint32_t)KU + 8u * (uint32_t)q) * 34u;
+    else return (((uint32_t)row * (uint32_t)KU >> 3) + (uint32_t)q) * (uint32_t)GfType<TY>::PB;
 }
 
-// The piece's raw windows of the tile's 128 weight rows into LDS: pair q = (row q / NCH,
-// chunk q % NCH) lands at raw + 16 q, so one wave instruction fills 1 KB. The buffers start
+// Raw group q's windows of the tile's 128 weight rows into LDS: pair i = (row i / NCH,
+// chunk i % NCH) lands at raw + 16 i, so one wave instruction fills 1 KB. The buffers start
 // at the 16-byte boundary at or below each matrix (m0 / m1 bytes before it) and end at the
-// boundary at or above its end, and a window starts at the boundary at or below its piece,
+// boundary at or above its end, and a window starts at the boundary at or below its group,
 // so every copy reads 16 whole aligned bytes; rows past the matrix read zero (buffer range).
 template <int TY, bool GU>
 __device__ __forceinline__ void gf_issue_raw(const v4i_t& r0, const v4i_t& r1, uint32_t m0, uint32_t m1, int n0,
-                                             int p, int K, uint32_t raw, int wave, int lane) {
+                                             int p, int KU, uint32_t raw, int wave, int lane) {
     constexpr int NCH = gf_nch<TY>(), TOT = GF_BN * NCH;
     for (int ii = wave; 64 * ii < TOT; ii += GF_THREADS / 64) {
         const int q = 64 * ii + lane;
@@ -126,7 +142,7 @@ __device__ __forceinline__ void gf_issue_raw(const v4i_t& r0, const v4i_t& r1, u
             const bool up = GU && r >= 64;
             const int row = GU ? n0 + (r & 63) : n0 + r;
             const uint32_t m = up ? m1 : m0;
-            const uint32_t voff = ((m + gf_piece_byte<TY>(row, p, K)) & ~15u) + 16u * (uint32_t)c;
+            const uint32_t voff = ((m + gf_group_byte<TY>(row, p, KU)) & ~15u) + 16u * (uint32_t)c;
             if (up) gf_dma(r1, voff, raw + 1024u * (uint32_t)ii);
             else gf_dma(r0, voff, raw + 1024u * (uint32_t)ii);
         }
@@ -212,7 +228,7 @@ __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uin
     }
 }
 
-template <int TY, bool GU>
+template <int TY, bool GU, bool SD>
 __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     extern __shared__ __align__(16) uint8_t smem[];
     // Work id w = (entry, column tile) of this workgroup. Workgroups are dealt round the 8
@@ -228,7 +244,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const GfEntry en = p.table[en_i];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const int wr = wave & 3, kh = wave >> 2, g = lane >> 5, rr = lane & 31;
-    const int K = p.K, P = K / GF_KP, N = p.N;
+    const int K = p.K, KU = K / 32, P = (KU + 7) / 8, N = p.N;
     const int n0 = tile * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
     const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
     const uint8_t* mat0 = base + p.w_off;
@@ -239,29 +255,43 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
                 rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const uint32_t raw = lds0 + GF_ROFF;
-    constexpr int D = gf_depth<TY>(), RAW = gf_raw<TY>();
+    constexpr int RA = gf_areas<TY, SD>(), RAW = gf_raw<TY>();
+    // raw groups per row (a straddling piece also reads the next group) and how many of the
+    // newest may still fly when a piece starts
+    const int NG = SD ? P + 1 : P;
+    constexpr int OUT = RA - 2 - (SD ? 1 : 0);
+    static_assert(OUT == 0 || OUT == 1, "raw groups in flight at a piece's start");
 
     // Activation tiles: row r holds sorted row r's piece as 32 chunks of 16 bytes, chunk c in
     // slot c ^ (r % 32), so the 32 rows of an MFMA operand read fall on distinct banks. They
     // arrive by buffer-to-LDS copies: wave w's copy i fills rows 8w + 2i and 8w + 2i + 1 (1 KB,
     // lane l: row 8w + 2i + l / 32, slot l % 32, so it reads chunk (l % 32) ^ row % 32).
     // Rows past the tile's read zeros (an offset past the buffer's end).
+    // Columns past K (the last piece of a row when K % 256 != 0) read zeros as well. Only the
+    // straddling variants and Q8_0 can have such a piece (a plain K-quant kernel has K % 256 == 0).
+    constexpr bool TAILS = SD || TY == 8;
     const v4i_t rx = gf_desc(reinterpret_cast<const uint8_t*>(p.src), p.src_bytes);
     uint32_t xo[4];
+    int xc[4];  // the first column of this lane's chunk in piece 0
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = 8 * wave + 2 * i + (lane >> 5);
         xo[i] = 0x80000000u;
+        xc[i] = 8 * ((lane & 31) ^ (r & 31));
         if (r < en.rows) {
             const int a = p.perm[en.row0 + r];
             const int64_t xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + r);
-            xo[i] = (uint32_t)(xrow * K * 2) + 16u * (uint32_t)((lane & 31) ^ (r & 31));
+            xo[i] = (uint32_t)(xrow * K * 2) + 2u * (uint32_t)xc[i];
         }
     }
     auto issue_x = [&](int pc) {
         const uint32_t t = lds0 + (uint32_t)(pc & 1) * GF_XB + (uint32_t)(8 * wave) * GF_RS;
+        const bool tail = TAILS && (K & (GF_KP - 1)) && pc == P - 1;  // wave-uniform
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gf_dma(rx, xo[i] + (uint32_t)pc * (2 * GF_KP), t + (uint32_t)(2 * i) * GF_RS);
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t o = tail && GF_KP * pc + xc[i] >= K ? 0x80000000u : xo[i] + (uint32_t)pc * (2 * GF_KP);
+            gf_dma(rx, o, t + (uint32_t)(2 * i) * GF_RS);
+        }
     };
     // this wave's raw copies per piece: instructions ii = wave, wave + 8, .. below NI
     constexpr int NI = (GF_BN * gf_nch<TY>() + 63) / 64, RWA = (NI + 7) / 8, RWB = NI / 8;
@@ -272,6 +302,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const int drow = GU ? n0 + (trow & 63) : n0 + trow;
     constexpr int NCH = gf_nch<TY>();
     const uint32_t dmis = GU && trow >= 64 ? mis1 : mis0;
+    const int ph = SD ? (int)(((uint32_t)drow * (uint32_t)KU) & 7u) : 0;  // the row's first unit in its super-block
 
     v16f_t acc[2];
 #pragma unroll
@@ -279,44 +310,57 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
-    // Piece pc's activations sit in tile pc % 2 and its raw blocks in area pc % D. As piece
-    // pc starts, the copies of piece pc + 1's activations and then of piece pc + D - 1's raw
-    // blocks go out, so the raw blocks fly for D - 1 pieces. A tile or area is rewritten one
-    // piece after it was last read, with the barrier of the piece between. Every load here
-    // is an inline-assembly copy (the compiler counts none of them), so the waits are
-    // explicit: at the top of piece pc everything must have landed but, with three areas,
-    // the raw copies of piece pc + 1 (the newest: RWA or RWB instructions of this wave).
+    // Piece pc's activations sit in tile pc % 2 and raw group q in area q % RA. As piece pc
+    // starts, the copies of piece pc + 1's activations and then of group pc + RA - 1 go out
+    // (into the area group pc - 1 left), so a group flies for RA - 2 pieces (plain) or
+    // RA - 3 (straddling: piece pc reads groups pc and pc + 1). A tile or area is rewritten
+    // one piece after it was last read, with the barrier of the piece between. Every load
+    // here is an inline-assembly copy (the compiler counts none of them), so the waits are
+    // explicit: at the top of piece pc everything must have landed but the newest OUT groups
+    // (the RWA or RWB instructions per group of this wave).
     issue_x(0);
-    gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 0, K, raw, wave, lane);
-    if (D == 3 && P > 1) gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, 1, K, raw + RAW, wave, lane);
+    for (int q = 0; q < RA - 1 && q < NG; ++q)
+        gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, q, KU, raw + (uint32_t)q * RAW, wave, lane);
     for (int pc = 0; pc < P; ++pc) {
         const uint8_t* xt = smem + (pc & 1) * GF_XB;
-        if (D == 3 && pc + 1 < P) {
+        if (OUT == 1 && pc + RA - 2 < NG) {
             if (rw_more) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RWA) : "memory");
             else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RWB) : "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        __syncthreads();  // piece pc's raw blocks and activations are in LDS; tile (pc + 1) % 2 and area (pc + D - 1) % D are free
+        __syncthreads();  // piece pc's raw groups and activations are in LDS; tile (pc + 1) % 2 and area (pc - 1) % RA are free
         if (pc + 1 < P) issue_x(pc + 1);
-        if (pc + D - 1 < P)
-            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + D - 1, K, raw + (uint32_t)((pc + D - 1) % D) * RAW, wave, lane);
-        const uint8_t* sb = smem + GF_ROFF + (pc % D) * RAW + 16 * NCH * trow +
-                            ((dmis + gf_piece_byte<TY>(drow, pc, K)) & 15u);
+        if (pc + RA - 1 < NG)
+            gf_issue_raw<TY, GU>(rs0, rs1, mis0, mis1, n0, pc + RA - 1, KU, raw + (uint32_t)((pc + RA - 1) % RA) * RAW,
+                                 wave, lane);
         // unit uu of the half, then its two K steps (the next unit's decode can issue while
         // these MFMAs run); step j: K 16 j .. + 15 of the half, lane half g holds K 16 j + 8 g .. + 7
         const uint8_t* xr0 = xt + rr * GF_RS;  // sorted row rr (t = 0) and 32 + rr (t = 1): same swizzle
+        // this lane's window of group pc (and, straddling, of group pc + 1)
+        const uint8_t* sb0 = smem + GF_ROFF + (pc % RA) * RAW + 16 * NCH * trow +
+                             ((dmis + gf_group_byte<TY>(drow, pc, KU)) & 15u);
+        const uint8_t* sb1 = SD ? smem + GF_ROFF + ((pc + 1) % RA) * RAW + 16 * NCH * trow +
+                                      ((dmis + gf_group_byte<TY>(drow, pc + 1, KU)) & 15u)
+                                : sb0;
+        const bool tail = TAILS && (KU & 7) && pc == P - 1;  // wave-uniform: the row's last, partial piece
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {
+            const int j = 4 * kh + uu;  // unit of the piece
+            const int v = ph + j;       // straddling: unit v % 8 of group pc + v / 8
             uint32_t av[8];
-            gf_decode_a<TY>(sb, 4 * kh + uu, g, av);
+            gf_decode_a<TY>(SD && v >= 8 ? sb1 : sb0, SD ? v & 7 : j, g, av);
+            if (tail && 8 * pc + j >= KU) {  // past the row's end: another row's values or zeros
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[i] = 0u;
+            }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                const int j = 2 * uu + s2;
+                const int j2 = 2 * uu + s2;
                 const bf16x8 A = __builtin_bit_cast(bf16x8, u32x4{av[4 * s2], av[4 * s2 + 1], av[4 * s2 + 2], av[4 * s2 + 3]});
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    const int c = (16 * kh + 2 * j + g) ^ rr;  // chunk of K 128 kh + 16 j + 8 g
+                    const int c = (16 * kh + 2 * j2 + g) ^ rr;  // chunk of K 128 kh + 16 j2 + 8 g
                     const bf16x8 B = *reinterpret_cast<const bf16x8*>(xr0 + 32 * t * GF_RS + 16 * c);
                     acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc[t], 0, 0, 0);
                 }
@@ -401,20 +445,28 @@ __global__ void __launch_bounds__(1024) gf_table_kernel(const int32_t* __restric
     if (e == 1023) n_entries[0] = pre[1023];
 }
 
-template <int TY, bool GU>
-const void* gf_fn() { return reinterpret_cast<const void*>(&gf_gemm_kernel<TY, GU>); }
+template <int TY, bool GU, bool SD>
+const void* gf_fn() { return reinterpret_cast<const void*>(&gf_gemm_kernel<TY, GU, SD>); }
 
-const void* gf_pick(int t, bool gu) {
+const void* gf_pick(int t, bool gu, bool sd) {
     switch (t) {
-        case 8: return gu ? gf_fn<8, true>() : gf_fn<8, false>();
-        case 12: return gu ? gf_fn<12, true>() : gf_fn<12, false>();
-        case 13: return gu ? gf_fn<13, true>() : gf_fn<13, false>();
-        case 14: return gu ? gf_fn<14, true>() : gf_fn<14, false>();
+        case 8: return gu ? gf_fn<8, true, false>() : gf_fn<8, false, false>();
+        case 12: return sd ? (gu ? gf_fn<12, true, true>() : gf_fn<12, false, true>())
+                           : (gu ? gf_fn<12, true, false>() : gf_fn<12, false, false>());
+        case 13: return sd ? (gu ? gf_fn<13, true, true>() : gf_fn<13, false, true>())
+                           : (gu ? gf_fn<13, true, false>() : gf_fn<13, false, false>());
+        case 14: return sd ? (gu ? gf_fn<14, true, true>() : gf_fn<14, false, true>())
+                           : (gu ? gf_fn<14, true, false>() : gf_fn<14, false, false>());
     }
     return nullptr;
 }
 
-int gf_lds_of(int t) { return t == 8 ? gf_lds<8>() : t == 12 ? gf_lds<12>() : t == 13 ? gf_lds<13>() : gf_lds<14>(); }
+int gf_lds_of(int t, bool sd) {
+    if (t == 8) return gf_lds<8, false>();
+    if (t == 12) return sd ? gf_lds<12, true>() : gf_lds<12, false>();
+    if (t == 13) return sd ? gf_lds<13, true>() : gf_lds<13, false>();
+    return sd ? gf_lds<14, true>() : gf_lds<14, false>();
+}
 
 int64_t gf_al256(int64_t v) { return (v + 255) / 256 * 256; }
 
@@ -447,12 +499,12 @@ bool gf_type_ok(int t, int64_t slot_bytes, int64_t off) {
 
 // Whether the grouped GGUF GEMMs cover a prefill call (else the decode kernels run over
 // token chunks): GGUF slots whose gate and up share a type, hidden and inter multiples of
-// 256 (no row straddles a super-block), bf16 activations, block alignment kept by the slot
-// size and offsets, and at least GF_MIN_ASSIGN assignments.
+// 32 (K-quant rows may start inside a super-block), bf16 activations, block alignment kept
+// by the slot size and offsets, and at least GF_MIN_ASSIGN assignments.
 bool gf_supported(const tsa_expert_layout& L, int x_dtype, int64_t T, int k) {
     const int64_t n = T * k;
-    return L.format == TSA_EXPERT_GGUF && L.gate_type == L.up_type && x_dtype == TSA_BF16 && L.hidden % GF_KP == 0 &&
-           L.inter % GF_KP == 0 && L.gate_bias_off < 0 && L.down_bias_off < 0 && n >= GF_MIN_ASSIGN &&
+    return L.format == TSA_EXPERT_GGUF && L.gate_type == L.up_type && x_dtype == TSA_BF16 && L.hidden % 32 == 0 &&
+           L.inter % 32 == 0 && L.gate_bias_off < 0 && L.down_bias_off < 0 && n >= GF_MIN_ASSIGN &&
            n / GF_BM + 1024 < 65535 && 2 * n * L.inter < ((int64_t)1 << 31) &&
            2 * n * L.hidden < ((int64_t)1 << 31) && gf_type_ok(L.gate_type, L.slot_bytes, L.gate_off) &&
            gf_type_ok(L.up_type, L.slot_bytes, L.up_off) && gf_type_ok(L.down_type, L.slot_bytes, L.down_off);
@@ -484,18 +536,18 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
                        nent, table);
     TSA_LAUNCH_CHECK();
 
-    static std::once_flag lds_once;
-    static hipError_t lds_err = hipSuccess;
-    std::call_once(lds_once, [] {
-        for (int t : {8, 12, 13, 14})
-            for (bool gu : {true, false})
-                if (lds_err == hipSuccess)
-                    lds_err = hipFuncSetAttribute(gf_pick(t, gu), hipFuncAttributeMaxDynamicSharedMemorySize, gf_lds_of(t));
-    });
-    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS): %s", hipGetErrorString(lds_err));
+    // a K-quant matrix whose K is not a multiple of 256 takes the straddling variant
+    const bool sd_gu = L.gate_type != 8 && L.hidden % GF_KP != 0, sd_dn = L.down_type != 8 && L.inter % GF_KP != 0;
+    const void* f_gu = gf_pick(L.gate_type, true, sd_gu);
+    const void* f_dn = gf_pick(L.down_type, false, sd_dn);
+    const int lds_gu = gf_lds_of(L.gate_type, sd_gu), lds_dn = gf_lds_of(L.down_type, sd_dn);
+    for (auto [f, b] : {std::pair<const void*, int>{f_gu, lds_gu}, std::pair<const void*, int>{f_dn, lds_dn}}) {
+        const hipError_t e = ensure_dynamic_lds(f, b);
+        TSA_REQUIRE(e == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", b, hipGetErrorString(e));
+    }
     const unsigned max_entries = (unsigned)(n / GF_BM + (E < n ? E : n) + 1);
-    auto mat_bytes = [](int t, int64_t rows, int64_t K) {
-        return rows * (K / GF_KP) * (t == 8 ? 272 : t == 12 ? 144 : t == 13 ? 176 : 210);
+    auto mat_bytes = [](int t, int64_t rows, int64_t K) {  // rows K values as one run of blocks
+        return t == 8 ? rows * K / 32 * 34 : rows * K / GF_KP * (t == 12 ? 144 : t == 13 ? 176 : 210);
     };
 
     GfGemm g{};
@@ -516,8 +568,8 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     g.w2_off = L.up_off;
     g.w_bytes = mat_bytes(L.gate_type, I, H);
     void* args[] = {&g};
-    TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.gate_type, true), dim3((unsigned)((I + GF_BN / 2 - 1) / (GF_BN / 2)), max_entries),
-                                  dim3(GF_THREADS), args, gf_lds_of(L.gate_type), stream));
+    TSA_HIP_CHECK(hipLaunchKernel(f_gu, dim3((unsigned)((I + GF_BN / 2 - 1) / (GF_BN / 2)), max_entries),
+                                  dim3(GF_THREADS), args, lds_gu, stream));
     // down: h [n, I] -> yk [n, H] by assignment id
     g.src = h;
     g.src_bytes = n * L.inter * 2;
@@ -527,8 +579,8 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     g.w_off = L.down_off;
     g.w2_off = L.down_off;
     g.w_bytes = mat_bytes(L.down_type, H, I);
-    TSA_HIP_CHECK(hipLaunchKernel(gf_pick(L.down_type, false), dim3((unsigned)((H + GF_BN - 1) / GF_BN), max_entries),
-                                  dim3(GF_THREADS), args, gf_lds_of(L.down_type), stream));
+    TSA_HIP_CHECK(hipLaunchKernel(f_dn, dim3((unsigned)((H + GF_BN - 1) / GF_BN), max_entries),
+                                  dim3(GF_THREADS), args, lds_dn, stream));
     return pf_combine(yk, idx, weights, expert_slot, E, n_slots, T, k, H, y, y_dtype, stream);
 }
 

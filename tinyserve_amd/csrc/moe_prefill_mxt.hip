@@ -30,7 +30,6 @@
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/_model_hooks.py:380-394 (MXFP4 expert with biases,
 // clamped SwiGLU).
-#include <mutex>
 
 #include "fused_common.h"
 #include "mfma_tile.h"
@@ -796,18 +795,13 @@ int pf_mxt_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_sl
                        nent, table, ctr);
     TSA_LAUNCH_CHECK();
 
-    static std::once_flag lds_once;
-    static hipError_t lds_err = hipSuccess;
-    std::call_once(lds_once, [] {
-        const void* kernels[4] = {reinterpret_cast<const void*>(pf_gemm_kernel<true, false>),
-                                  reinterpret_cast<const void*>(pf_gemm_kernel<false, false>),
-                                  reinterpret_cast<const void*>(pf_gemm_kernel<true, true>),
-                                  reinterpret_cast<const void*>(pf_gemm_kernel<false, true>)};
-        for (const void* f : kernels)
-            if (lds_err == hipSuccess)
-                lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
-    });
-    TSA_REQUIRE(lds_err == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", PF_LDS, hipGetErrorString(lds_err));
+    for (const void* f : {reinterpret_cast<const void*>(pf_gemm_kernel<true, false>),
+                          reinterpret_cast<const void*>(pf_gemm_kernel<false, false>),
+                          reinterpret_cast<const void*>(pf_gemm_kernel<true, true>),
+                          reinterpret_cast<const void*>(pf_gemm_kernel<false, true>)}) {
+        const hipError_t e = ensure_dynamic_lds(f, PF_LDS);
+        TSA_REQUIRE(e == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", PF_LDS, hipGetErrorString(e));
+    }
     const int grid = (num_cus() / 8) * 8;
     PfGemm g{};
     g.L = L;

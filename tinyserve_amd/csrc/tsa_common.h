@@ -52,6 +52,9 @@ inline bool gguf_geometry(int type, int* block_elems, int* type_size) {
 }
 
 int num_cus();  // compute units of the current device (cached per device)
+// Allow `fn` `bytes` of dynamic LDS on the current device (hipFuncSetAttribute once per
+// device and kernel, for launches above the 64 KiB default; thread-safe).
+hipError_t ensure_dynamic_lds(const void* fn, int bytes);
 
 // The MoE decode workspace starts with a sync area of MXT_SYNC_BYTES, used only by the
 // one-launch MXFP4 decode (moe_decode_mxt.hip): a call counter and one flag per workgroup of

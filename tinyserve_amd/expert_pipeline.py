@@ -33,13 +33,14 @@ import torch.nn as nn
 from . import ops
 from .expert_cache import ExpertCache
 from .expert_forward import (_build_cpp_layout_args, _build_gpu_int4_forward, _build_inline_forward,
-                             _build_mxfp4_inline_forward, _precompute_param_refs)
+                             _build_mxfp4_inline_forward, _precompute_param_refs, mxfp4_expert_layout)
 
 
 class ExpertPipeline:
     def __init__(self, store, template: nn.Module | None = None, device="cuda", staging_buffer_a=None,
                  staging_buffer_b=None, transfer_stream=None, compute_stream=None, cache: ExpertCache | None = None,
-                 shared_stream=None, ram_cache=None, cpu_expert=None, max_top_k: int = 8):
+                 shared_stream=None, ram_cache=None, cpu_expert=None, max_top_k: int = 8,
+                 tile_mxfp4: bool = True):
         self.store = store
         self.template = template
         self.device = torch.device(device)
@@ -52,14 +53,19 @@ class ExpertPipeline:
         self.max_top_k = max_top_k
         self.cache_bias = 0.0
         self.profiler = None
+        self._native_quant = hasattr(store, "ggml_types")
+        # MXFP4 experts kept in checkpoint order by the store are tiled on their way into the
+        # cache, so the cache's slots run the tiled decode and grouped prefill GEMMs
+        self._tiled_layout = (self._mxfp4_tiled_cache_layout(store, cache, getattr(template, "_act_fn", None))
+                              if tile_mxfp4 and not self._native_quant and self.device.type == "cuda" else None)
+        self.cache_layout = self._tiled_layout or store.layout
         if cache is None:  # room for every expert of every layer
             n = store.num_layers * store.num_experts
-            cache = ExpertCache(n, store.expert_bytes, self.device, num_layers=max(self._layer_ids()) + 1,
+            cache = ExpertCache(n, self.cache_layout.total_bytes, self.device, num_layers=max(self._layer_ids()) + 1,
                                 num_experts=store.num_experts)
         self.cache = cache
         self.shared_stream = shared_stream if shared_stream is not None else (
             torch.cuda.Stream(self.device) if self.device.type == "cuda" else None)
-        self._native_quant = hasattr(store, "ggml_types")
         if self._native_quant:
             from .ggml_forward import GGMLExpertForward
 
@@ -73,9 +79,9 @@ class ExpertPipeline:
             self._act_fn = getattr(template, "_act_fn", None)
             self._param_refs = _precompute_param_refs(template, store.layout) if template is not None else None
             self._inline_fwd = (_build_inline_forward(store.layout, self._act_fn)
-                                or _build_mxfp4_inline_forward(store.layout, self._act_fn)
+                                or _build_mxfp4_inline_forward(self.cache_layout, self._act_fn)
                                 or _build_gpu_int4_forward(store.layout, self._act_fn))
-            self._cpp_layout_args = _build_cpp_layout_args(store.layout, self._act_fn)
+            self._cpp_layout_args = _build_cpp_layout_args(self.cache_layout, self._act_fn)
         self._kernel_layouts: dict[int, object] = {}
         self._decode_ws: dict[tuple, torch.Tensor] = {}
 
@@ -86,12 +92,35 @@ class ExpertPipeline:
         return list(layers) if layers else list(range(self.store.num_layers))
 
     # ---- residency and layouts
+    @staticmethod
+    def _mxfp4_tiled_cache_layout(store, cache, act_fn):
+        """The slot layout of a cache that holds the store's MXFP4 experts in the tile order,
+        or None: the store is not MXFP4, already tiled, the tiled kernels do not take its
+        shapes, or a given cache's slots are too small for the tiled bytes."""
+        from .expert_forward import _mx_tiled_specs
+        from .expert_store import TensorLayout, mxfp4_tiled_specs
+
+        layout = getattr(store, "layout", None)
+        if (layout is None or "gate_up_proj_scales" not in layout.specs or "down_proj_scales" not in layout.specs
+                or getattr(store, "tiled", False) or _mx_tiled_specs(layout)):
+            return None
+        try:
+            tiled = TensorLayout(mxfp4_tiled_specs(layout.specs))
+            if cache is not None and cache.expert_bytes < tiled.total_bytes:
+                return None
+            ops.moe_decode_workspace_size(mxfp4_expert_layout(tiled, act_fn, tiled.total_bytes, tiled=True), 1, 1)
+        except (ValueError, NotImplementedError, RuntimeError):
+            return None
+        return tiled
+
     def kernel_layout(self, layer_idx: int):
         """The kernels' tsa_expert_layout of this layer's slots (GGUF layers may differ in type)."""
         L = self._kernel_layouts.get(layer_idx)
         if L is None:
             if self._native_quant:
                 L = self.store.expert_layout(layer_idx)
+            elif self._tiled_layout is not None:
+                L = mxfp4_expert_layout(self._tiled_layout, self._act_fn, self.cache.expert_bytes, tiled=True)
             else:
                 L = self.store.expert_layout(self._act_fn)
             self._kernel_layouts[layer_idx] = L
@@ -107,8 +136,30 @@ class ExpertPipeline:
         for e in range(E):
             if not cache.contains(layer_idx, e):
                 slot = cache.allocate(layer_idx, e)
-                self.store.copy_to_buffer_slot(cache, slot, layer_idx, e)
+                if self._tiled_layout is not None:
+                    self._copy_tiled(slot, layer_idx, e)
+                else:
+                    self.store.copy_to_buffer_slot(cache, slot, layer_idx, e)
         cache.flush_slot_updates()
+
+    def _copy_tiled(self, slot: int, layer_idx: int, expert_idx: int) -> None:
+        """One checkpoint-order MXFP4 expert into a tiled cache slot: its bytes to the device
+        staging buffer, both matrices repacked into the slot by the tiling kernel
+        (tsa_mxfp4_tile), the other tensors (biases) copied as they are. Stream-ordered on
+        the current stream, like the kernels that read the slot."""
+        buf = self.staging_buffer_a
+        self.store.copy_to_buffer(buf, layer_idx, expert_idx)
+        dst, tl = self.cache._packed[slot], self._tiled_layout
+        for name in tl.specs:
+            if name.endswith("_scales") and name[: -len("_scales")] in ("gate_up_proj", "down_proj"):
+                continue
+            off, nb = tl.offsets[name], tl.sizes[name]
+            if name in ("gate_up_proj", "down_proj"):
+                so, sn = tl.offsets[name + "_scales"], tl.sizes[name + "_scales"]
+                ops.mxfp4_tile(buf.get_tensor(name), buf.get_tensor(name + "_scales"),
+                               out_blocks=dst[off : off + nb], out_scales=dst[so : so + sn])
+            else:
+                dst[off : off + nb].copy_(buf.packed[buf.layout.offsets[name] : buf.layout.offsets[name] + nb])
 
     def _workspace(self, L, T: int, k: int) -> torch.Tensor:
         key = (int(L.hidden), int(L.inter), int(L.format), T, k)

@@ -48,6 +48,26 @@ def pack_tensors(dest: torch.Tensor, layout: TensorLayout, tensors: dict[str, to
         dest[off : off + nb].copy_(t.contiguous().reshape(-1).view(torch.uint8))
 
 
+def mxfp4_tiled_specs(specs: dict) -> dict:
+    """The slot specs with both MXFP4 matrices in the 16-row MFMA tile order (mx_tiles): the
+    blocks keep their shape and size, each scale tensor becomes [rows / 16, tile-scale bytes];
+    the key order is kept. Raises ValueError for specs without MXFP4 blocks and scales or
+    with shapes the tile order cannot hold (rows % 16, columns % 32)."""
+    from .mx_tiles import tile_sizes
+
+    out = dict(specs)
+    for mat in ("gate_up_proj", "down_proj"):
+        if mat not in specs or mat + "_scales" not in specs:
+            raise ValueError(f"tiled slots need MXFP4 {mat} blocks and scales (found {sorted(specs)})")
+        shape, dtype = specs[mat]
+        if len(shape) != 3 or shape[2] != 16 or dtype != torch.uint8:
+            raise ValueError(f"{mat}: MXFP4 blocks must be uint8 [rows, K / 32, 16] (got {shape}, {dtype})")
+        N, G, _ = shape
+        _, sb = tile_sizes(N, 32 * G)
+        out[mat + "_scales"] = ((N // 16, sb // (N // 16)), torch.uint8)
+    return out
+
+
 class ExpertBuffer:
     """One expert's packed bytes on a device (tinyserve/expert_store.py:84-112)."""
 
@@ -121,14 +141,7 @@ class ExpertStore:
         num_experts = int(next(iter(first.values())).shape[0])
         specs = {n: (tuple(t.shape[1:]), t.dtype) for n, t in first.items()}
         if tiled:
-            from .mx_tiles import tile_sizes
-
-            for mat in ("gate_up_proj", "down_proj"):
-                if mat not in specs or mat + "_scales" not in specs:
-                    raise ValueError(f"tiled slots need MXFP4 {mat} blocks and scales (found {sorted(specs)})")
-                N, G, _ = specs[mat][0]
-                _, sb = tile_sizes(N, 32 * G)
-                specs[mat + "_scales"] = ((N // 16, sb // (N // 16)), torch.uint8)
+            specs = mxfp4_tiled_specs(specs)
         layout = TensorLayout(specs)
         data = torch.empty((len(layers), num_experts, layout.total_bytes), dtype=torch.uint8,
                            pin_memory=torch.cuda.is_available())

@@ -172,12 +172,18 @@ def _n_slots(pool: torch.Tensor, layout: _lib.ExpertLayout) -> int:
     return n
 
 
+def moe_decode_workspace_size(layout: _lib.ExpertLayout, T: int, k: int) -> int:
+    """Bytes of the decode workspace for T tokens, k experts each; validates the layout
+    (host only, raises RuntimeError with the library's message)."""
+    n = ctypes.c_int64()
+    _lib.check(_lib.load().tsa_moe_decode_workspace_size(ctypes.byref(layout), int(T), int(k), ctypes.byref(n)))
+    return n.value
+
+
 def moe_decode_workspace(layout: _lib.ExpertLayout, T: int, k: int, device) -> torch.Tensor:
     """Decode workspace, zeroed: its leading sync area (the one-launch MXFP4 decode's call
     counter and workgroup flags) must hold one value in every word before the first call."""
-    n = ctypes.c_int64()
-    _lib.check(_lib.load().tsa_moe_decode_workspace_size(ctypes.byref(layout), int(T), int(k), ctypes.byref(n)))
-    return torch.zeros(max(n.value, 1), dtype=torch.uint8, device=device)
+    return torch.zeros(max(moe_decode_workspace_size(layout, T, k), 1), dtype=torch.uint8, device=device)
 
 
 def set_decode_options(tiled_form: int = 1, wait_limit: int = 1 << 18) -> None:
