@@ -186,7 +186,9 @@ int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int
  * no allocating library call) and works in a device array of 8 MiB per GPU that the library
  * holds until the process ends; calls whose workspace would exceed it (see
  * tsa_moe_decode_workspace_size) return TSA_ERR_WORKSPACE. All calls on one GPU share that
- * array, so calls that overlap on one GPU race: order them on one stream.
+ * array, so calls that overlap on one GPU race: order them on one stream. The tiled MXFP4
+ * decode always runs as two launches here (tsa_set_decode_options does not apply), so the
+ * array's sync area is never used.
  * No counterpart in the reference. For callers that cannot allocate: code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation. */
 int tsa_moe_decode_routed_noalloc(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,

@@ -439,11 +439,12 @@ static int two_launch_decode(const tsa_expert_layout& L, const uint8_t* pl, int6
     return TSA_OK;
 }
 
-extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
-                                     const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype,
-                                     int mode, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
-                                     int32_t* idx_out, float* w_out, void* workspace, int64_t workspace_bytes,
-                                     void* stream) {
+// The routed decode; one_launch_ok false keeps the tiled MXFP4 decode on two launches
+// whatever tsa_set_decode_options chose (the workspace's sync area is then never used).
+static int decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                         const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype, int mode,
+                         int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype, int32_t* idx_out,
+                         float* w_out, void* workspace, int64_t workspace_bytes, void* stream, bool one_launch_ok) {
     clear_error();
     int rc = validate_layout(layout);
     if (rc) return rc;
@@ -460,8 +461,8 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
                 (long long)workspace_bytes, (long long)need);
     hipStream_t st = as_stream(stream);
     const uint8_t* pl = static_cast<const uint8_t*>(pool);
-    uint8_t* sync = static_cast<uint8_t*>(workspace);
-    uint8_t* ws = sync + MXT_SYNC_BYTES;
+    uint8_t* ws = static_cast<uint8_t*>(workspace) + MXT_SYNC_BYTES;
+    uint8_t* sync = one_launch_ok ? static_cast<uint8_t*>(workspace) : nullptr;
     const int64_t wsb = workspace_bytes - MXT_SYNC_BYTES;
     if (L.mx_tiled && E <= 256)
         return tiled_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
@@ -470,13 +471,12 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
         const int64_t tc = 65535 / k;
         for (int64_t t0 = 0; t0 < T; t0 += tc) {
             const int64_t n = T - t0 < tc ? T - t0 : tc;
-            rc = tsa_moe_decode_routed(layout, pool, n_slots, expert_slot, E,
-                                       static_cast<const uint8_t*>(logits) + t0 * E * dtype_size(logits_dtype),
-                                       logits_dtype, mode, n, k,
-                                       static_cast<const uint8_t*>(x) + t0 * L.hidden * dtype_size(x_dtype), x_dtype,
-                                       static_cast<uint8_t*>(y) + t0 * L.hidden * dtype_size(y_dtype), y_dtype,
-                                       idx_out ? idx_out + t0 * k : nullptr, w_out ? w_out + t0 * k : nullptr,
-                                       workspace, workspace_bytes, stream);
+            rc = decode_routed(layout, pool, n_slots, expert_slot, E,
+                               static_cast<const uint8_t*>(logits) + t0 * E * dtype_size(logits_dtype), logits_dtype,
+                               mode, n, k, static_cast<const uint8_t*>(x) + t0 * L.hidden * dtype_size(x_dtype),
+                               x_dtype, static_cast<uint8_t*>(y) + t0 * L.hidden * dtype_size(y_dtype), y_dtype,
+                               idx_out ? idx_out + t0 * k : nullptr, w_out ? w_out + t0 * k : nullptr, workspace,
+                               workspace_bytes, stream, one_launch_ok);
             if (rc) return rc;
         }
         return TSA_OK;
@@ -504,6 +504,15 @@ extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void
         return tiled_decode(L, pl, n_slots, slots, w, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x, x_dtype, y,
                             y_dtype, sync, ws, wsb, st);
     return two_launch_decode(L, pl, n_slots, slots, w, T, k, x, x_dtype, y, y_dtype, ws, st);
+}
+
+extern "C" int tsa_moe_decode_routed(const tsa_expert_layout* layout, const void* pool, int64_t n_slots,
+                                     const int32_t* expert_slot, int64_t E, const void* logits, int logits_dtype,
+                                     int mode, int64_t T, int k, const void* x, int x_dtype, void* y, int y_dtype,
+                                     int32_t* idx_out, float* w_out, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+    return decode_routed(layout, pool, n_slots, expert_slot, E, logits, logits_dtype, mode, T, k, x, x_dtype, y,
+                         y_dtype, idx_out, w_out, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int tsa_set_decode_options(int tiled_form, uint32_t wait_limit) {
@@ -575,6 +584,8 @@ extern "C" int tsa_moe_decode_routed_noalloc(const tsa_expert_layout* layout, co
     uint8_t* ws = nullptr;
     rc = scratch_for_current_device(&ws);
     if (rc) return rc;
-    return tsa_moe_decode_routed(layout, pool, n_slots, expert_slot, E, logits, logits_dtype, mode, T, k, x, x_dtype, y,
-                                 y_dtype, idx_out, w_out, ws, kNoAllocScratchBytes, stream);
+    // always two launches: the shared array's sync area could not be cleared by a caller
+    // after a one-launch wait gave up
+    return decode_routed(layout, pool, n_slots, expert_slot, E, logits, logits_dtype, mode, T, k, x, x_dtype, y,
+                         y_dtype, idx_out, w_out, ws, kNoAllocScratchBytes, stream, false);
 }
