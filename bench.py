@@ -93,7 +93,7 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 # the experts in checkpoint order).
 STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
-                "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_kernel",),
+                "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_mfma_kernel",),
                 "8": ("router_logits_decode_kernel", "mxt_gate_up_kernel", "mxt_down_kernel")}
 
 

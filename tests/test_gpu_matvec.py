@@ -97,6 +97,55 @@ def test_mxfp4_matvec_vs_oracle(N, K, T, bias):
     assert_close_bf16(y, ref, f"mxfp4 N {N} K {K} T {T}")
 
 
+@pytest.mark.parametrize("N,K,T,bias_dt,out_dt", [
+    (5760, 2880, 1, torch.bfloat16, torch.bfloat16),  # workload 7: 22.5 pieces of 128 per row
+    (100, 96, 3, torch.float32, torch.float32),        # 3 blocks per row, a partial 16-row slice
+    (48, 4096, 8, None, torch.bfloat16),               # the largest K and a full column of 8 tokens
+    (33, 2880, 9, torch.bfloat16, torch.float32),      # two token columns (8 + 1)
+    (16, 32, 17, None, torch.float32),                 # one block per row, three token columns
+    (64, 4128, 2, torch.bfloat16, torch.bfloat16),     # past the matrix-core form's K: the row kernel
+])
+def test_mxfp4_matvec_matrix_core_shapes(N, K, T, bias_dt, out_dt):
+    """bf16 tokens take the matrix-core matvec (checkpoint-order blocks as the scaled MFMA's
+    fp4 operand, x as block-scaled fp8 terms) up to K 4096: ragged rows, partial pieces,
+    several token columns, bias dtypes and fp32 outputs."""
+    rng = np.random.default_rng(N * 7 + K + T)
+    blocks = rng.integers(0, 256, size=(N, K // 32, 16), dtype=np.uint8)
+    scales = rng.integers(112, 132, size=(N, K // 32), dtype=np.uint8)
+    xf, xd = _x(rng, T, K, torch.bfloat16)
+    ref = xf @ omx.dequant_mxfp4_no_transpose(blocks, scales, "f32").T
+    bias = None
+    if bias_dt is not None:
+        bf = rng.normal(0.0, 0.5, N).astype(np.float32)
+        bias = torch.from_numpy(bf).to(bias_dt)
+        ref = ref + bias.float().numpy()
+        bias = bias.cuda()
+    y = ops.mxfp4_matvec(xd, torch.from_numpy(blocks).cuda(), torch.from_numpy(scales).cuda(), bias, out_dtype=out_dt)
+    assert y.shape == (T, N) and y.dtype == out_dt
+    assert_close_bf16(y, ref, f"mxfp4 N {N} K {K} T {T}")
+
+
+@pytest.mark.parametrize("case", ["outlier_channel", "small_scales", "wide_scales"])
+def test_mxfp4_matvec_matrix_core_precision(case):
+    """The fp8 hi/lo terms keep each bf16 x value exactly unless it lies 2^9 below its
+    32-block's maximum: an x channel 10^3 x the rest, weights with e8m0 scales near
+    2^-14 (outputs ~1e-3), and scales over the whole e8m0 range but NaN."""
+    rng = np.random.default_rng({"outlier_channel": 1, "small_scales": 2, "wide_scales": 3}[case])
+    N, K, T = 320, 2880, 2
+    blocks = rng.integers(0, 256, size=(N, K // 32, 16), dtype=np.uint8)
+    lo, hi = {"outlier_channel": (119, 126), "small_scales": (111, 116), "wide_scales": (60, 190)}[case]
+    scales = rng.integers(lo, hi, size=(N, K // 32), dtype=np.uint8)
+    x = rng.normal(0.0, 1.0, (T, K)).astype(np.float32)
+    if case == "outlier_channel":
+        x[:, 1234] *= 1000.0
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ref = xt.float().numpy().astype(np.float64) @ omx.dequant_mxfp4_no_transpose(blocks, scales, "f32").T.astype(np.float64)
+    y = ops.mxfp4_matvec(xt.cuda(), torch.from_numpy(blocks).cuda(), torch.from_numpy(scales).cuda(), None,
+                         out_dtype=torch.float32)
+    cos, rel = metrics(to_f32(y), ref.astype(np.float32))
+    assert cos >= 0.9999 and rel <= 1e-2, (case, cos, rel)
+
+
 def test_mxfp4_matvec_f32_out_tight():
     rng = np.random.default_rng(2)
     N, K = 256, 2880

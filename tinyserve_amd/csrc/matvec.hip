@@ -257,6 +257,9 @@ int pick_tch(int64_t T, int64_t K) {
 }  // namespace tsa
 
 namespace tsa {
+bool mxm_supported(const void* blocks, const void* x, int x_dtype, int64_t N, int64_t K);
+int mxm_matvec(const uint8_t* blocks, const uint8_t* scales, const void* bias, int bias_dtype, const void* x,
+               int64_t T, void* y, int y_dtype, int64_t N, int64_t K, hipStream_t st);
 const char* gq_matvec_unsupported(int type, const void* w, int64_t T, int64_t K, int64_t N, int x_dtype);
 int gq_matvec(int type, const uint8_t* w, int64_t w_bytes, const void* x, int x_dtype, int64_t T, int64_t K, void* y,
               int y_dtype, int64_t N, hipStream_t st);
@@ -332,8 +335,11 @@ extern "C" int tsa_mxfp4_matvec(const void* blocks, const void* scales, const vo
     TSA_REQUIRE(blocks && scales && x && y, TSA_ERR_INVALID_ARG, "null pointer");
     const uint8_t* bl = static_cast<const uint8_t*>(blocks);
     const uint8_t* sc = static_cast<const uint8_t*>(scales);
-    const int tch = pick_tch(T, K);
     hipStream_t st = as_stream(stream);
+    // bf16 tokens, a few at a time: the matrix-core form (mx_matvec.hip)
+    if (T <= 32 && mxm_supported(blocks, x, x_dtype, N, K))
+        return mxm_matvec(bl, sc, bias, bias_dtype, x, T, y, y_dtype, N, K, st);
+    const int tch = pick_tch(T, K);
     hipError_t e = (reinterpret_cast<uintptr_t>(blocks) & 15) == 0
                        ? launch_mx_aligned(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st)
                        : launch_mx<1>(bl, sc, bias, bias_dtype, x, x_dtype, T, y, y_dtype, N, K, tch, st);

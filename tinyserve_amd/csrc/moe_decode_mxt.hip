@@ -35,6 +35,7 @@
 // SwiGLU), :456-473 (routing), tinyserve/csrc/expert_loop.cpp:83-121 (weighted sum).
 #include "fused_common.h"
 #include "mfma_tile.h"
+#include "mx_terms.h"
 
 namespace tsa {
 
@@ -51,7 +52,6 @@ constexpr int VCH = 3072 / 8 / 64;  // 8-value chunks per lane when a wave holds
 constexpr int ASC_BYTES = 16 * VCH;  // A-scale table of one vector: one e8m0 byte per 32-value block (<= 96 blocks)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 struct MxtParams {
     tsa_expert_layout L;
@@ -165,14 +165,6 @@ __device__ __forceinline__ v4f mfma_fp8_fp4(const v8i& A, const v8i& B, const v4
 // of the next two pieces are read ahead of each MFMA (sched barriers keep them there: left
 // alone the scheduler moves the reads next to their use and the MFMAs wait for LDS, and
 // the reads are volatile so that no earlier pass hoists them all to the top).
-// 16 bytes from LDS (p points into LDS). Volatile: the read stays where it is written; the
-// explicit address space keeps it a ds_read with an immediate offset (through a generic
-// pointer the compiler precomputes a 64-bit flat address per read and runs out of registers).
-typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
-__device__ __forceinline__ u32x4 lds16(const uint8_t* p) {
-    return *(lds_u32x4*)(p);
-}
-typedef __attribute__((address_space(3))) const volatile uint32_t lds_u32;
 template <int MM, int PD = 2>
 __device__ __forceinline__ float tile_dot(const Tile<MM>& tl, const uint8_t* src, const uint8_t* table, int lane,
                                          const uint8_t* bst = nullptr) {
@@ -231,46 +223,13 @@ __device__ __forceinline__ const uint8_t* a_source(const uint8_t* terms, const u
     return row < 2 ? terms + row * kp + 16 * kq : zero;
 }
 
-// Two e4m3 terms of v * s: hi = RNE(v s), lo = RNE(v s - hi) (OCP e4m3; |v s| < 448).
-__device__ __forceinline__ void fp8_terms(float v0, float v1, uint32_t& hi2, uint32_t& lo2) {
-    const int h = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
-    const float r0 = v0 - __builtin_amdgcn_cvt_f32_fp8(h, 0), r1 = v1 - __builtin_amdgcn_cvt_f32_fp8(h, 1);
-    hi2 = (uint32_t)h & 0xFFFFu;
-    lo2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false) & 0xFFFFu;
-}
-
-// A vector's A-scale table: one e8m0 byte per 32-value block b, at byte 4 (4 (b / 16) + b % 4)
-// + (b % 16) / 4, so that dword 4g + q holds in byte j the scale of block 16g + 4j + q, which
-// is block q of piece 4g + j: lane 16q + r reads dword 4g + q for pieces 4g .. 4g + 3 (all
-// lanes read a word: rows 2..15 of A are zero, and every table byte is a finite scale).
-
-// Block-scaled fp8 terms of chunk set i of a bf16 vector: lane l holds chunk c = l + 64 i (8
-// values, zero past the vector's end), so a lane quad holds one 32-value block, block
-// 16 i + l / 4. The quad's largest magnitude has exponent e (clamped to [-120, 127]; 0 for
-// an all-zero block); the lane writes its values' terms v 2^(7 - e) (largest in [128, 256))
-// at terms + 8c (hi) and terms + kp + 8c (lo) if 8c < kp, and the quad's first lane writes
-// the block's A scale 2^(e - 7) (e8m0 byte 120 + e) into the table. Every lane of the wave
-// must be active (the quad maximum is taken by DPP).
+// Block-scaled fp8 terms of chunk set i of a bf16 vector (mx_terms.h): lane l holds chunk
+// c = l + 64 i (8 values, zero past the vector's end), so a lane quad holds block 16 i + l / 4.
+// (All lanes read an A-scale word: rows 2..15 of A are zero, and every table byte is a
+// finite scale.)
 __device__ __forceinline__ void chunk_terms(const u32x4& v, int i, int lane, uint8_t* terms, int kp, uint8_t* table) {
-    us2 mb = us2{0, 0};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) mb = __builtin_elementwise_max(mb, __builtin_bit_cast(us2, v[d] & 0x7FFF7FFFu));
-    // for non-negative bf16 the integer order of the bits is the order of the values
-    int m = mb[0] > mb[1] ? mb[0] : mb[1];
-    m = max(m, __builtin_amdgcn_mov_dpp(m, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
-    m = max(m, __builtin_amdgcn_mov_dpp(m, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-    const int e = m ? min(max((m >> 7) - 127, -120), 127) : 0;
-    const float s = __uint_as_float((uint32_t)(134 - e) << 23);  // 2^(7 - e)
     const int c = lane + 64 * i;
-    if (8 * c < kp) {
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-            fp8_terms(bf16_bits_to_f32(v[d] & 0xFFFFu) * s, bf16_bits_to_f32(v[d] >> 16) * s, hw[d], lw[d]);
-        *reinterpret_cast<uint2*>(terms + 8 * c) = uint2{hw[0] | (hw[1] << 16), hw[2] | (hw[3] << 16)};
-        *reinterpret_cast<uint2*>(terms + kp + 8 * c) = uint2{lw[0] | (lw[1] << 16), lw[2] | (lw[3] << 16)};
-    }
-    if ((lane & 3) == 0) table[4 * (4 * i + ((lane >> 2) & 3)) + (lane >> 4)] = (uint8_t)(120 + e);
+    block_terms(v, c >> 2, (lane & 3) == 0, 8 * c < kp ? terms + 8 * c : nullptr, terms + kp + 8 * c, table);
 }
 
 // Zero bytes [from, to) of an LDS area (16-byte multiples), spread over nthr threads.
