@@ -92,7 +92,7 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 # The kernels of one step of each decode workload (name substrings; "3c" = workload 3 with
 # the experts in checkpoint order).
 STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
-                "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mx_decode_kernel",),
+                "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mxt_gate_up_kernel", "mxt_down_kernel"),
                 "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_mfma_kernel",),
                 "8": ("router_logits_decode_kernel", "mxt_gate_up_kernel", "mxt_down_kernel")}
 
@@ -624,7 +624,7 @@ def main() -> int:
     ap.add_argument("--decode-form", choices=["one", "two"], default="two",
                     help="workload 3: the tiled decode in one launch (down waits for gate_up in-kernel) or two")
     ap.add_argument("--checkpoint-order", action="store_true",
-                    help="workload 3: keep the experts in the checkpoint order (the slower row-major kernel)")
+                    help="workload 3: keep the experts in the checkpoint order (the MFMA decode loading lane by lane)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="launch a 256 MiB copy first (for rocprofv3 --pmc traffic calibration)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),

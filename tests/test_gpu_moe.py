@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import expert as oex
-from tests.helpers import DECODE_SYNC_BYTES, assert_close_bf16, bf16_dev, to_f32
+from tests.helpers import DECODE_SYNC_BYTES, assert_close_bf16, bf16_dev, tiled_h, to_f32
 from tinyserve_amd import ops, synth
 from tinyserve_amd.expert_forward import gguf_expert_layout, mxfp4_expert_layout
 
@@ -142,29 +142,36 @@ def test_moe_decode_negative_slots_and_permutation():
 
 @pytest.mark.parametrize("H,E,k,T,routed", [(512, 6, 4, 1, False), (512, 8, 4, 4, True), (1024, 5, 2, 2, True),
                                              (2048, 4, 4, 1, False), (512, 20, 6, 3, False)])
-def test_fused_decode_intermediate_and_output(H, E, k, T, routed):
-    """The single-launch kernel (H == I, bf16 x, T <= 4): the published intermediate h
-    (workspace, phase A) and the output (phase B) against the oracle."""
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_fused_decode_intermediate_and_output(H, E, k, T, routed, x_dtype):
+    """Checkpoint-order MXFP4 slots (H == I, T <= 4): the published intermediate h
+    (workspace) and the output against the oracle. bf16 x runs the MFMA decode loading the
+    checkpoint order lane by lane (h bf16 [T k, I]); fp32 x the single-launch VALU kernel
+    (h fp32 [T, k, I])."""
     rng, lay, experts, pool = _mx_setup(H, H, E, seed=H + E + k + T)
     L = mxfp4_expert_layout(lay)
     x_bits = synth.bf16_normal(rng, (T, H))
+    xf = synth.bf16_to_f32(x_bits)
+    x = bf16_dev(x_bits) if x_dtype == torch.bfloat16 else torch.from_numpy(xf).cuda()
     logits = rng.normal(size=(T, E)).astype(np.float32)
     idx, w = oex.route_topk_then_softmax(logits, k)
     ws = ops.moe_decode_workspace(L, T, k, "cuda")
-    ws.fill_(0xFF)  # no initialisation needed: the decode keeps no state in it
+    ws.fill_(0xFF)  # the two-launch forms read nothing they did not write in the call
     if routed:
         y, gidx, gw = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
-                                            torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k, workspace=ws,
+                                            torch.from_numpy(logits).cuda(), x, k, workspace=ws,
                                             return_routing=True)
         assert np.array_equal(gidx.cpu().numpy(), idx)
         np.testing.assert_allclose(gw.cpu().numpy(), w, rtol=1e-5)
     else:
         y = ops.moe_decode(L, pool, torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
-                           bf16_dev(x_bits), workspace=ws)
+                           x, workspace=ws)
     torch.cuda.synchronize()
-    xf = synth.bf16_to_f32(x_bits)
     o = DECODE_SYNC_BYTES  # h follows the workspace's sync area
-    h_gpu = ws[o : o + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
+    if x_dtype == torch.bfloat16:
+        h_gpu = tiled_h(ws, T * k, H).reshape(T, k, H)
+    else:
+        h_gpu = ws[o : o + T * k * H * 4].view(torch.float32).cpu().numpy().reshape(T, k, H)
     for t in range(T):
         for j in range(k):
             e = experts[idx[t, j]]

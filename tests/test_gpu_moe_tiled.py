@@ -90,6 +90,50 @@ def test_tiled_decode_vs_oracle(H, I, E, k, T, routed, form):
             assert_close_bf16(h[t, j], h_ref, f"h[{t0 + t},{j}]")
 
 
+@pytest.mark.parametrize("H,I,E,k,T,routed,small", [
+    (256, 128, 6, 2, 1, False, False), (288, 96, 5, 2, 3, True, False),   # 9 and 3 blocks per row
+    (2880, 2880, 8, 4, 1, True, False), (768, 256, 16, 16, 2, False, False),
+    (256, 128, 8, 3, 7, True, False), (512, 1024, 6, 3, 2, True, True),     # 2 launch pairs; small |h|
+    (256, 128, 6, 2, 65, False, False),                                   # past 64 tokens: the VALU kernels
+])
+def test_checkpoint_order_mfma_decode_vs_oracle(H, I, E, k, T, routed, small):
+    """Checkpoint-order slots through the MFMA decode (each lane loads its 16-byte block of
+    the [N, K/32, 16] array and its scale byte): output and the bf16 intermediate h."""
+    rng = np.random.default_rng(H + 5 * I + E + k + T)
+    lay = synth.mxfp4_layout(H, I, bias=not small)
+    sc = dict(scale_lo=113, scale_hi=117) if small else {}
+    experts = [synth.make_mxfp4_expert(rng, H, I, bias=not small, **sc) for _ in range(E)]
+    pool = torch.from_numpy(np.stack([synth.pack_mxfp4_expert(e, lay) for e in experts])).cuda()
+    L = mxfp4_expert_layout(lay)
+    assert L.mx_tiled == 0
+    x_bits = synth.bf16_normal(rng, (T, H))
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    idx, w = oex.route_topk_then_softmax(logits, k)
+    ws = ops.moe_decode_workspace(L, T, k, "cuda")
+    ws.fill_(0xFF)
+    if routed:
+        y, gidx, _ = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                           torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k, workspace=ws,
+                                           return_routing=True)
+        assert np.array_equal(gidx.cpu().numpy(), idx)
+    else:
+        y = ops.moe_decode(L, pool, torch.from_numpy(idx.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
+                           bf16_dev(x_bits), workspace=ws)
+    torch.cuda.synchronize()
+    xf = synth.bf16_to_f32(x_bits)
+    assert_close_bf16(y, _ref(experts, xf, idx, w), "checkpoint-order decode")
+    if T <= 64:  # the last chunk's h (bf16 after the sync area)
+        t0 = 4 * ((T - 1) // 4)
+        tc = T - t0
+        h = tiled_h(ws, tc * k, I).reshape(tc, k, I)
+        for t in range(tc):
+            for j in range(k):
+                e = experts[idx[t0 + t, j]]
+                wgu, _ = oex.mxfp4_expert_weights(e)
+                pre = xf[t0 + t : t0 + t + 1] @ wgu.T + (0.0 if small else e["gate_up_bias"])
+                assert_close_bf16(h[t, j], oex.gptoss_swiglu(pre).reshape(-1), f"h[{t0 + t},{j}]")
+
+
 def test_tiled_equals_checkpoint_order_path():
     """Both layouts of the same experts give the same result (each checked against the oracle)."""
     H, I, E, k = 512, 256, 6, 3

@@ -316,8 +316,15 @@ __global__ void __launch_bounds__(256) tsa_map_slots_kernel(const int32_t* __res
     slots[a] = (e >= 0 && e < E) ? expert_slot[e] : -1;
 }
 
-// Tiled MXFP4 layouts: the MFMA decode over chunks of up to 4 tokens (stream-ordered on
-// the shared workspace).
+// Checkpoint-order MXFP4 pools that the MFMA decode takes (bf16 activations, the layout's
+// sizes and 16-byte alignment, the pool and x aligned); others keep mx_fused_decode.
+static bool mxt_checkpoint_ok(const tsa_expert_layout& L, const uint8_t* pl, const void* x, int x_dtype, int k) {
+    return L.format == TSA_EXPERT_MXFP4 && !L.mx_tiled && x_dtype == TSA_BF16 && k <= 16 && !*mxt_unsupported(L) &&
+           ((reinterpret_cast<uintptr_t>(pl) | reinterpret_cast<uintptr_t>(x)) & 15) == 0;
+}
+
+// Tiled MXFP4 layouts (and checkpoint-order ones, mxt_checkpoint_ok): the MFMA decode over
+// chunks of up to 4 tokens (stream-ordered on the shared workspace).
 static int tiled_decode(const tsa_expert_layout& L, const uint8_t* pl, int64_t n_slots, const int32_t* slots,
                         const float* weights, const void* logits, int logits_dtype, int mode,
                         const int32_t* expert_slot, int64_t E, int32_t* idx_out, float* w_out, int64_t T, int k,
@@ -369,7 +376,7 @@ extern "C" int tsa_moe_decode(const tsa_expert_layout* layout, const void* pool,
     uint8_t* sync = static_cast<uint8_t*>(workspace);
     uint8_t* ws = sync + MXT_SYNC_BYTES;
     const int64_t wsb = workspace_bytes - MXT_SYNC_BYTES;
-    if (L.mx_tiled)
+    if (L.mx_tiled || (T <= 64 && mxt_checkpoint_ok(L, pl, x, x_dtype, k)))
         return tiled_decode(L, pl, n_slots, slots, weights, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, T, k, x,
                             x_dtype, y, y_dtype, sync, ws, wsb, st);
     if (T * k > 65535) {  // the other paths launch one grid row per assignment: token chunks
@@ -464,7 +471,7 @@ static int decode_routed(const tsa_expert_layout* layout, const void* pool, int6
     uint8_t* ws = static_cast<uint8_t*>(workspace) + MXT_SYNC_BYTES;
     uint8_t* sync = one_launch_ok ? static_cast<uint8_t*>(workspace) : nullptr;
     const int64_t wsb = workspace_bytes - MXT_SYNC_BYTES;
-    if (L.mx_tiled && E <= 256)
+    if ((L.mx_tiled || (T <= 64 && mxt_checkpoint_ok(L, pl, x, x_dtype, k))) && E <= 256)
         return tiled_decode(L, pl, n_slots, nullptr, nullptr, logits, logits_dtype, mode, expert_slot, E, idx_out,
                             w_out, T, k, x, x_dtype, y, y_dtype, sync, ws, wsb, st);
     if (!L.mx_tiled && T * k > 65535) {  // the row-per-assignment paths: token chunks, routed one by one

@@ -130,6 +130,57 @@ __device__ __forceinline__ void tile_stash(const Tile<MM>& tl, uint8_t* st, int 
     for (int g = 0; g < Tile<MM>::MS; ++g) *reinterpret_cast<uint32_t*>(st + 4 * (64 * g + lane)) = tl.sc[g];
 }
 
+// ---- checkpoint order ([N, G, 16] blocks, [N, G] scales, G = K / 32): the same MFMA operands,
+// loaded lane by lane. Lane 16q + i loads, for piece m, the 16 bytes of the tile's row i,
+// block 4m + q (its fp4 operand for column i, K block q), so a wave instruction reads 64
+// contiguous bytes of each of the 16 rows; blocks past G read zero. The tile's scale bytes
+// (16 G contiguous bytes, 16-byte aligned) come first as two 16-byte loads per lane into
+// `scr`, for tile_stash_ck. CK_STAGE: LDS bytes of a wave's scale staging area.
+constexpr int CK_STAGE = 2048;  // 16 G <= 2048 (G <= 96)
+template <int MM>
+__device__ __forceinline__ void tile_load_ck(Tile<MM>& tl, u32x4 (&scr)[2], const uint8_t* blocks,
+                                             const uint8_t* scales, int G, int lane) {
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(blocks), (short)0, 256 * G, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(scales), (short)0, 16 * G, 0x00020000);
+    tl.w = Tile<MM>::MS;  // scales past the row are masked in the stash
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+        scr[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (lane + 64 * c), 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {  // nt: streamed once
+        const int g = 4 * m + q;
+        const int off = g < G ? 16 * (i * G + g) : 256 * G;  // past the buffer: zero
+        tl.q[m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The scale bytes of a checkpoint-order tile rearranged into tile_stash's word layout (word
+// g of lane 16q + i: byte j = scale of row i, block 16g + 4j + q; 127, a unit scale, past the
+// row) through the wave's staging area; waits for the scale loads only.
+template <int MM>
+__device__ __forceinline__ void tile_stash_ck(const u32x4 (&scr)[2], uint8_t* stage, uint8_t* st, int G, int lane) {
+    *reinterpret_cast<u32x4*>(stage + 16 * lane) = scr[0];
+    *reinterpret_cast<u32x4*>(stage + 16 * (lane + 64)) = scr[1];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads what its lanes wrote
+    const int i = lane & 15, q = lane >> 4;
+    const uint8_t* row = stage + i * G;
+#pragma unroll
+    for (int g = 0; g < Tile<MM>::MS; ++g) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 16 * g + 4 * j + q;
+            w |= (uint32_t)(b < G ? row[b] : 127) << (8 * j);
+        }
+        *reinterpret_cast<uint32_t*>(st + 4 * (64 * g + lane)) = w;
+    }
+}
+
 // The bias of row r as one dword load bounded to the n-element bias vector (n * element
 // size is a multiple of 4 here; a 2-byte element is the half of its dword that r & 1
 // selects). A zero-size bound (no bias) reads 0. One register, so no reuse of a pending
@@ -270,7 +321,7 @@ __device__ float route_weights(const P& p, int lane, const float lg[4], const in
 // knows the slot. Each wave also loads all of x; in the shadow of the tile loads the waves
 // convert interleaved 512-value chunk sets of x into the shared block-scaled terms and meet
 // at the workgroup's barrier before the dot.
-template <int MM, int NW>
+template <int MM, int NW, bool CK = false>
 __device__ __forceinline__ void gate_up_body(const MxtParams& p, int b) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = 128 * MM;  // padded vector length
@@ -333,8 +384,13 @@ __device__ __forceinline__ void gate_up_body(const MxtParams& p, int b) {
     const int64_t brow = row0 + (lane & 15);
     const uint32_t bw = bias_word(base + (hbias ? L.gate_bias_off : 0), L.bias_dtype, hbias ? 2 * (int64_t)I : 0, brow);
     Tile<MM> tl;
-    tile_load<MM>(tl, base + L.gate_off + (row0 / 16) * p.gu_tile, p.gu_tile,
-                  base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
+    u32x4 scr[2];
+    const int G = H / 32;
+    if constexpr (CK)
+        tile_load_ck<MM>(tl, scr, base + L.gate_off + row0 * 16 * G, base + L.gate_scales_off + row0 * G, G, lane);
+    else
+        tile_load<MM>(tl, base + L.gate_off + (row0 / 16) * p.gu_tile, p.gu_tile,
+                      base + L.gate_scales_off + (row0 / 16) * p.gu_stile, p.gu_stile, lane);
     if (publisher) publish();  // while the tile streams in
 
     // ---- x as block-scaled terms (chunk sets i = wave, wave + NW, ...; past H they are zero)
@@ -342,9 +398,12 @@ __device__ __forceinline__ void gate_up_body(const MxtParams& p, int b) {
     for (int i = 0; i < VCH; ++i)
         if (i % NW == wave) chunk_terms(xr[i], i, lane, vec, KP, table);
     lds_zero(zero, 0, KP, tid, 64 * NW);
+    uint8_t* stash = table + ASC_BYTES + wave * (CK_STAGE + 256 * Tile<MM>::MS) + CK_STAGE;
+    if constexpr (CK) tile_stash_ck<MM>(scr, stash - CK_STAGE, stash, G, lane);
     __syncthreads();  // every pair is live or dead for all waves: all get here or none
 
-    const float a = tile_dot<MM>(tl, a_source(vec, zero, KP, lane), table, lane);
+    const float a = CK ? tile_dot<MM>(tl, a_source(vec, zero, KP, lane), table, lane, stash)
+                       : tile_dot<MM>(tl, a_source(vec, zero, KP, lane), table, lane);
     const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
     const float tot = a + bias;  // lanes 0..15: row row0 + lane
     // rows alternate gate, up: lane 2r holds h[row0 / 2 + r]; lanes 0, 4, 8, 12 store two
@@ -357,9 +416,9 @@ __device__ __forceinline__ void gate_up_body(const MxtParams& p, int b) {
             ((uint32_t)hb & 0xFFFFu) | ((uint32_t)hb2 << 16);
 }
 
-template <int MM>
+template <int MM, bool CK>
 __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p) {
-    gate_up_body<MM, GU_WAVES>(p, (int)blockIdx.x);
+    gate_up_body<MM, GU_WAVES, CK>(p, (int)blockIdx.x);
 }
 
 // ---- launch 2 of the two-launch form: workgroup d (token d / (H / 16), output rows
@@ -367,7 +426,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) mxt_gate_up_kernel(MxtParams p)
 // j = expert j (further experts take further rounds), and sums the waves' weighted rows in a
 // fixed order in LDS (one writer per output, deterministic). Each wave turns its pair's h
 // into block-scaled terms while its tile streams in.
-template <int MM>
+template <int MM, bool CK>
 __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KP = 128 * MM;  // padded vector length
@@ -382,6 +441,8 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
     uint8_t* table = smem + 64 * WAVES + ASC_BYTES * wave;  // this wave's h A-scale table
     uint8_t* hs = smem + MISC_LDS + wave * 2 * KP;          // this wave's h terms [2][KP]
     uint8_t* zero = smem + MISC_LDS + WAVES * 2 * KP;
+    uint8_t* stash = zero + KP + wave * (CK_STAGE + 256 * Tile<MM>::MS) + CK_STAGE;  // checkpoint order
+    const int G = I / 32;
     const bool hbias = L.down_bias_off >= 0;
     const int rounds = (k + WAVES - 1) / WAVES;
 
@@ -413,13 +474,19 @@ __global__ void __launch_bounds__(256, 2) mxt_down_kernel(MxtParams p) {
         Tile<MM> tl;
         const int64_t brow = n0 + (lane & 15);
         const uint32_t bw = bias_word(base + (hbias ? L.down_bias_off : 0), L.bias_dtype, hbias ? (int64_t)H : 0, brow);
-        tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
-                      base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
+        u32x4 scr[2];
+        if constexpr (CK)
+            tile_load_ck<MM>(tl, scr, base + L.down_off + n0 * 16 * G, base + L.down_scales_off + n0 * G, G, lane);
+        else
+            tile_load<MM>(tl, base + L.down_off + (n0 / 16) * p.dn_tile, p.dn_tile,
+                          base + L.down_scales_off + (n0 / 16) * p.dn_stile, p.dn_stile, lane);
         // h as block-scaled terms while the tile streams in (the h loads are the oldest)
 #pragma unroll
         for (int i = 0; i < VCH; ++i) chunk_terms(hr[i], i, lane, hs, KP, table);
+        if constexpr (CK) tile_stash_ck<MM>(scr, stash - CK_STAGE, stash, G, lane);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's own terms and table are in LDS
-        const float a = tile_dot<MM>(tl, a_source(hs, zero, KP, lane), table, lane);
+        const float a = CK ? tile_dot<MM>(tl, a_source(hs, zero, KP, lane), table, lane, stash)
+                           : tile_dot<MM>(tl, a_source(hs, zero, KP, lane), table, lane);
         const float bias = bias_word_value(bw, L.bias_dtype, brow);  // 0 without a bias
         yv += w * (a + bias);
     }
@@ -802,9 +869,11 @@ __global__ void __launch_bounds__(64 * F_WAVES) __attribute__((amdgpu_waves_per_
 const void* kernel_for_mm(int MM, int which) {
 #define TSA_MXT_CASE(M)                                                                   \
     case M:                                                                               \
-        return which == 1 ? reinterpret_cast<const void*>(&mxt_down_kernel<M>)            \
+        return which == 1   ? reinterpret_cast<const void*>(&mxt_down_kernel<M, false>)   \
                : which == 2 ? reinterpret_cast<const void*>(&mxt_fused_kernel<M>)         \
-                           : reinterpret_cast<const void*>(&mxt_gate_up_kernel<M>);
+               : which == 3 ? reinterpret_cast<const void*>(&mxt_gate_up_kernel<M, true>) \
+               : which == 4 ? reinterpret_cast<const void*>(&mxt_down_kernel<M, true>)    \
+                            : reinterpret_cast<const void*>(&mxt_gate_up_kernel<M, false>);
     switch (MM) {
         TSA_MXT_CASE(4)
         TSA_MXT_CASE(8)
@@ -834,7 +903,8 @@ int64_t mxt_ws_bytes(const tsa_expert_layout& L, int64_t T, int k) {
     return h_bytes(L, T, k) + 2 * al256(T * k * 4);
 }
 
-// Requirements of the tiled path beyond validate_layout: "" if met.
+// Requirements of the MFMA decode beyond validate_layout, for tiled layouts and (the same
+// kernels loading lane by lane) checkpoint-order ones: "" if met.
 const char* mxt_unsupported(const tsa_expert_layout& L) {
     if (L.format != TSA_EXPERT_MXFP4 || L.act != TSA_ACT_SWIGLU_OAI) return "tiled layouts need MXFP4 experts with the SwiGLU-OAI activation";
     if (L.hidden % 32 || L.inter % 32) return "tiled layouts need hidden and inter to be multiples of 32";
@@ -860,8 +930,9 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     TSA_REQUIRE(L.hidden % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0, TSA_ERR_INVALID_ARG,
                 "tiled decode needs 16-byte aligned activations");
     const int ma = pick_mm(mx_tile_groups(L.hidden)), mb = pick_mm(mx_tile_groups(L.inter));
-    const void* ka = kernel_for_mm(ma, 0);
-    const void* kd = kernel_for_mm(mb, 1);
+    const bool ck = !L.mx_tiled;  // checkpoint order: the same kernels with lane-wise tile loads
+    const void* ka = kernel_for_mm(ma, ck ? 3 : 0);
+    const void* kd = kernel_for_mm(mb, ck ? 4 : 1);
     TSA_REQUIRE(ka && kd && L.hidden <= 3072 && L.inter <= 3072, TSA_ERR_SHAPE, "tiled decode: unsupported sizes");
 
     MxtParams p{};
@@ -897,7 +968,7 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
 
     void* args[] = {&p};
     const int64_t n_gu = T * k * (L.inter / 64), n_dn = T * (L.hidden / 16);
-    if (sync && mxt_form() == 0 && k <= WAVES && L.inter % 64 == 0 && n_gu <= MXT_SYNC_GFLAGS &&
+    if (!ck && sync && mxt_form() == 0 && k <= WAVES && L.inter % 64 == 0 && n_gu <= MXT_SYNC_GFLAGS &&
         n_dn <= MXT_SYNC_DFLAGS) {
         const int mm = ma > mb ? ma : mb;
         p.sync = reinterpret_cast<MxtSync*>(sync);
@@ -910,8 +981,10 @@ int mxt_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
                                       la > lb ? la : lb, st));
         return TSA_OK;
     }
-    const size_t lds_a = 3 * 128 * (size_t)ma + ASC_BYTES;
-    const size_t lds_b = MISC_LDS + (2 * WAVES + 1) * 128 * (size_t)mb;
+    const size_t ck_a = ck ? GU_WAVES * (CK_STAGE + 256 * (size_t)((ma + 3) / 4)) : 0;
+    const size_t ck_b = ck ? WAVES * (CK_STAGE + 256 * (size_t)((mb + 3) / 4)) : 0;
+    const size_t lds_a = 3 * 128 * (size_t)ma + ASC_BYTES + ck_a;
+    const size_t lds_b = MISC_LDS + (2 * WAVES + 1) * 128 * (size_t)mb + ck_b;
     TSA_HIP_CHECK(hipLaunchKernel(ka, dim3((unsigned)(T * k * (L.inter / (8 * GU_WAVES)))), dim3(64 * GU_WAVES), args,
                                   lds_a, st));
     TSA_HIP_CHECK(hipLaunchKernel(kd, dim3((unsigned)(T * (L.hidden / 16))), dim3(256), args, lds_b, st));
