@@ -199,6 +199,23 @@ def test_gguf_decode_more_assignments_than_grid_rows():
     assert_close_bf16(y, ref, "GGUF decode, T k = 65600")
 
 
+def test_gguf_routed_decode_more_assignments_than_grid_rows():
+    """The routed entry with T k above 65535: routed and decoded in token chunks."""
+    rng = np.random.default_rng(67)
+    H, I, E, k, T = 256, 256, 8, 8, 8200
+    L, experts, pool = _pool(rng, H, I, (8, 8, 8), E)
+    x_bits = synth.bf16_normal(rng, (T, H))
+    logits = synth.zipf_logits(rng, T, E)
+    y, gidx, gw = ops.moe_decode_routed(L, pool, torch.arange(E, dtype=torch.int32, device="cuda"),
+                                        torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k,
+                                        mode="softmax_then_topk", return_routing=True)
+    idx, w = oex.route_softmax_then_topk(logits, k)
+    assert np.array_equal(gidx.cpu().numpy(), idx)
+    ref = oex.moe_combine_grouped(synth.bf16_to_f32(x_bits), idx, w,
+                                  lambda e, xx: oex.gguf_expert_forward(xx, experts[e]))
+    assert_close_bf16(y, ref, "routed GGUF decode, T k = 65600")
+
+
 def test_ggml_expert_forward_other_activation():
     """GGMLExpertForward with a non-SiLU act_fn (here GELU) runs act_fn(gate) * up between the
     GGUF matvecs, as the reference passes any act_fn."""
