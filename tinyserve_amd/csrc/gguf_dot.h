@@ -3,9 +3,9 @@
 //
 // Loads: a wave copies the contiguous byte range of its rows' super-blocks into its LDS
 // area with coalesced 16-byte buffer-to-LDS loads (gq_stage_raw). Work unit: one lane then
-// owns a whole quantisation unit of the stream (Q4_K / Q5_K: a 256-value super-block, 144
-// / 176 bytes; Q6_K: half a super-block, 128 values: its 64 ql bytes, 32 qh bytes and 8
-// scales; Q8_0: a 32-value block, 34 bytes) and reads it from LDS with 16-byte reads at
+// owns a quantisation unit of the stream (Q4_K / Q5_K: half a super-block, 128 values: its
+// 64 qs bytes with the super-block's header (and Q5_K's 32 qh bytes); Q6_K: half a
+// super-block: its 64 ql bytes, 32 qh bytes and 8 scales; Q8_0: a 32-value block, 34 bytes) and reads it from LDS with 16-byte reads at
 // 2-byte alignment (which gfx950 serves). Rows may start inside a unit (the flat stream at
 // K = 2880), so results are attributed per 32-value sub-block to the unit's row or the
 // next one.
@@ -132,11 +132,15 @@ __device__ __forceinline__ float dot32x(const uint32_t q[8], const GqXr& r) {
     return dot16x<SPLIT>(q, r, 0) + dot16x<SPLIT>(q + 4, r, 1);
 }
 
+// Values per unit: a Q8_0 block, or half a K-quant super-block (128 values: a wave of 64
+// lanes then holds whole units of rows of 256 values or more at half the work per lane of
+// a whole super-block, so a wave's compute after its copies arrive is half as long).
+__host__ __device__ constexpr uint32_t gq_unit_values(int type) { return type == 8 ? 32u : 128u; }
 template <int TYPE> struct GqUnit;
 // values per unit, super-block (or block) bytes, units per super-block
 template <> struct GqUnit<8>  { static constexpr int V = 32,  SB = 34,  PER_SB = 1; };
-template <> struct GqUnit<12> { static constexpr int V = 256, SB = 144, PER_SB = 1; };
-template <> struct GqUnit<13> { static constexpr int V = 256, SB = 176, PER_SB = 1; };
+template <> struct GqUnit<12> { static constexpr int V = 128, SB = 144, PER_SB = 2; };
+template <> struct GqUnit<13> { static constexpr int V = 128, SB = 176, PER_SB = 2; };
 template <> struct GqUnit<14> { static constexpr int V = 128, SB = 210, PER_SB = 2; };
 
 __device__ __forceinline__ u32x4 ld16u(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -160,6 +164,15 @@ __device__ __forceinline__ void lds_words(const uint8_t* p, uint32_t (&w)[N]) {
 
 typedef int gq_v4i __attribute__((ext_vector_type(4)));
 
+// Buffer descriptor of (base, records) for the inline-assembly copies below, its words
+// taken from the first lane: the "s" operand must sit in scalar registers, which the
+// compiler only guarantees for values it can prove wave-uniform.
+__device__ __forceinline__ gq_v4i gq_rsrc(const uint8_t* base, uint32_t records) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return gq_v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+                  __builtin_amdgcn_readfirstlane((int)records), 0x00020000};
+}
+
 // Records of a buffer that starts mis bytes below n bytes of data: whole 16-byte chunks, so
 // the copy that holds the data's last bytes is not cut off by the range check (the rest of
 // that chunk lies on the same page).
@@ -174,8 +187,7 @@ __device__ __forceinline__ uint32_t gq_records(uint64_t n, uint32_t mis) {
 // wait for every load before any later LDS read); the caller waits with gq_wait_dma.
 __device__ __forceinline__ void gq_stage_raw(const uint8_t* base, uint32_t records, uint32_t a0, uint32_t n,
                                              uint32_t dst, int lane) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    const gq_v4i r = gq_v4i{(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)records, 0x00020000};
+    const gq_v4i r = gq_rsrc(base, records);
     for (uint32_t c = 0; c < n; c += 1024) {
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst + c);
         if (c + 16 * lane < n)
@@ -190,8 +202,7 @@ __device__ __forceinline__ void gq_stage_raw(const uint8_t* base, uint32_t recor
 // per instruction.
 __device__ __forceinline__ void gq_stage_vec_raw(const uint8_t* base, uint32_t records, uint32_t a0, uint32_t n,
                                                  uint32_t dst, int lane) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    const gq_v4i r = gq_v4i{(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)records, 0x00020000};
+    const gq_v4i r = gq_rsrc(base, records);
     for (uint32_t c = 0; c < n; c += 256) {
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst + c + 16 * (c >> 8));
         if (lane < 16 && c + 16 * lane < n)
@@ -243,69 +254,112 @@ __device__ __forceinline__ GqVec gq_vec(uint8_t* dst, int n, bool split = false)
     return vec;
 }
 
+// One 8-value chunk of a vector as loaded: bf16 / fp16 values in a, fp32 values 0..3 in a
+// and 4..7 in b.
+struct GqRaw {
+    u32x4 a, b;
+};
+
+// Chunk i of nv vectors of n values (cpv = n / 8 chunks each; vector jj from src (dtype) at
+// element off0 + jj * src_stride): its loads (16 bytes for bf16 / fp16, 32 for fp32; rows
+// 16-byte aligned, as the callers' are).
+__device__ __forceinline__ GqRaw gq_chunk_load(const void* src, int dtype, int64_t off0, int64_t src_stride, int cpv,
+                                               int i) {
+    const int jj = i / cpv, c = i - jj * cpv;
+    const int64_t e = off0 + jj * src_stride + 8 * (int64_t)c;  // first element of the chunk
+    GqRaw r;
+    if (dtype == TSA_F32) {
+        r.a = *reinterpret_cast<const u32x4*>(static_cast<const float*>(src) + e);
+        r.b = *reinterpret_cast<const u32x4*>(static_cast<const float*>(src) + e + 4);
+    } else {
+        r.a = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + e);
+        r.b = u32x4{0u, 0u, 0u, 0u};
+    }
+    return r;
+}
+
+// Chunk i (< cpv) of one vector of n values (cpv = n / 8), elements of es bytes (2 or 4) in
+// the buffer rsrc (the vector's bytes; chunks past it read zero): straight-line buffer
+// loads with no branch and no select on the loaded values, so that later loads issue
+// before these return.
+__device__ __forceinline__ GqRaw gq_chunk_load_buf(__amdgpu_buffer_rsrc_t rsrc, int es, int i) {
+    const uint32_t off = (uint32_t)(8 * es) * (uint32_t)i;
+    GqRaw r;
+    r.a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    r.b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, es == 4 ? off + 16 : 0x80000000u, 0, 0));
+    return r;
+}
+
+// Chunk i's values into the staged layout at dst0 + jj * dst_stride (as bf16, RNE; non-bf16
+// sources as the hi / lo pair, the layout gq_vec(.., n, true) describes) with its share of
+// the sums over every 32 and 16 consecutive positions, which come from neighbouring lanes
+// by DPP: every lane of the wave calls, chunks in lane order (lanes 4m .. 4m + 3 hold four
+// consecutive chunks of one vector, cpv % 4 == 0); invalid chunks (i past the last) write
+// nothing.
+__device__ __forceinline__ void gq_chunk_store(const GqRaw& r, bool valid, uint8_t* dst0, int dst_stride, int dtype,
+                                               int n, int cpv, int i) {
+    const bool split = dtype != TSA_BF16;
+    const int jj = valid ? i / cpv : 0, c = valid ? i - jj * cpv : 0;
+    uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+    float s8 = 0.0f;
+    if (valid) {
+        float f[8];
+        if (dtype == TSA_BF16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hw[q] = r.a[q];
+                s8 += bf16_bits_to_f32(r.a[q] & 0xFFFFu) + bf16_bits_to_f32(r.a[q] >> 16);
+            }
+        } else {
+            if (dtype == TSA_F32) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f[q] = __uint_as_float(r.a[q]);
+                    f[4 + q] = __uint_as_float(r.b[q]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f[2 * q] = f16_bits_to_f32(r.a[q] & 0xFFFFu);
+                    f[2 * q + 1] = f16_bits_to_f32(r.a[q] >> 16);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t h = f32_to_bf16_bits(f[q]);
+                const float hf = bf16_bits_to_f32(h);
+                const uint32_t l = f32_to_bf16_bits(f[q] - hf);
+                hw[q / 2] |= h << (16 * (q & 1));
+                lw[q / 2] |= l << (16 * (q & 1));
+                s8 += hf + bf16_bits_to_f32(l);  // hi + lo exactly: 16 significant bits
+            }
+        }
+    }
+    const float s16 = s8 + dpp_f<0xB1, 0xF, 0xF>(s8, 0.0f);    // quad_perm [1,0,3,2]
+    const float s32 = s16 + dpp_f<0x4E, 0xF, 0xF>(s16, 0.0f);  // quad_perm [2,3,0,1]
+    if (valid) {
+        uint8_t* dst = dst0 + jj * dst_stride;
+        const GqVec vec = gq_vec(dst, n, split);
+        *reinterpret_cast<u32x4*>(dst + gq_pad(8 * c)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        if (split)
+            *reinterpret_cast<u32x4*>(const_cast<uint8_t*>(vec.lo) + gq_pad(8 * c)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        if ((c & 1) == 0) const_cast<float*>(vec.s16)[c / 2] = s16;
+        if ((c & 3) == 0) const_cast<float*>(vec.s32)[c / 4] = s32;
+    }
+}
+
 // Stages nv vectors of n values (n % 32 == 0): vector jj from src (dtype) at element
-// off0 + jj * src_stride into LDS at dst0 + jj * dst_stride as bf16 (RNE; non-bf16 sources
-// as the hi / lo pair, the layout gq_vec(.., n, true) describes), with the sums over every
-// 32 and 16 consecutive positions. Threads tid of nthr (nthr a multiple of 64, whole waves
-// calling) take 8-value chunks in lane order, so each load instruction reads one
-// contiguous span (16 bytes per lane for bf16 / fp16, 32 for fp32; rows 16-byte aligned,
-// as the callers' are); the 16- and 32-value sums come from neighbouring lanes by DPP.
+// off0 + jj * src_stride into LDS at dst0 + jj * dst_stride (gq_chunk_store's layout).
+// Threads tid of nthr (nthr a multiple of 64, whole waves calling) take 8-value chunks in
+// lane order, so each load instruction reads one contiguous span.
 __device__ void gq_stage_vecs(uint8_t* dst0, int dst_stride, const void* src, int dtype, int64_t off0,
                               int64_t src_stride, int n, int nv, int tid, int nthr) {
-    const bool split = dtype != TSA_BF16;
     const int cpv = n / 8, total = cpv * nv;  // chunks per vector (a multiple of 4)
     for (int base = 0; base < total; base += nthr) {
         const int i = base + tid;
         const bool valid = i < total;
-        const int jj = valid ? i / cpv : 0, c = valid ? i - jj * cpv : 0;
-        const int64_t e = off0 + jj * src_stride + 8 * (int64_t)c;  // first element of the chunk
-        uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-        float s8 = 0.0f;
-        if (valid) {
-            float f[8];
-            if (dtype == TSA_BF16) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + e);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    hw[q] = v[q];
-                    s8 += bf16_bits_to_f32(v[q] & 0xFFFFu) + bf16_bits_to_f32(v[q] >> 16);
-                }
-            } else {
-                if (dtype == TSA_F32) {
-                    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + e);
-                    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + e + 4);
-                    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-                } else {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + e);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        f[2 * q] = f16_bits_to_f32(v[q] & 0xFFFFu);
-                        f[2 * q + 1] = f16_bits_to_f32(v[q] >> 16);
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const uint32_t h = f32_to_bf16_bits(f[q]);
-                    const float hf = bf16_bits_to_f32(h);
-                    const uint32_t l = f32_to_bf16_bits(f[q] - hf);
-                    hw[q / 2] |= h << (16 * (q & 1));
-                    lw[q / 2] |= l << (16 * (q & 1));
-                    s8 += hf + bf16_bits_to_f32(l);  // hi + lo exactly: 16 significant bits
-                }
-            }
-        }
-        // lanes 4m .. 4m + 3 hold chunks 4m' .. 4m' + 3 of one vector (cpv % 4 == 0)
-        const float s16 = s8 + dpp_f<0xB1, 0xF, 0xF>(s8, 0.0f);    // quad_perm [1,0,3,2]
-        const float s32 = s16 + dpp_f<0x4E, 0xF, 0xF>(s16, 0.0f);  // quad_perm [2,3,0,1]
-        if (valid) {
-            uint8_t* dst = dst0 + jj * dst_stride;
-            const GqVec vec = gq_vec(dst, n, split);
-            *reinterpret_cast<u32x4*>(dst + gq_pad(8 * c)) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-            if (split)
-                *reinterpret_cast<u32x4*>(const_cast<uint8_t*>(vec.lo) + gq_pad(8 * c)) = u32x4{lw[0], lw[1], lw[2], lw[3]};
-            if ((c & 1) == 0) const_cast<float*>(vec.s16)[c / 2] = s16;
-            if ((c & 3) == 0) const_cast<float*>(vec.s32)[c / 4] = s32;
-        }
+        const GqRaw r = valid ? gq_chunk_load(src, dtype, off0, src_stride, cpv, i) : GqRaw{};
+        gq_chunk_store(r, valid, dst0, dst_stride, dtype, n, cpv, i);
     }
 }
 __device__ void gq_stage(uint8_t* dst, const void* src, int dtype, int64_t off, int n, int tid, int nthr) {
@@ -424,38 +478,50 @@ __device__ __forceinline__ void gq_unit(const uint8_t* __restrict__ b, uint32_t 
         const float dl = d32(ql, kk) - 128.0f * sx, dh = d32(qh, kk) - 128.0f * sx;
         pa += d * (16.0f * dh + dl - 128.0f * sx);
     } else if constexpr (TYPE == 12 || TYPE == 13) {
+        // half hh of super-block u / 2: sub-blocks 4 hh .. 4 hh + 3, qs bytes [64 hh, + 64)
+        // (32 bytes per pair of sub-blocks, low nibbles then high), all 32 qh bytes (Q5_K:
+        // bit j of byte i is the fifth bit of value i of sub-block j), the 12 scale bytes
         constexpr int QS = TYPE == 12 ? 16 : 48;
+        const uint32_t hh = u & 1;
         const u32x4 hdr = ld16u(b);  // d, dmin | scales[12]
-        u32x4 qv[8];
+        u32x4 qv[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qv[i] = ld16u(b + QS + 16 * i);
+        for (int i = 0; i < 4; ++i) qv[i] = ld16u(b + QS + 64 * hh + 16 * i);
         u32x4 hv[2];
         if constexpr (TYPE == 13) {
             hv[0] = ld16u(b + 16);
             hv[1] = ld16u(b + 32);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) hv[i][e] >>= 4 * hh;  // bit jl: sub-block 4 hh + jl
         }
         const float d = f16_bits_to_f32(hdr[0] & 0xFFFFu), dmin = f16_bits_to_f32(hdr[0] >> 16);
-        const uint32_t s[3] = {hdr[1], hdr[2], hdr[3]};
         GqXr xr[2];
         ldx(0, xr[0]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (j + 1 < 8) ldx(j + 1, xr[(j + 1) & 1]);
+        for (int jl = 0; jl < 4; ++jl) {
+            if (jl + 1 < 4) ldx(jl + 1, xr[(jl + 1) & 1]);
             __builtin_amdgcn_sched_barrier(0);
-            if (outside(g0 + 32 * j)) continue;
-            uint32_t sc, m;
-            k_scale_min(s, j, sc, m);
+            if (outside(g0 + 32 * jl)) continue;
+            // the 6-bit scale and min of sub-block j = 4 hh + jl (ggml's get_scale_min_k4):
+            // j < 4 from bytes j, j + 4; j >= 4 from the low / high nibbles of byte j + 4 and
+            // the top two bits of bytes j - 4, j
+            const uint32_t b0 = (hdr[1] >> (8 * jl)) & 0xFFu, b1 = (hdr[2] >> (8 * jl)) & 0xFFu;
+            const uint32_t b2 = (hdr[3] >> (8 * jl)) & 0xFFu;
+            const uint32_t sc = hh ? ((b2 & 15u) | ((b0 >> 6) << 4)) : (b0 & 63u);
+            const uint32_t m = hh ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u);
             uint32_t q[8];
-            const int c = j >> 1, sh = 4 * (j & 1);
+            const int c = jl >> 1, sh = 4 * (jl & 1);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 uint32_t n = (qv[2 * c + (i >> 2)][i & 3] >> sh) & 0x0F0F0F0Fu;
-                if constexpr (TYPE == 13) n |= ((hv[i >> 2][i & 3] >> j) & 0x01010101u) << 4;
+                if constexpr (TYPE == 13) n |= ((hv[i >> 2][i & 3] >> jl) & 0x01010101u) << 4;
                 q[i] = n;
             }
-            const float sx = xr[j & 1].s[0];
-            const float dq = dot32x<SPLIT>(q, xr[j & 1]) - 128.0f * sx;
-            add(j, d * (float)sc * dq - dmin * (float)m * sx);
+            const float sx = xr[jl & 1].s[0];
+            const float dq = dot32x<SPLIT>(q, xr[jl & 1]) - 128.0f * sx;
+            add(jl, d * (float)sc * dq - dmin * (float)m * sx);
         }
     } else {  // Q6_K, half h of super-block u / 2: ql[64h, +64), qh[32h, +32), sc[8h, +8), d @208
         const uint32_t hh = u & 1;

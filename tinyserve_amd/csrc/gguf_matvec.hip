@@ -109,7 +109,7 @@ struct MvShape {
 // Rows per wave: the least gq_cost within the LDS budget (ties to more rows).
 MvShape mv_shape(int type, int64_t T, int64_t K, int64_t N, bool split, int cus) {
     const uint32_t sb = type == 8 ? 34u : type == 12 ? 144u : type == 13 ? 176u : 210u;
-    const uint32_t vs = type == 8 ? 32u : 256u, v = type == 8 ? 32u : type == 14 ? 128u : 256u;
+    const uint32_t vs = type == 8 ? 32u : 256u, v = gq_unit_values(type);
     const size_t vec = ((size_t)gq_vec_bytes((int)K, split) + 15) / 16 * 16;
     MvShape best;
     double best_cost = 0.0;

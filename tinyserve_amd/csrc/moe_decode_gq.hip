@@ -27,6 +27,7 @@ constexpr int GQ_RW = 4;         // phase A: intermediate rows per wave, at most
 constexpr int GQ_RB = 8;         // phase B: output rows per wave, at most
 constexpr int GQ_B_WAVES = 8;
 constexpr int GQ_MISC = 2048;    // slot / weight tables, per-(expert, row) partials
+constexpr int GQ_XC = 4;         // phase A: 8-value chunks of x per thread (hidden <= 8192)
 
 struct GqParams {
     tsa_expert_layout L;
@@ -57,43 +58,6 @@ struct GqParams {
 __device__ __forceinline__ float gq_act(const tsa_expert_layout& L, float gate, float up) {
     if (L.act == TSA_ACT_SWIGLU_OAI) return swiglu_oai(L, gate, up);
     return gate * sigmoidf_(gate) * up;
-}
-
-// Routing (wave 0) or the given slot table for token t into s_slot / s_w; expert j of the
-// token is at index gq_sel(p, t) + j (routing writes the whole [T, k] table, T <= 4). With
-// need >= 0 and no table to write, only selection `need` is made (need + 1 rounds), and
-// only its slot is written.
-__device__ __forceinline__ int gq_sel(const GqParams& p, int t) { return p.logits ? t * p.k : 0; }
-__device__ void gq_route(const GqParams& p, int t, bool write_out, int* s_slot, float* s_w, int need = -1) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    if (p.logits) {
-        if (tid < 64) {
-            int es[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
-            if (!write_out && need >= 0) {
-                float lg[4];
-                load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
-                uint32_t myk;
-                int mysel, myslot;
-                select_topk(p, lane, lg, es, need + 1, myk, mysel, myslot);
-                if (lane == need) s_slot[t * p.k + need] = myslot;
-                return;
-            }
-            const int sel = route_token(p, t, lane, es, s_slot, s_w);
-            if (write_out && lane < p.k) {
-                if (p.idx_out) {
-                    p.idx_out[t * p.k + lane] = sel;
-                    p.w_out[t * p.k + lane] = s_w[t * p.k + lane];
-                }
-                p.tab_slot[t * p.k + lane] = s_slot[t * p.k + lane];  // written by this lane
-                p.tab_w[t * p.k + lane] = s_w[t * p.k + lane];
-            }
-        }
-    } else if (tid < p.k) {
-        s_slot[tid] = p.slots[(int64_t)t * p.k + tid];
-        s_w[tid] = p.wts[(int64_t)t * p.k + tid];
-    }
 }
 
 // Phase A units of one wave: lane i takes units i, i + 64, ... of gate (i < nu) then up.
@@ -140,32 +104,78 @@ __device__ __forceinline__ void gq_b_units(const uint8_t* rbuf, uint32_t shift, 
     }
 }
 
-template <int TG>
+// SPLIT: x is fp32 / fp16, staged as a bf16 hi / lo pair (its own instantiation: the pair's
+// registers would otherwise set the bf16 kernel's register budget, and so its occupancy).
+template <int TG, bool SPLIT>
 __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
-    const int a = blockIdx.y, t = a / k;
+    const int a = blockIdx.y, t = a / k, jj = a % k;
     int* s_slot = reinterpret_cast<int*>(smem);
     float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
-    const bool split = p.x_dtype != TSA_BF16;
+    constexpr bool split = SPLIT;  // p.x_dtype != TSA_BF16
     const GqVec xv = gq_vec(smem + GQ_MISC, H, split);
-    gq_route(p, t, blockIdx.x == 0 && a % k == 0, s_slot, s_w, a % k);
-    if (!p.logits) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid, 256);
-    else if (tid >= 64) gq_stage(smem + GQ_MISC, p.x, p.x_dtype, (int64_t)t * H, H, tid - 64, 192);
-    __syncthreads();
-    const int64_t slot = uniform(s_slot[gq_sel(p, t) + a % k]);
+
+    // ---- loads, all issued before any is used: this thread's chunks of x (thread order,
+    // zero past the vector), then the routing inputs (or the pair's slot as a scalar load)
+    const int xes = p.x_dtype == TSA_F32 ? 4 : 2, cpv = H / 8;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(p.x) + (int64_t)t * H * xes), (short)0, H * xes, 0x00020000);
+    GqRaw xr[GQ_XC];
+#pragma unroll
+    for (int c = 0; c < GQ_XC; ++c) xr[c] = gq_chunk_load_buf(rx, xes, tid + 256 * c);
+    const bool routed = p.logits != nullptr;
+    float lg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int es[4] = {0, 0, 0, 0};
+    int64_t slot = -1;
+    if (routed) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) es[j] = p.expert_slot[min(lane + 64 * j, p.E - 1)];
+        load4(p.logits, p.logits_dtype, (int64_t)t * p.E, p.E, lane, lg);
+    } else {
+        slot = uniform(p.slots[(int64_t)t * k + jj]);
+    }
+    // ---- every wave selects the pair's expert itself (round jj of the top-k); wave 0 of the
+    // token's first workgroup makes all k selections and writes the table for phase B
+    if (routed) {
+        if (blockIdx.x == 0 && jj == 0 && wave == 0) {
+            const int sel = route_token_v(p, t, lane, lg, es, s_slot, s_w);
+            if (lane < k) {
+                if (p.idx_out) {
+                    p.idx_out[t * k + lane] = sel;
+                    p.w_out[t * k + lane] = s_w[t * k + lane];
+                }
+                p.tab_slot[t * k + lane] = s_slot[t * k + lane];  // written by this lane
+                p.tab_w[t * k + lane] = s_w[t * k + lane];
+            }
+            slot = uniform(s_slot[t * k]);  // lane 0's own write
+        } else {
+            uint32_t myk;
+            int mysel, myslot;
+            select_topk(p, lane, lg, es, jj + 1, myk, mysel, myslot);
+            slot = __builtin_amdgcn_readlane(myslot, jj);
+        }
+    }
+    // every wave of the workgroup made the same selection: all return here or none
     if (slot < 0 || slot >= p.n_slots) return;  // a dead pair's h is never read
+    // ---- x into LDS (every wave its chunks), then the super-block copies
+#pragma unroll
+    for (int c = 0; c < GQ_XC; ++c) {
+        if (256 * c >= cpv) break;
+        const int i = tid + 256 * c;
+        gq_chunk_store(xr[c], i < cpv, smem + GQ_MISC, 0, p.x_dtype, H, cpv, i);
+    }
     const int n0 = ((int)blockIdx.x * 4 + wave) * p.rw;
-    if (n0 >= I) return;
+    const bool has_rows = n0 < I;
     const int n1 = n0 + p.rw < I ? n0 + p.rw : I;
     const uint8_t* base = p.pool + slot * L.slot_bytes;
     using U = GqUnit<TG>;
     constexpr uint32_t VS = TG == 8 ? 32 : 256, SB = U::SB;
-    const uint32_t lo = (uint32_t)n0 * H, hi = (uint32_t)n1 * H;
+    const uint32_t lo = (uint32_t)n0 * H, hi = (uint32_t)(has_rows ? n1 : n0) * H;
     const uint32_t u0 = lo / U::V, nu = (hi + U::V - 1) / U::V - u0;
-    // stage the super-blocks of rows [n0, n1) of gate and up into this wave's LDS area
+    // the super-blocks of rows [n0, n1) of gate and up into this wave's LDS area
     const uint32_t s0 = lo / VS, nsb = gq_sb_count<TG>(lo, hi);
     const uint32_t raw = gq_raw_bytes(nsb, SB);
     uint8_t* rbuf = smem + p.raw_off_a + wave * p.raw_stride_a;
@@ -177,9 +187,13 @@ __global__ void __launch_bounds__(256) gq_phase_a(GqParams p) {
     for (int m = 0; m < 2; ++m) {
         const uint32_t first = mis + (uint32_t)(m ? L.up_off : L.gate_off) + s0 * SB;  // byte in the buffer
         shift[m] = first & 15u;
-        gq_stage_raw(base - mis, gq_records((uint64_t)L.slot_bytes, mis), first - shift[m], raw, lds_r + m * raw, lane);
+        if (has_rows)
+            gq_stage_raw(base - mis, gq_records((uint64_t)L.slot_bytes, mis), first - shift[m], raw, lds_r + m * raw,
+                         lane);
     }
     gq_wait_dma();
+    __syncthreads();  // x complete (every wave's chunks)
+    if (!has_rows) return;
     float acc[2][GQ_RW];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
@@ -211,13 +225,9 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
     const tsa_expert_layout& L = p.L;
     const int H = (int)L.hidden, I = (int)L.inter, k = p.k;
     const int t = blockIdx.y;
-    int* s_slot = reinterpret_cast<int*>(smem);
-    float* s_w = reinterpret_cast<float*>(smem + 4 * FUSED_MAXT * FUSED_MAXK);
     float* s_part = reinterpret_cast<float*>(smem + 8 * FUSED_MAXT * FUSED_MAXK);  // [8 waves][GQ_RB]
     uint8_t* hbuf = smem + GQ_MISC + (wave % (k < GQ_B_WAVES ? k : GQ_B_WAVES)) * p.vec_stride_b;  // this wave's expert
-    gq_route(p, t, false, s_slot, s_w);
-    for (int i = tid; i < GQ_B_WAVES * GQ_RB; i += blockDim.x) s_part[i] = 0.0f;
-    __syncthreads();
+    for (int i = tid; i < GQ_B_WAVES * GQ_RB; i += blockDim.x) s_part[i] = 0.0f;  // ordered by the rounds' barriers
 
     const int kk = k < GQ_B_WAVES ? k : GQ_B_WAVES;          // experts per round
     const int S = GQ_B_WAVES / kk;                            // row slices
@@ -239,7 +249,10 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
     const uint32_t lds_r = (uint32_t)reinterpret_cast<uintptr_t>(rbuf);
     for (int j0 = 0; j0 < k; j0 += kk) {  // rounds of kk experts (workgroup-uniform)
         const int j = j0 + jw, nj = k - j0 < kk ? k - j0 : kk;
-        const int64_t slot = j < k ? uniform(s_slot[gq_sel(p, t) + j]) : -1;
+        // the wave's expert as scalar loads of the [T, k] table (phase A's routed one or the
+        // caller's), ahead of every vector load
+        const int64_t slot = j < k ? uniform(p.slots[(int64_t)t * k + j]) : -1;
+        const float wj = j < k ? __int_as_float(uniform(__float_as_int(p.wts[(int64_t)t * k + j]))) : 0.0f;
         const bool live = mine && j < k && slot >= 0 && slot < p.n_slots;
         const uint8_t* sbase = p.pool + (live ? slot : 0) * L.slot_bytes;
         const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(sbase) & 15u;  // as in phase A
@@ -252,7 +265,6 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
         gq_wait_dma();
         __syncthreads();
         if (live) {
-            const float wj = s_w[gq_sel(p, t) + j];
             const GqVec hv = gq_vec(hbuf, I);
             if (I % U::V == 0)
                 gq_b_units<TD, false>(rbuf, shift, s0, u0, nu, n0, I, lo, hi, hv, wj, lane, acc);
@@ -274,16 +286,18 @@ __global__ void __launch_bounds__(64 * GQ_B_WAVES) gq_phase_b(GqParams p) {
 }
 
 template <int TG>
-const void* phase_a_fn() { return reinterpret_cast<const void*>(&gq_phase_a<TG>); }
+const void* phase_a_fn(bool split) {
+    return split ? reinterpret_cast<const void*>(&gq_phase_a<TG, true>) : reinterpret_cast<const void*>(&gq_phase_a<TG, false>);
+}
 template <int TD>
 const void* phase_b_fn() { return reinterpret_cast<const void*>(&gq_phase_b<TD>); }
 
-const void* pick_a(int t) {
+const void* pick_a(int t, bool split = false) {
     switch (t) {
-        case 8: return phase_a_fn<8>();
-        case 12: return phase_a_fn<12>();
-        case 13: return phase_a_fn<13>();
-        case 14: return phase_a_fn<14>();
+        case 8: return phase_a_fn<8>(split);
+        case 12: return phase_a_fn<12>(split);
+        case 13: return phase_a_fn<13>(split);
+        case 14: return phase_a_fn<14>(split);
     }
     return nullptr;
 }
@@ -362,7 +376,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     const int ta = L.gate_type, tb = L.down_type;
     auto sb_bytes = [](int t) { return t == 8 ? 34u : t == 12 ? 144u : t == 13 ? 176u : 210u; };
     auto vs = [](int t) { return t == 8 ? 32u : 256u; };
-    auto uv = [](int t) { return t == 8 ? 32u : t == 14 ? 128u : 256u; };
+    auto uv = [](int t) { return gq_unit_values(t); };
     const int cus = num_cus();
     const size_t vecA = ((size_t)gq_vec_bytes((int)L.hidden, x_dtype != TSA_BF16) + 15) / 16 * 16;
     const size_t vecB = ((size_t)gq_vec_bytes((int)L.inter) + 15) / 16 * 16;
@@ -394,7 +408,7 @@ int gq_decode(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots, 
     const size_t lds_b = GQ_MISC + GQ_B_WAVES * (vecB + rawB);
     TSA_REQUIRE(lds_a <= 160 * 1024 && lds_b <= 160 * 1024, TSA_ERR_SHAPE, "GGUF decode: LDS %zu / %zu bytes", lds_a,
                 lds_b);
-    const void* fa = pick_a(L.gate_type);
+    const void* fa = pick_a(L.gate_type, x_dtype != TSA_BF16);
     const void* fb = pick_b(L.down_type);
     TSA_HIP_CHECK(ensure_dynamic_lds(fb, (int)lds_b));
     TSA_HIP_CHECK(ensure_dynamic_lds(fa, (int)lds_a));

@@ -114,7 +114,9 @@ __device__ __forceinline__ void gf_dma(const v4i_t& r, uint32_t voff, uint32_t l
 __device__ __forceinline__ v4i_t gf_desc(const uint8_t* p, int64_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
     const uint32_t n = bytes < 0xFFFFFFF0ll ? (uint32_t)bytes : 0xFFFFFFF0u;
-    return v4i_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)n, 0x00020000};
+    // words from the first lane: gf_dma's "s" operand must sit in scalar registers
+    return v4i_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+                 __builtin_amdgcn_readfirstlane((int)n), 0x00020000};
 }
 
 // Byte offset in its matrix of raw group q of weight row `row` (K = 32 KU values per row):

@@ -100,10 +100,13 @@ struct PfGemm {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// Raw buffer descriptor (base, num_records bytes; loads past the end return zero).
+// Raw buffer descriptor (base, num_records bytes; loads past the end return zero), its
+// words from the first lane: the copies' "s" operand must sit in scalar registers, which
+// the compiler only guarantees for values it can prove wave-uniform.
 __device__ __forceinline__ v4i buf_desc(const void* p, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
-    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+    return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+               __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
 }
 
 // 16 (or 4) bytes per lane from buffer offset voff straight into LDS at lds + 16 lane (or
