@@ -54,6 +54,36 @@ def test_gguf_decode_routed_vs_oracle(H, I, types, E, k, T, mode):
     assert_close_bf16(y, _ref(experts, synth.bf16_to_f32(x_bits), ridx, rw), f"routed gguf {types} k={k} T={T} {mode}")
 
 
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+@pytest.mark.parametrize("E,k", [(32, 4), (128, 8), (200, 16)])
+def test_gguf_decode_routing_ties_and_nan(E, k):
+    """Every phase A wave selects its own pair's expert (the rank alone, by a threshold
+    search) while one wave per token writes the whole top-k table for phase B: both must
+    rank NaN first, then descending logits, ties to the lower id (torch.topk's order), or
+    a pair's h would belong to another expert than its weight. Rows: integer logits with
+    many ties, all-equal logits, NaN and +inf (weights NaN, as torch's softmax gives), and
+    a plain row; the outputs of the rows without NaN or inf are checked against the oracle."""
+    rng = np.random.default_rng(E + k)
+    H, I, T = 256, 256, 4
+    L, experts, pool = _pool(rng, H, I, (13, 13, 14), 6)
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    logits[0] = rng.integers(-2, 3, size=E).astype(np.float32)
+    logits[1] = 0.0
+    logits[2, 3] = np.nan
+    logits[2, E - 1] = np.nan
+    logits[2, 5] = np.inf
+    ridx, rw = oex.route_topk_then_softmax(logits, k)
+    es = torch.arange(E, dtype=torch.int32, device="cuda") % 6
+    x_bits = synth.bf16_normal(rng, (T, H))
+    y, idx, w = ops.moe_decode_routed(L, pool, es, torch.from_numpy(logits).cuda(), bf16_dev(x_bits), k,
+                                      return_routing=True)
+    assert np.array_equal(idx.cpu().numpy(), ridx), "routing indices"
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, equal_nan=True)
+    ok = [0, 1, 3]
+    ref = _ref([experts[e % 6] for e in range(E)], synth.bf16_to_f32(x_bits)[ok], ridx[ok], rw[ok])
+    assert_close_bf16(y[ok], ref, f"gguf decode, ties and NaN, E={E} k={k}")
+
+
 def test_gguf_decode_routed_repeats_and_missing_expert():
     """Repeated routed calls on one workspace agree; an expert without a resident slot
     contributes nothing (its weight stays in the normalisation, as in the reference)."""
