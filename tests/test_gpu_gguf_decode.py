@@ -144,6 +144,29 @@ def test_gguf_decode_one_expert_stream_kernels(types, H, I, T, x_dtype, pad):
         assert_close_bf16(y2, _ref(experts, xf, eidx, ew), f"one-expert routed decode {types}")
 
 
+@pytest.mark.parametrize("H,I,types,x_dtype", [
+    (2880, 2880, (13, 13, 14), torch.bfloat16),  # rows start inside units in both launches
+    (2880, 2880, (12, 12, 14), torch.float32),   # the same through the hi / lo activation kernels
+    (288, 96, (13, 13, 14), torch.bfloat16),     # rows of 2.25 / 0.75 half super-blocks
+    (96, 288, (12, 12, 14), torch.float16),
+    (320, 2880, (14, 14, 12), torch.bfloat16),   # Q6_K gate / up, Q4_K down
+])
+def test_gguf_decode_rows_straddling_units(H, I, types, x_dtype):
+    """Several experts per token (the super-block kernels, half a K-quant super-block per
+    lane) at row lengths that are not multiples of 128 values, so rows start inside units
+    and a unit's sub-blocks go to two rows: against the fp32 oracle."""
+    rng = np.random.default_rng(H + 3 * I + sum(types))
+    E, k, T = 4, 3, 2
+    L, experts, pool = _pool(rng, H, I, types, E)
+    x = rng.normal(0.0, 1.0, (T, H)).astype(np.float32)
+    xt = torch.from_numpy(x).to(x_dtype)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.2, 1.0, size=(T, k)).astype(np.float32)
+    y = ops.moe_decode(L, pool, torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), xt.cuda(),
+                       out_dtype=torch.float32)
+    assert_close_bf16(y, _ref(experts, xt.float().numpy(), idx, w), f"gguf decode {types} H {H} I {I} {x_dtype}")
+
+
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.float16])
 def test_gguf_decode_wide_activations(x_dtype):
     """fp32 / fp16 activations are staged as a bf16 hi/lo pair: the result follows the fp32
