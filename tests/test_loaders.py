@@ -219,6 +219,56 @@ def test_safetensors_store_without_experts(tmp_path):
         ExpertStore.from_safetensors(str(tmp_path))
 
 
+def test_gguf_hf_name_convention():
+    """GGUF <-> Hugging Face names as the reference's loader maps them
+    (gguf_loader.py:121-229): per-expert FFN tensors, model-level and per-layer tensors,
+    both directions, and unknown names passed through unchanged."""
+    from tinyserve_amd.gguf_store import gguf_to_hf_name, hf_to_gguf_name
+
+    known = {
+        "token_embd.weight": ("model.embed_tokens.weight", False, None, None),
+        "output_norm.weight": ("model.norm.weight", False, None, None),
+        "output.weight": ("lm_head.weight", False, None, None),
+        "blk.0.attn_q.weight": ("model.layers.0.self_attn.q_proj.weight", False, 0, None),
+        "blk.11.attn_output.bias": ("model.layers.11.self_attn.o_proj.bias", False, 11, None),
+        "blk.3.attn_k_norm.weight": ("model.layers.3.self_attn.k_norm.weight", False, 3, None),
+        "blk.5.ffn_norm.weight": ("model.layers.5.post_attention_layernorm.weight", False, 5, None),
+        "blk.5.ffn_gate_inp.weight": ("model.layers.5.mlp.gate.weight", False, 5, None),
+        "blk.2.ffn_up_exps.weight": ("model.layers.2.mlp.shared_expert.up_proj.weight", False, 2, None),
+        "blk.2.ffn_gate_up_exps.weight": ("model.layers.2.mlp.shared_expert.gate_up_proj.weight", False, 2, None),
+        "blk.7.ffn_down.127.weight": ("model.layers.7.mlp.experts.127.down_proj.weight", True, 7, 127),
+        "blk.0.ffn_gate.0.weight": ("model.layers.0.mlp.experts.0.gate_proj.weight", True, 0, 0),
+    }
+    for g, want in known.items():
+        assert gguf_to_hf_name(g) == want, g
+        assert hf_to_gguf_name(want[0]) == g, g
+    for odd in ("blk.x.attn_q.weight", "blk.1.attn_qkv.weight", "blk.1.ffn_gate.x.weight", "rope_freqs.weight",
+                "blk.1.ffn_gate.3.bias"):
+        assert gguf_to_hf_name(odd) == (odd, False, None, None), odd
+    for odd in ("model.layers.1.unknown.weight", "model.layers.x.self_attn.q_proj.weight", "something"):
+        assert hf_to_gguf_name(odd) == odd
+
+
+def test_gguf_linear_weights_default_names(tmp_path):
+    """Without a name map, gguf_linear_weights names the quantised non-expert linears by the
+    GGUF -> Hugging Face convention and leaves per-expert tensors, norms and F32 tensors out."""
+    from tinyserve_amd.gguf_store import gguf_linear_weights
+
+    rng = np.random.default_rng(9)
+    q = synth.make_gguf(rng, 13, 256 * 64)
+    tensors = [("blk.1.attn_v.weight", (256, 64), 13, q),
+               ("blk.1.ffn_up.0.weight", (256, 64), 13, q),
+               ("blk.1.attn_norm.weight", (256,), 0, np.ones(256, np.float32)),
+               ("output.weight", (256, 64), 13, q),
+               ("blk.1.mystery.weight", (256, 64), 13, q)]
+    p = tmp_path / "names.gguf"
+    write_gguf(p, tensors)
+    with gr.GGUFReader(p) as r:
+        lw = gguf_linear_weights(r)
+    assert sorted(lw) == ["lm_head", "model.layers.1.self_attn.v_proj"]
+    assert lw["lm_head"][1:] == (13, (64, 256))
+
+
 def test_gguf_linear_weights_selection(tmp_path):
     """Quantised 2-D .weight tensors named by the map become replace_linear_with_ggml input
     ((out, in) from ne = [in, out]); norms, embeddings' F32 and unmapped names are left out."""

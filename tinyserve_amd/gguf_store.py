@@ -13,6 +13,11 @@ ggml types are in ``layer_ggml_types``).
 What this build adds: ``load_layer`` copies a whole layer's experts into one device pool
 (all experts resident, as the 288 GB of one GPU allows) and ``expert_layout`` gives the
 matching ``tsa_expert_layout`` for that layer.
+
+Non-expert weights: ``gguf_linear_weights`` selects the native-quantised linears for
+``replace_linear_with_ggml``, named by ``gguf_to_hf_name`` / ``hf_to_gguf_name`` (the
+GGUF <-> Hugging Face convention of tinyserve/gguf_loader.py:121-229) unless the caller
+gives its own map.
 """
 from __future__ import annotations
 
@@ -165,16 +170,104 @@ class MmapExpertStore:
         self._reader.close()
 
 
+# GGUF <-> Hugging Face parameter names (the naming convention the reference's loader
+# applies, tinyserve/gguf_loader.py:121-229): three model-level tensors, per-layer suffixes
+# under blk.<L>. <-> model.layers.<L>., and per-expert FFN tensors blk.<L>.ffn_<p>.<E>.weight
+# <-> model.layers.<L>.mlp.experts.<E>.<p>_proj.weight. The pairs are the convention itself,
+# so they are listed as the reference lists them.
+_GLOBAL_NAMES = (
+    ("token_embd.weight", "model.embed_tokens.weight"),
+    ("output_norm.weight", "model.norm.weight"),
+    ("output.weight", "lm_head.weight"),
+)
+_LAYER_NAMES = (
+    ("attn_q.weight", "self_attn.q_proj.weight"),
+    ("attn_k.weight", "self_attn.k_proj.weight"),
+    ("attn_v.weight", "self_attn.v_proj.weight"),
+    ("attn_output.weight", "self_attn.o_proj.weight"),
+    ("attn_norm.weight", "input_layernorm.weight"),
+    ("attn_q_norm.weight", "self_attn.q_norm.weight"),
+    ("attn_k_norm.weight", "self_attn.k_norm.weight"),
+    ("ffn_norm.weight", "post_attention_layernorm.weight"),
+    ("ffn_gate_inp.weight", "mlp.gate.weight"),
+    ("ffn_gate_exps.weight", "mlp.shared_expert.gate_proj.weight"),
+    ("ffn_up_exps.weight", "mlp.shared_expert.up_proj.weight"),
+    ("ffn_down_exps.weight", "mlp.shared_expert.down_proj.weight"),
+    ("ffn_gate_up_exps.weight", "mlp.shared_expert.gate_up_proj.weight"),
+    ("attn_q.bias", "self_attn.q_proj.bias"),
+    ("attn_k.bias", "self_attn.k_proj.bias"),
+    ("attn_v.bias", "self_attn.v_proj.bias"),
+    ("attn_output.bias", "self_attn.o_proj.bias"),
+)
+_G2H_GLOBAL, _H2G_GLOBAL = dict(_GLOBAL_NAMES), {h: g for g, h in _GLOBAL_NAMES}
+_G2H_LAYER, _H2G_LAYER = dict(_LAYER_NAMES), {h: g for g, h in _LAYER_NAMES}
+
+
+def _split_layer(name: str, prefix: str) -> tuple[int, str] | None:
+    """``<prefix><L>.<rest>`` -> (L, rest), else None."""
+    if not name.startswith(prefix):
+        return None
+    head, dot, rest = name[len(prefix):].partition(".")
+    return (int(head), rest) if dot and head.isascii() and head.isdigit() else None
+
+
+def gguf_to_hf_name(gguf_name: str) -> tuple[str, bool, int | None, int | None]:
+    """(hf_name, is_expert, layer, expert) for a GGUF tensor name, as the reference's
+    ``gguf_to_hf_name`` (tinyserve/gguf_loader.py:163-195): a per-expert FFN tensor maps
+    to ``model.layers.<L>.mlp.experts.<E>.<p>_proj.weight`` with is_expert True; a
+    model-level or known per-layer tensor to its Hugging Face name; anything else comes
+    back unchanged (layer None)."""
+    parsed = _split_layer(gguf_name, "blk.")
+    if parsed is not None:
+        layer, rest = parsed
+        parts = rest.split(".")
+        if (len(parts) == 3 and parts[2] == "weight" and parts[1].isdigit()
+                and parts[0] in ("ffn_gate", "ffn_up", "ffn_down")):
+            proj, expert = parts[0][4:], int(parts[1])
+            return f"model.layers.{layer}.mlp.experts.{expert}.{proj}_proj.weight", True, layer, expert
+    if gguf_name in _G2H_GLOBAL:
+        return _G2H_GLOBAL[gguf_name], False, None, None
+    if parsed is not None and parsed[1] in _G2H_LAYER:
+        return f"model.layers.{parsed[0]}.{_G2H_LAYER[parsed[1]]}", False, parsed[0], None
+    return gguf_name, False, None, None
+
+
+def hf_to_gguf_name(hf_name: str) -> str:
+    """The inverse (tinyserve/gguf_loader.py:198-229); unknown names come back unchanged."""
+    if hf_name in _H2G_GLOBAL:
+        return _H2G_GLOBAL[hf_name]
+    parsed = _split_layer(hf_name, "model.layers.")
+    if parsed is None:
+        return hf_name
+    layer, rest = parsed
+    parts = rest.split(".")
+    if (len(parts) == 5 and parts[:2] == ["mlp", "experts"] and parts[2].isdigit() and parts[4] == "weight"
+            and parts[3] in ("gate_proj", "up_proj", "down_proj")):
+        return f"blk.{layer}.ffn_{parts[3][:-5]}.{parts[2]}.weight"
+    if rest in _H2G_LAYER:
+        return f"blk.{layer}.{_H2G_LAYER[rest]}"
+    return hf_name
+
+
+def _default_linear_name(gguf_name: str) -> str | None:
+    """A non-expert tensor's Hugging Face name, or None for expert and unknown tensors."""
+    hf, is_expert, _, _ = gguf_to_hf_name(gguf_name)
+    return None if is_expert or hf == gguf_name else hf
+
+
 _QUANT_TYPES = (2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 15)
 
 
-def gguf_linear_weights(reader: GGUFReader, name_map) -> dict[str, tuple[torch.Tensor, int, tuple[int, int]]]:
+def gguf_linear_weights(reader: GGUFReader, name_map=None) -> dict[str, tuple[torch.Tensor, int, tuple[int, int]]]:
     """Native-quantised 2-D ``.weight`` tensors of a GGUF file as ``replace_linear_with_ggml``
     input: module path -> (raw bytes, ggml type, (out_features, in_features)), the selection
     the reference's loader makes for non-expert linears (tinyserve/gguf_loader.py:610-623:
     GGUF ne = [in, out]). ``name_map`` maps GGUF tensor names to model parameter names (a
-    dict, or a callable returning None to skip); only types ``GGMLLinear`` can run are kept
-    (the row kernels serve Q8_0 / Q4_K / Q5_K / Q6_K)."""
+    dict, or a callable returning None to skip; by default the generic convention of
+    ``gguf_to_hf_name`` without the expert tensors); only types ``GGMLLinear`` can run are
+    kept (the row kernels serve Q8_0 / Q4_K / Q5_K / Q6_K)."""
+    if name_map is None:
+        name_map = _default_linear_name
     from .ops import gguf_block_info
 
     out: dict[str, tuple[torch.Tensor, int, tuple[int, int]]] = {}
