@@ -94,7 +94,8 @@ def _pmc_rows(d: str, counter: str) -> list[tuple[str, float]]:
 STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_kernel"),
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mxt_gate_up_kernel", "mxt_down_kernel"),
                 "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_mfma_kernel",),
-                "8": ("router_logits_decode_kernel", "mxt_gate_up_kernel", "mxt_down_kernel")}
+                "8": ("router_logits_decode_kernel", "mxt_gate_up_kernel", "mxt_down_kernel"),
+                "5": ("pf_gemm_kernel",), "6": ("gf_gemm_kernel",)}
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str, key: str, command: str) -> dict:
@@ -319,6 +320,12 @@ class MxMatvecWorkload:
                                         self.N, self.K, st))
 
 
+def _routed_experts(logits: torch.Tensor, k: int) -> int:
+    """Distinct experts in the top-k of every token (the selection is by logit in every
+    routing mode)."""
+    return int(torch.unique(torch.topk(logits.float().cpu(), k, dim=-1).indices).numel())
+
+
 class PrefillWorkload:
     """Workload 5: resident tiled MXFP4 layers, router logits and activations of a
     2048-token prefill; one step = one layer's whole batched MoE."""
@@ -328,6 +335,7 @@ class PrefillWorkload:
         self.H, self.I, self.E, self.k = base["hidden"], base["inter"], base["E"], base["top_k"]
         lay = synth.mxfp4_tiled_layout(self.H, self.I)
         self.L = mxfp4_expert_layout(lay, tiled=True, prefill_mfma=prefill_mfma)
+        self.slot_bytes = lay.total_bytes
         pool0 = np.stack([synth.pack_mxfp4_expert_tiled(e, lay) for e in base["experts"]])
         g = torch.Generator(device=dev)
         g.manual_seed(20261205)
@@ -349,6 +357,10 @@ class PrefillWorkload:
     def flops_per_step(self) -> int:
         """2 x (gate_up 2I x H + down H x I) multiply-adds per (token, expert) assignment."""
         return 2 * self.T * self.k * (2 * self.I * self.H + self.H * self.I)
+
+    def min_bytes_per_step(self) -> int:
+        """HBM bytes the step cannot avoid: every routed expert's slot once, x in, y out."""
+        return _routed_experts(self.logits, self.k) * self.slot_bytes + 2 * self.T * self.H * 2
 
     def step(self, s: int) -> None:
         lib = _lib.load()
@@ -390,6 +402,7 @@ class GgufPrefillWorkload:
             logits, x_bits = synth.zipf_logits(rng, T, self.E), synth.bf16_normal(rng, (T, self.H))
         self.L = gguf_expert_layout(lay, dict(zip(("gate", "up", "down"), self.types)),
                                     {"gate": (self.H, self.I), "up": (self.H, self.I), "down": (self.I, self.H)})
+        self.slot_bytes = lay.total_bytes
         while len(self.pools) < n_layers:  # further layers: random codes, super-block scales in range
             p = torch.randint(0, 256, (self.E, lay.total_bytes), dtype=torch.uint8, device=dev, generator=g)
             MoEWorkload._fix_scales(p, lay, g, self.types)
@@ -406,6 +419,9 @@ class GgufPrefillWorkload:
 
     def flops_per_step(self) -> int:
         return 2 * self.T * self.k * (2 * self.I * self.H + self.H * self.I)
+
+    def min_bytes_per_step(self) -> int:
+        return _routed_experts(self.logits, self.k) * self.slot_bytes + 2 * self.T * self.H * 2
 
     def step(self, s: int) -> None:
         lib = _lib.load()
@@ -477,6 +493,14 @@ def run_prefill(args, dev) -> int:
                                          "multiply-add (hi and lo activation terms)" if fp6 else
                                          "peak = dense bf16 MFMA")},
     }
+    tr = load_traffic(str(args.workload)) if not (gguf and args.gguf_shape == "2880") and (gguf or fp6) else None
+    if tr:
+        line["roofline"]["traffic"] = round(tr["traffic_bytes_per_step"])
+        line["roofline"]["traffic_note"] = (
+            f"HBM bytes per step of the two GEMM launches ({STEP_KERNELS[str(args.workload)][0]}) from rocprofv3 "
+            f"FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading for a 256 MiB copy (factors "
+            f"{tr['FETCH_SIZE']['copy_factor']:.3f}, {tr['WRITE_SIZE']['copy_factor']:.3f}); the step's "
+            f"unavoidable bytes (every routed expert's slot once, x, y) are {wl.min_bytes_per_step()}")
     if not args.no_cpu_baseline:
         # the 2880-wide GGUF form has no CPU leg: its layers are random codes, not oracle experts
         line["cpu_baseline"] = None if gguf and args.gguf_shape == "2880" else cpu_baseline(args.workload)
@@ -651,6 +675,8 @@ def main() -> int:
             args.steps = 20
         if "--warmup" not in sys.argv:
             args.warmup = 3
+        if args.copy_calibration:
+            copy_calibration(dev)
         return run_prefill(args, dev)
     K, W = args.steps, args.warmup
     n_layers = args.layers
