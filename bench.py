@@ -1,6 +1,6 @@
 """Benchmark of the MoE expert dequant-matvec hot path on one MI355X.
 
-Default workload (BASELINE workload 3): GPT-OSS-20B-shaped MXFP4 MoE layer decode,
+Default workload (workload 3, the headline metric's): GPT-OSS-20B-shaped MXFP4 MoE layer decode,
 hidden 2880, 32 experts, top-4 (topk -> softmax), batch 1. One step = one token
 through one MoE layer: router top-k on the GPU + the fused expert FFN (gate_up ->
 clamped SwiGLU -> down, biases, weighted top-k sum). Steps rotate over --layers
