@@ -4,9 +4,9 @@
 // Loads: a wave copies the contiguous byte range of its rows' super-blocks into its LDS
 // area with coalesced 16-byte buffer-to-LDS loads (gq_stage_raw). Work unit: one lane then
 // owns a quantisation unit of the stream (Q4_K / Q5_K: half a super-block, 128 values: its
-// 64 qs bytes with the super-block's header (and Q5_K's 32 qh bytes); Q6_K: half a
-// super-block: its 64 ql bytes, 32 qh bytes and 8 scales; Q8_0: a 32-value block, 34 bytes) and reads it from LDS with 16-byte reads at
-// 2-byte alignment (which gfx950 serves). Rows may start inside a unit (the flat stream at
+// 64 qs bytes with the super-block's header and, for Q5_K, its 32 qh bytes; Q6_K: half a
+// super-block: its 64 ql bytes, 32 qh bytes and 8 scales; Q8_0: a 32-value block, 34 bytes)
+// and reads it from LDS with 16-byte reads at 2-byte alignment (which gfx950 serves). Rows may start inside a unit (the flat stream at
 // K = 2880), so results are attributed per 32-value sub-block to the unit's row or the
 // next one.
 //
@@ -132,9 +132,9 @@ __device__ __forceinline__ float dot32x(const uint32_t q[8], const GqXr& r) {
     return dot16x<SPLIT>(q, r, 0) + dot16x<SPLIT>(q + 4, r, 1);
 }
 
-// Values per unit: a Q8_0 block, or half a K-quant super-block (128 values: a wave of 64
-// lanes then holds whole units of rows of 256 values or more at half the work per lane of
-// a whole super-block, so a wave's compute after its copies arrive is half as long).
+// Values per unit: a Q8_0 block, or half a K-quant super-block (128 values: half the work
+// per lane of a whole super-block, so a wave's compute after its copies arrive is half as
+// long, and the same rows fill twice the lanes).
 __host__ __device__ constexpr uint32_t gq_unit_values(int type) { return type == 8 ? 32u : 128u; }
 template <int TYPE> struct GqUnit;
 // values per unit, super-block (or block) bytes, units per super-block
