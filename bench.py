@@ -95,7 +95,7 @@ STEP_KERNELS = {"1": ("gs_matvec_kernel",), "2": ("gs_gate_up_kernel", "gs_down_
                 "3": ("mxt_gate_up_kernel", "mxt_down_kernel"), "3c": ("mxt_gate_up_kernel", "mxt_down_kernel"),
                 "4": ("gq_phase_a", "gq_phase_b"), "7": ("mxfp4_mv_mfma_kernel",),
                 "8": ("router_logits_decode_kernel", "mxt_gate_up_kernel", "mxt_down_kernel"),
-                "5": ("pf_gemm_kernel",), "6": ("gf_gemm_kernel",)}
+                "5": ("pf_gemm_kernel",), "6": ("gf_step_kernel", "gf_gemm_kernel")}
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str, key: str, command: str) -> dict:

@@ -107,13 +107,24 @@ def _run(L, experts, pool, rng, T, k, E, expert_slot=None, idx=None, out_dtype=N
     return y, ref
 
 
-@pytest.mark.parametrize("types", [(12, 12, 14), (13, 13, 14), (8, 8, 8), (14, 14, 14), (13, 13, 13), (12, 12, 8)])
+@pytest.mark.parametrize("types", [(12, 12, 14), (13, 13, 14), (8, 8, 8), (14, 14, 14), (13, 13, 13), (12, 12, 8),
+                                   (12, 12, 12), (8, 8, 14)])
 def test_gguf_grouped_prefill_types(types):
     rng = np.random.default_rng(100 + sum(types))
     H, I, E, k, T = 512, 256, 16, 4, 40  # 160 assignments: ragged tiles of the 16 experts
     L, experts, pool = _pool(rng, H, I, types, E)
     y, ref = _run(L, experts, pool, rng, T, k, E, grouped=True)
     assert_close_bf16(y, ref, f"GGUF grouped prefill, types {types}")
+
+
+def test_gguf_grouped_prefill_partial_column_tile():
+    """inter 160: the gate_up launch's last column tile holds 32 of its 64 gate / up rows (the
+    rest read zeros past the matrix and are not stored); the down rows then straddle."""
+    rng = np.random.default_rng(12)
+    H, I, E, k, T = 512, 160, 8, 4, 40
+    L, experts, pool = _pool(rng, H, I, (13, 13, 14), E)
+    y, ref = _run(L, experts, pool, rng, T, k, E, grouped=True)
+    assert_close_bf16(y, ref, "GGUF grouped prefill, partial column tile")
 
 
 def test_gguf_grouped_prefill_multi_tile_and_fp32_out():

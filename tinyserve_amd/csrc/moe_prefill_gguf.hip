@@ -15,20 +15,27 @@
 //   combine: y[t] = sum_j w[t, j] yk[t k + j] in j order (one writer per output).
 //
 // Workgroup: 8 waves, a tile of 64 sorted rows x 128 weight rows (gate_up: 64 gate rows and
-// the same 64 up rows, so the activation is formed in the workgroup). K advances in pieces
-// of 256 values (one K-quant super-block of each row, or 8 Q8_0 blocks): the piece's raw
-// blocks for the 128 rows (a 16-byte-aligned window per row) and its activations come in
-// by buffer-to-LDS copies, the activations into one of two tiles as the previous piece
-// starts, the raw blocks into one of three areas two pieces ahead. Where K is not a
-// multiple of 256 (hidden 2880), a K-quant row starts inside a super-block (GGUF stores a
-// matrix as one run of blocks) and a piece of it covers the end of one super-block and the
-// start of the next: that variant keeps each row's super-blocks in a ring of areas, one new
-// super-block per piece, and decodes every 32-value unit from whichever super-block holds
-// it; the last piece of a row is partial, its units past K zeroed. Wave (wr, kh) owns weight
-// rows 32 wr .. + 31 and K half kh of every piece: each lane decodes the values of its row
-// that it feeds v_mfma_f32_32x32x16_bf16 as the A operand straight into registers (no row
-// is decoded twice, no weight tile goes through LDS), the activations are the B operand
-// from LDS, and the two K halves' sums meet in LDS after the last piece.
+// the same 64 up rows, so the activation is formed in the workgroup). Wave (wr, kh) owns
+// weight rows 32 wr .. + 31 and half the K values of every step: each lane decodes the values
+// of its row that it feeds v_mfma_f32_32x32x16_bf16 as the A operand straight into registers
+// (no row is decoded twice, no weight tile goes through LDS), the activations are the B
+// operand from LDS, and the two halves' sums meet in LDS after the last step. The raw blocks
+// (a 16-byte-aligned window per row) and the activations come in by buffer-to-LDS copies.
+//
+// gf_step_kernel (K-quants, K a multiple of 256): K in steps of 128 values, half a
+// super-block of each row; a step's activations and the rows' half windows (the header and
+// the codes that half reads) come in one step ahead into one of two tiles and areas, 77 KB
+// of LDS at most, so two workgroups share a CU.
+//
+// gf_gemm_kernel (Q8_0, and K-quant rows that straddle super-blocks): K in pieces of 256
+// values (one super-block of each row, or 8 Q8_0 blocks), up to 154 KB of LDS, one workgroup
+// per CU: the activations into one of two tiles as the previous piece starts, the raw blocks
+// into a ring of areas ahead of their piece. Where K is not a multiple of 256 (hidden 2880),
+// a K-quant row starts inside a super-block (GGUF stores a matrix as one run of blocks) and a
+// piece of it covers the end of one super-block and the start of the next: that variant keeps
+// each row's super-blocks in a ring of areas, one new super-block per piece, and decodes
+// every 32-value unit from whichever super-block holds it; the last piece of a row is
+// partial, its units past K zeroed.
 //
 // Semantics: tinyserve/expert_pipeline.py:166-239 (group by expert, batched forward,
 // weighted scatter), tinyserve/ggml_forward.py:117-151 (bf16 weights, F.linear,
@@ -74,20 +81,18 @@ template <int TY> constexpr int gf_align() { return TY == 12 || TY == 13 ? 16 : 
 // wave's lanes decode from then sit 4 (mod 8) dwords apart and spread over 16 bank groups
 // (an even count halves that or worse: Q6_K's 14 chunks cost its kernel 8% against 15).
 template <int TY> constexpr int gf_nch() { return ((GfType<TY>::PB + (gf_align<TY>() == 16 ? 0 : 14) + 15) / 16) | 1; }
-// Raw areas, each the 128 rows' windows of one group. Plain: the piece in use and the next
-// two (one ahead for Q8_0, whose windows would not fit three areas beside the activation
-// tiles). Straddling (SD): a piece reads two groups of its row, so one more area (Q6_K:
-// none more fit, so its next group flies for one piece only).
-template <int TY, bool SD> constexpr int gf_areas() { return SD ? (TY == 14 ? 3 : 4) : TY == 8 ? 2 : 3; }
+// gf_gemm_kernel's raw areas, each the 128 rows' windows of one group. Plain (Q8_0): the
+// piece in use and the next (three areas of its windows would not fit beside the activation
+// tiles). Straddling (SD): a piece reads two groups of its row, and one or two more areas
+// take the groups ahead (Q6_K: one; its windows leave room for three areas only).
+template <int TY, bool SD> constexpr int gf_areas() { return SD ? (TY == 14 ? 3 : 4) : 2; }
 template <int TY> constexpr int gf_raw() { return GF_BN * gf_nch<TY>() * 16; }
 template <int TY, bool SD> constexpr int gf_lds() {
     return GF_ROFF + gf_areas<TY, SD>() * gf_raw<TY>() > GF_STAGE ? GF_ROFF + gf_areas<TY, SD>() * gf_raw<TY>()
                                                                   : GF_STAGE;
 }
-static_assert(gf_lds<8, false>() <= 160 * 1024 && gf_lds<12, false>() <= 160 * 1024 &&
-                  gf_lds<13, false>() <= 160 * 1024 && gf_lds<14, false>() <= 160 * 1024 &&
-                  gf_lds<12, true>() <= 160 * 1024 && gf_lds<13, true>() <= 160 * 1024 &&
-                  gf_lds<14, true>() <= 160 * 1024,
+static_assert(gf_lds<8, false>() <= 160 * 1024 && gf_lds<12, true>() <= 160 * 1024 &&
+                  gf_lds<13, true>() <= 160 * 1024 && gf_lds<14, true>() <= 160 * 1024,
               "LDS per workgroup");
 
 struct GfGemm {
@@ -106,8 +111,11 @@ struct GfGemm {
     tsa_expert_layout L;
 };
 
+// One 1 KB copy: lane l's 16 bytes at buffer offset voff land at LDS byte lds + 16 l (the LDS
+// address is the wave's, taken from the first lane).
 __device__ __forceinline__ void gf_dma(const v4i_t& r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r),
+                 "s"(__builtin_amdgcn_readfirstlane((int)lds))
                  : "memory", "m0");
 }
 
@@ -160,11 +168,16 @@ __device__ __forceinline__ void gf_issue_raw(const v4i_t& r0, const v4i_t& r1, u
 // rounding, fused or not); Q6_K (d*sc) * (q - 32), here as (d*sc/4) times the signed byte
 // 4 (q - 32) (q ^ 32 is q - 32 as a 6-bit two's-complement field, and two more bits to the
 // left make the byte's sign), exact like the reference's product, signed zeros included.
-template <int TY>
+// HALF: sb is a half window (gf_step_kernel) holding only what units 4h .. 4h + 3 (h = u / 4)
+// read, at the offsets gf_half_chunk lays out: Q4_K / Q5_K keep the header (and Q5_K's high
+// bits) and take the half's 64 bytes of codes right after; Q6_K's half window is the half's
+// low codes (block bytes 64 h ..), high codes (128 + 32 h ..) at +80 and scales and d
+// (192 ..) at -64, each from sb.
+template <int TY, bool HALF = false>
 __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uint32_t (&o)[8]) {
     if constexpr (TY == 12 || TY == 13) {  // sb is 16-byte aligned
         const u32x4 hdr = *reinterpret_cast<const u32x4*>(sb);
-        const uint8_t* qs = sb + (TY == 12 ? 16 : 48) + 32 * (u >> 1);
+        const uint8_t* qs = sb + (TY == 12 ? 16 : 48) + 32 * (HALF ? (u >> 1) & 1 : u >> 1);
         const uint2 q0 = *reinterpret_cast<const uint2*>(qs + 8 * g), q1 = *reinterpret_cast<const uint2*>(qs + 16 + 8 * g);
         const uint32_t q[4] = {q0.x, q0.y, q1.x, q1.y};
         uint32_t hb[4] = {0u, 0u, 0u, 0u};
@@ -193,7 +206,7 @@ __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uin
         auto ld4 = [&](int off, uint32_t (&w)[4]) {  // dwords 2g, 2g + 1, 2g + 4, 2g + 5 of the 32 bytes at sb + off
             const int b0 = (off >> 2) + 2 * g;
             const uint32_t t0 = wb[b0], t1 = wb[b0 + 1], t2 = wb[b0 + 2];
-            const uint32_t t4 = wb[b0 + 4], t5 = wb[b0 + 5], t6 = wb[b0 + 6];  // at most the ninth: inside the block
+            const uint32_t t4 = wb[b0 + 4], t5 = wb[b0 + 5], t6 = wb[b0 + 6];  // at most the ninth: inside the block or half window
             w[0] = __builtin_amdgcn_alignbyte(t1, t0, ob);
             w[1] = __builtin_amdgcn_alignbyte(t2, t1, ob);
             w[2] = __builtin_amdgcn_alignbyte(t5, t4, ob);
@@ -205,10 +218,10 @@ __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uin
         };
         const int hh = u >> 2, t = u & 3;
         uint32_t ql[4], qh[4];
-        ld4(64 * hh + 32 * (t & 1), ql);
-        ld4(128 + 32 * hh, qh);
-        const uint32_t scw = ld16(192 + 2 * u);
-        const float d = f16_bits_to_f32(ld16(208));
+        ld4(HALF ? 32 * (t & 1) : 64 * hh + 32 * (t & 1), ql);
+        ld4(HALF ? 80 : 128 + 32 * hh, qh);
+        const uint32_t scw = ld16((HALF ? 128 : 192) + 2 * u);
+        const float d = f16_bits_to_f32(ld16(HALF ? 144 : 208));
         const float d0 = 0.25f * (d * (float)(int8_t)(scw & 0xFF)), d1 = 0.25f * (d * (float)(int8_t)(scw >> 8));
         const int shl = 4 * (t >> 1), shh = 2 * t;
 #pragma unroll
@@ -230,6 +243,59 @@ __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uin
     }
 }
 
+// The epilogue of a tile: acc[t][4u + r] = tile row 32 wr + 8u + 4g + r, sorted row 32 t + rr,
+// over K half kh (wave (wr, kh), lane (g, rr)). Both halves' sums into LDS (nothing may be in
+// flight and every wave is here), stage[kh][sorted row][tile row], then each output adds its
+// two halves: gate_up h = act(gate, up) rounded once to bf16 in sorted order, down one bf16
+// row per assignment.
+template <bool GU>
+__device__ __forceinline__ void gf_store_tile(const GfGemm& p, const GfEntry& en, int n0, const v16f_t (&acc)[2],
+                                              uint8_t* smem) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, kh = wave >> 2, g = lane >> 5, rr = lane & 31;
+    const int N = p.N;
+    __syncthreads();
+    float* stage = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            *reinterpret_cast<float4*>(stage + (kh * GF_BM + 32 * t + rr) * GF_SS + 32 * wr + 8 * u + 4 * g) =
+                make_float4(acc[t][4 * u], acc[t][4 * u + 1], acc[t][4 * u + 2], acc[t][4 * u + 3]);
+    __syncthreads();
+    if constexpr (GU) {
+        // h = act(gate, up) rounded once to bf16, 8 columns per thread
+        const int hr = tid >> 3, hc = 8 * (tid & 7);
+        if (hr < en.rows && n0 + hc < N) {
+            const float* s0 = stage + hr * GF_SS + hc;
+            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
+            float h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float gv = s0[i] + s1[i], uv = s0[64 + i] + s1[64 + i];
+                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gv, uv) : gv * sigmoidf_(gv) * uv;
+            }
+            *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
+                make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
+                           pack_bf16x2(h[6], h[7]));
+        }
+    } else {
+        // 16 output rows per thread, bf16 per assignment
+        const int hr = tid >> 3, hc = 16 * (tid & 7);
+        if (hr < en.rows && n0 + hc < N) {  // N % 16 == 0
+            const int64_t a = p.perm[en.row0 + hr];
+            const float* s0 = stage + hr * GF_SS + hc;
+            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
+            uint32_t o[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = pack_bf16x2(s0[2 * i] + s1[2 * i], s0[2 * i + 1] + s1[2 * i + 1]);
+            uint4* dst = reinterpret_cast<uint4*>(p.out + a * N + n0 + hc);
+            dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+            dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        }
+    }
+}
+
 template <int TY, bool GU, bool SD>
 __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -246,7 +312,7 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
     const GfEntry en = p.table[en_i];
     const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
     const int wr = wave & 3, kh = wave >> 2, g = lane >> 5, rr = lane & 31;
-    const int K = p.K, KU = K / 32, P = (KU + 7) / 8, N = p.N;
+    const int K = p.K, KU = K / 32, P = (KU + 7) / 8;
     const int n0 = tile * (GU ? GF_BN / 2 : GF_BN);  // first output column of the tile
     const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
     const uint8_t* mat0 = base + p.w_off;
@@ -370,49 +436,166 @@ __global__ void __launch_bounds__(GF_THREADS, 1) gf_gemm_kernel(GfGemm p) {
         }
     }
 
-    // acc[t][4u + r] = tile row 32 wr + 8u + 4g + r, sorted row 32 t + rr, over K half kh.
-    // Both halves' sums into LDS (nothing is in flight and every wave is here),
-    // stage[kh][sorted row][tile row], then each output adds its two halves.
-    __syncthreads();
-    float* stage = reinterpret_cast<float*>(smem);
+    gf_store_tile<GU>(p, en, n0, acc, smem);
+}
+
+// ---- gf_step_kernel: the plain K-quant matrices (K % 256 == 0), K in steps of 128 values
+
+constexpr int GF_KS = 128;               // values per step: half a super-block of each row
+constexpr int GF_SRS = 2 * GF_KS;        // a step's activation row: 256 bytes, 16 chunks
+constexpr int GF_SXB = GF_BM * GF_SRS;   // one step activation tile; two of them
+constexpr int GF_SROFF = 2 * GF_SXB;     // then two raw areas
+
+// 16-byte chunks of a row's half window (odd, as gf_nch): Q4_K header + 4 of codes; Q5_K
+// header, high bits + 4 of codes; Q6_K 5 of low codes, 3 of high codes, 2 of scales and d
+// (+1 unused), each run from the boundary at or below it (a Q6_K block sits 0..14 bytes past
+// one).
+template <int TY> constexpr int gf_half_nch() { return TY == 12 ? 5 : TY == 13 ? 7 : 11; }
+template <int TY> constexpr int gf_half_raw() { return GF_BN * gf_half_nch<TY>() * 16; }
+template <int TY> constexpr int gf_step_lds() {
+    return GF_SROFF + 2 * gf_half_raw<TY>() > GF_STAGE ? GF_SROFF + 2 * gf_half_raw<TY>() : GF_STAGE;
+}
+static_assert(gf_step_lds<12>() <= 80 * 1024 && gf_step_lds<13>() <= 80 * 1024 && gf_step_lds<14>() <= 80 * 1024,
+              "two workgroups per CU");
+
+// Source chunk of half window slot c in half h, counted from the boundary at or below the
+// super-block (Q4_K 9 chunks, Q5_K 11; a Q6_K block covers chunks 0 .. 13).
+template <int TY> __device__ __forceinline__ int gf_half_chunk(int c, int h) {
+    if constexpr (TY == 12) return c == 0 ? 0 : c + 4 * h;
+    else if constexpr (TY == 13) return c < 3 ? c : c + 4 * h;
+    else return c < 5 ? 4 * h + c : c < 8 ? 3 + 2 * h + c : c < 10 ? 4 + c : 13;
+}
+
+// The same tile as gf_gemm_kernel (64 sorted rows x 128 weight rows, wave (wr, kh) decoding
+// the A operands of its 32 rows), with K in steps of 128 values: a step's activations (16 KB)
+// and the half windows of its 128 rows' super-blocks come in one step ahead into one of two
+// tiles and areas, so a workgroup holds at most 77 KB of LDS and two share a CU (what one
+// workgroup's barrier, copy waits, prologue and epilogue leave idle, the other fills). Step s
+// is half s % 2 of piece s / 2; wave kh decodes units 4 h + 2 kh and 4 h + 2 kh + 1 of it, and
+// the steps of a piece are unrolled and the two kh branches written out, so every unit index
+// and shift is a constant and the LDS addresses of the B operands and windows are fixed per lane.
+template <int TY, bool GU>
+__global__ void __launch_bounds__(GF_THREADS, 2) gf_step_kernel(GfGemm p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tiles = (int)gridDim.x, nact = *p.n_entries * tiles;
+    const int lin = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    if (lin >= nact) return;  // workgroup-uniform
+    const int xcd = lin & 7, q8 = nact >> 3, rem = nact & 7;
+    const int wid = xcd * q8 + (xcd < rem ? xcd : rem) + (lin >> 3);  // as gf_gemm_kernel
+    const int en_i = wid / tiles, tile = wid - en_i * tiles;
+    const GfEntry en = p.table[en_i];
+    const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+    const int wr = wave & 3, kh = wave >> 2, g = lane >> 5, rr = lane & 31;
+    const int K = p.K, KU = K / 32, P = K / GF_KP;
+    const int n0 = tile * (GU ? GF_BN / 2 : GF_BN);
+    const uint8_t* base = p.pool + (int64_t)en.slot * p.slot_bytes;
+    const uint8_t* mat0 = base + p.w_off;
+    const uint8_t* mat1 = base + (GU ? p.w2_off : p.w_off);
+    const uint32_t mis0 = (uint32_t)reinterpret_cast<uintptr_t>(mat0) & 15u;
+    const uint32_t mis1 = (uint32_t)reinterpret_cast<uintptr_t>(mat1) & 15u;
+    const v4i_t rs0 = gf_desc(mat0 - mis0, (p.w_bytes + mis0 + 15) & ~15ll),
+                rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    constexpr int RAW = gf_half_raw<TY>(), NCH = gf_half_nch<TY>(), PB = GfType<TY>::PB;
+    // a step's raw copies: 128 NCH chunks = 2 NCH wave instructions (ii = wave, wave + 8, ..)
+    constexpr int RI = (2 * NCH + 7) / 8;
+
+    // Activation tiles: row r holds sorted row r's step as 16 chunks, chunk c in slot c ^ (r % 16);
+    // wave w's copy i fills rows 8w + 4i .. 8w + 4i + 3 (lane l: row 8w + 4i + l / 16, slot l % 16).
+    // Rows past the tile read zeros (an offset past the buffer's end).
+    const v4i_t rx = gf_desc(reinterpret_cast<const uint8_t*>(p.src), p.src_bytes);
+    uint32_t xo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 8 * wave + 4 * i + (lane >> 4);
+        xo[i] = 0x80000000u;
+        if (r < en.rows) {
+            const int a = p.perm[en.row0 + r];
+            const int64_t xrow = GU ? (int64_t)(a / p.k) : (int64_t)(en.row0 + r);
+            xo[i] = (uint32_t)(xrow * K * 2) + 16u * (uint32_t)((lane & 15) ^ (r & 15));
+        }
+    }
+    // Raw areas: pair q = (row q / NCH, slot q % NCH) of the 128 rows' half windows at 16 q.
+    // Per copy instruction i of this wave: its lane's row's first super-block (byte offset from
+    // the buffer base, the matrix's misalignment included) and its chunk in half 0 and half 1.
+    // 128 NCH is a multiple of 64, so every instruction is whole, and its rows are all gate or
+    // all up rows (ii < NCH: rows 0 .. 63).
+    uint32_t rg[RI], rc0[RI], rc1[RI];
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+        const int q = 64 * (wave + 8 * i) + lane, r = q / NCH, c = q - r * NCH;
+        const int row = GU ? n0 + (r & 63) : n0 + r;
+        rg[i] = (GU && r >= 64 ? mis1 : mis0) + gf_group_byte<TY>(row, 0, KU);
+        rc0[i] = 16u * (uint32_t)gf_half_chunk<TY>(c, 0);
+        rc1[i] = 16u * (uint32_t)gf_half_chunk<TY>(c, 1);
+    }
+    auto issue = [&](int s) {  // step s's activations and half windows, into tile and area s % 2
+        const int pc = s >> 1, h = s & 1;
+        const uint32_t t = lds0 + (uint32_t)h * GF_SXB + (uint32_t)(8 * wave) * GF_SRS;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) gf_dma(rx, xo[i] + (uint32_t)s * (2 * GF_KS), t + (uint32_t)(4 * i) * GF_SRS);
+        const uint32_t ra = lds0 + GF_SROFF + (uint32_t)h * RAW;
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int ii = wave + 8 * i;
+            if (ii < 2 * NCH) {  // wave-uniform
+                const uint32_t voff = ((rg[i] + (uint32_t)pc * PB) & ~15u) + (h ? rc1[i] : rc0[i]);
+                gf_dma(GU && ii >= NCH ? rs1 : rs0, voff, ra + 1024u * (uint32_t)ii);
+            }
+        }
+    };
+
+    // this lane's weight row (tile row 32 wr + rr) and its half window; the B operands: K steps
+    // j2 = 4 kh + j (j = 0 .. 3) of a step, lane half g reading chunk 2 j2 + g of sorted row rr
+    const int trow = 32 * wr + rr;
+    const int drow = GU ? n0 + (trow & 63) : n0 + trow;
+    const uint32_t dg = (GU && trow >= 64 ? mis1 : mis0) + gf_group_byte<TY>(drow, 0, KU);
+    const uint8_t* win = smem + GF_SROFF + 16 * NCH * trow;
+    const uint8_t* xa[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xa[j] = smem + rr * GF_SRS + 16 * ((2 * (4 * kh + j) + g) ^ (rr & 15));
+
+    v16f_t acc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            *reinterpret_cast<float4*>(stage + (kh * GF_BM + 32 * t + rr) * GF_SS + 32 * wr + 8 * u + 4 * g) =
-                make_float4(acc[t][4 * u], acc[t][4 * u + 1], acc[t][4 * u + 2], acc[t][4 * u + 3]);
-    __syncthreads();
-    if constexpr (GU) {
-        // h = act(gate, up) rounded once to bf16, 8 columns per thread
-        const int hr = tid >> 3, hc = 8 * (tid & 7);
-        if (hr < en.rows && n0 + hc < N) {
-            const float* s0 = stage + hr * GF_SS + hc;
-            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
-            float h[8];
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+
+    // units 4 h + 2 khc + uu of the step in tile / area h: each decoded straight into the A
+    // operands of its two K steps, each times sorted rows 0 .. 31 and 32 .. 63
+    auto units = [&](const uint8_t* sb, int h, int khc) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float gv = s0[i] + s1[i], uv = s0[64 + i] + s1[64 + i];
-                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gv, uv) : gv * sigmoidf_(gv) * uv;
+        for (int uu = 0; uu < 2; ++uu) {
+            uint32_t av[8];
+            gf_decode_a<TY, true>(sb, 4 * h + 2 * khc + uu, g, av);
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const bf16x8 A = __builtin_bit_cast(bf16x8, u32x4{av[4 * s2], av[4 * s2 + 1], av[4 * s2 + 2], av[4 * s2 + 3]});
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const bf16x8 B = *reinterpret_cast<const bf16x8*>(xa[2 * uu + s2] + h * GF_SXB + 32 * t * GF_SRS);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc[t], 0, 0, 0);
+                }
             }
-            *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
-                make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
-                           pack_bf16x2(h[6], h[7]));
         }
-    } else {
-        // 16 output rows per thread, bf16 per assignment
-        const int hr = tid >> 3, hc = 16 * (tid & 7);
-        if (hr < en.rows && n0 + hc < N) {  // N % 16 == 0
-            const int64_t a = p.perm[en.row0 + hr];
-            const float* s0 = stage + hr * GF_SS + hc;
-            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
-            uint32_t o[8];
+    };
+
+    // Step s waits for everything this wave copied (step s's data: nothing newer flies), then
+    // the barrier: every wave's copies of step s have landed and tile / area (s + 1) % 2, last
+    // read in step s - 1, is free for step s + 1's copies.
+    issue(0);
+    for (int pc = 0; pc < P; ++pc) {
+        const uint8_t* sbp = win + ((dg + (uint32_t)pc * PB) & 15u);  // the block's place in its window
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = pack_bf16x2(s0[2 * i] + s1[2 * i], s0[2 * i + 1] + s1[2 * i + 1]);
-            uint4* dst = reinterpret_cast<uint4*>(p.out + a * N + n0 + hc);
-            dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-            dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        for (int h = 0; h < 2; ++h) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (h == 0 || pc + 1 < P) issue(2 * pc + h + 1);
+            if (kh == 0) units(sbp + h * RAW, h, 0);
+            else units(sbp + h * RAW, h, 1);
         }
     }
+    gf_store_tile<GU>(p, en, n0, acc, smem);
 }
 
 // Tiles of up to GF_BM sorted rows per resident expert: entry = (slot, first sorted row,
@@ -450,24 +633,33 @@ __global__ void __launch_bounds__(1024) gf_table_kernel(const int32_t* __restric
 template <int TY, bool GU, bool SD>
 const void* gf_fn() { return reinterpret_cast<const void*>(&gf_gemm_kernel<TY, GU, SD>); }
 
-const void* gf_pick(int t, bool gu, bool sd) {
+// gf_gemm_kernel runs Q8_0 (plain) and the K-quants' straddling rows
+const void* gf_pick(int t, bool gu) {
     switch (t) {
         case 8: return gu ? gf_fn<8, true, false>() : gf_fn<8, false, false>();
-        case 12: return sd ? (gu ? gf_fn<12, true, true>() : gf_fn<12, false, true>())
-                           : (gu ? gf_fn<12, true, false>() : gf_fn<12, false, false>());
-        case 13: return sd ? (gu ? gf_fn<13, true, true>() : gf_fn<13, false, true>())
-                           : (gu ? gf_fn<13, true, false>() : gf_fn<13, false, false>());
-        case 14: return sd ? (gu ? gf_fn<14, true, true>() : gf_fn<14, false, true>())
-                           : (gu ? gf_fn<14, true, false>() : gf_fn<14, false, false>());
+        case 12: return gu ? gf_fn<12, true, true>() : gf_fn<12, false, true>();
+        case 13: return gu ? gf_fn<13, true, true>() : gf_fn<13, false, true>();
+        case 14: return gu ? gf_fn<14, true, true>() : gf_fn<14, false, true>();
     }
     return nullptr;
 }
 
-int gf_lds_of(int t, bool sd) {
-    if (t == 8) return gf_lds<8, false>();
-    if (t == 12) return sd ? gf_lds<12, true>() : gf_lds<12, false>();
-    if (t == 13) return sd ? gf_lds<13, true>() : gf_lds<13, false>();
-    return sd ? gf_lds<14, true>() : gf_lds<14, false>();
+template <int TY, bool GU>
+const void* gf_step_fn() { return reinterpret_cast<const void*>(&gf_step_kernel<TY, GU>); }
+
+const void* gf_step_pick(int t, bool gu) {
+    switch (t) {
+        case 12: return gu ? gf_step_fn<12, true>() : gf_step_fn<12, false>();
+        case 13: return gu ? gf_step_fn<13, true>() : gf_step_fn<13, false>();
+        case 14: return gu ? gf_step_fn<14, true>() : gf_step_fn<14, false>();
+    }
+    return nullptr;
+}
+
+int gf_step_lds_of(int t) { return t == 12 ? gf_step_lds<12>() : t == 13 ? gf_step_lds<13>() : gf_step_lds<14>(); }
+
+int gf_lds_of(int t) {
+    return t == 8 ? gf_lds<8, false>() : t == 12 ? gf_lds<12, true>() : t == 13 ? gf_lds<13, true>() : gf_lds<14, true>();
 }
 
 int64_t gf_al256(int64_t v) { return (v + 255) / 256 * 256; }
@@ -538,11 +730,14 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
                        nent, table);
     TSA_LAUNCH_CHECK();
 
-    // a K-quant matrix whose K is not a multiple of 256 takes the straddling variant
+    // a K-quant matrix whose K is a multiple of 256 takes gf_step_kernel; one whose K is not,
+    // the straddling variant of gf_gemm_kernel; Q8_0 its plain variant
     const bool sd_gu = L.gate_type != 8 && L.hidden % GF_KP != 0, sd_dn = L.down_type != 8 && L.inter % GF_KP != 0;
-    const void* f_gu = gf_pick(L.gate_type, true, sd_gu);
-    const void* f_dn = gf_pick(L.down_type, false, sd_dn);
-    const int lds_gu = gf_lds_of(L.gate_type, sd_gu), lds_dn = gf_lds_of(L.down_type, sd_dn);
+    const bool st_gu = L.gate_type != 8 && !sd_gu, st_dn = L.down_type != 8 && !sd_dn;
+    const void* f_gu = st_gu ? gf_step_pick(L.gate_type, true) : gf_pick(L.gate_type, true);
+    const void* f_dn = st_dn ? gf_step_pick(L.down_type, false) : gf_pick(L.down_type, false);
+    const int lds_gu = st_gu ? gf_step_lds_of(L.gate_type) : gf_lds_of(L.gate_type),
+              lds_dn = st_dn ? gf_step_lds_of(L.down_type) : gf_lds_of(L.down_type);
     for (auto [f, b] : {std::pair<const void*, int>{f_gu, lds_gu}, std::pair<const void*, int>{f_dn, lds_dn}}) {
         const hipError_t e = ensure_dynamic_lds(f, b);
         TSA_REQUIRE(e == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", b, hipGetErrorString(e));
