@@ -279,7 +279,8 @@ def test_single_expert_workload2_full():
 
 
 # ----------------------------------------------------------------------------- grouping / prefill
-@pytest.mark.parametrize("T,k,E", [(2048, 4, 32), (37, 8, 128), (1, 1, 1), (3000, 2, 1000), (5000, 3, 64)])
+@pytest.mark.parametrize("T,k,E", [(2048, 4, 32), (37, 8, 128), (1, 1, 1), (3000, 2, 1000), (5000, 3, 64),
+                                   (4096, 8, 1024), (1000, 4, 2)])  # the most experts; most lanes of a batch share one
 def test_group_by_expert_vs_oracle(T, k, E):
     rng = np.random.default_rng(T + k + E)
     idx = rng.integers(0, E, size=(T, k)).astype(np.int32)

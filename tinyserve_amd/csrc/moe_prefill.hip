@@ -22,39 +22,38 @@ constexpr int GROUP_WAVES = GROUP_THREADS / 64;
 constexpr int MAX_GROUP_E = 1024;
 constexpr int GROUP_AHEAD = 8;  // id batches loaded ahead per wave
 
-// Lanes of the wave holding the same expert as this lane (e >= 0; lanes with e < 0 are in
-// no group), found with one ballot per bit of the expert id instead of a loop over the
-// distinct experts.
-__device__ __forceinline__ unsigned long long peers(int e, int nbits) {
-    unsigned long long m = __ballot(e >= 0);
-    for (int b = 0; b < nbits; ++b) {
-        const bool bit = (e >> b) & 1;
-        const unsigned long long v = __ballot(bit);
-        m &= bit ? v : ~v;
-    }
-    return m;
-}
+// LDS of group_kernel for E experts: per (wave, expert) counters, the experts' offsets, and
+// per (wave, expert) 64-bit lane masks (8-byte aligned).
+__host__ __device__ constexpr int group_lds_bytes(int E) { return ((GROUP_WAVES + 1) * E * 4 + 7) / 8 * 8 + GROUP_WAVES * E * 8; }
 
 // Single-workgroup stable counting sort of assignment ids by expert. Wave w owns one
 // contiguous chunk of the assignments (a multiple of 64 long) and walks it in batches of
-// 64. Pass 1 counts per (wave, expert) in LDS: the lowest lane of each group of equal
-// experts in a batch adds the group's size (a wave owns its row of counters, so no
-// atomics). An exclusive scan over the waves, per expert, then gives each wave its first
-// rank inside the expert, and a scan over the experts the offsets. Pass 2 walks the same
-// batches in the same order and places each assignment at offset + the wave's running
-// rank + its rank among the group's lanes, so every expert's run keeps assignment order
+// 64. Pass 1 counts per (wave, expert) with LDS atomic adds (a wave owns its row of
+// counters; the order of the adds does not matter). An exclusive scan over the waves, per
+// expert, then gives each wave its first rank inside the expert, and a scan over the
+// experts the offsets. Pass 2 walks the same batches in the same order and places each
+// assignment at offset + the wave's running rank + its rank among the batch's lanes of the
+// same expert: every lane ORs its bit into its wave's mask of the expert and reads the mask
+// back (LDS runs one wave's instructions in order), the lowest lane of each group then
+// clears the mask and advances the running rank. Every expert's run keeps assignment order
 // (token-major), as the reference's grouping does.
 __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __restrict__ idx, int64_t n, int E,
                                                               int32_t* __restrict__ counts,
                                                               int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ perm) {
-    __shared__ int wcnt[GROUP_WAVES][MAX_GROUP_E];
-    __shared__ int eoff[MAX_GROUP_E];
+    extern __shared__ __align__(16) unsigned char gsm[];
+    int* wcnt = reinterpret_cast<int*>(gsm);  // [wave][expert]
+    int* eoff = wcnt + GROUP_WAVES * E;
+    unsigned long long* wmask = reinterpret_cast<unsigned long long*>(gsm + ((GROUP_WAVES + 1) * E * 4 + 7) / 8 * 8);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (int i = tid; i < GROUP_WAVES * MAX_GROUP_E; i += GROUP_THREADS) (&wcnt[0][0])[i] = 0;
+    for (int i = tid; i < GROUP_WAVES * E; i += GROUP_THREADS) {
+        wcnt[i] = 0;
+        wmask[i] = 0ull;
+    }
     __syncthreads();
+    int* cnt = wcnt + wave * E;
+    unsigned long long* msk = wmask + wave * E;
     const int64_t chunk = ((n + GROUP_WAVES - 1) / GROUP_WAVES + 63) / 64 * 64;
     const int64_t a0 = wave * chunk, a1 = a0 + chunk < n ? a0 + chunk : n;
     // Batches of 64 assignments in order; the ids of GROUP_AHEAD batches are loaded together
@@ -67,19 +66,15 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __r
             ev[j] = a < a1 ? idx[a] : -1;
         }
 #pragma unroll
-        for (int j = 0; j < GROUP_AHEAD; ++j) {
-            if (b0 + 64 * j >= a1) break;
-            const int e = ev[j] < E ? ev[j] : -1;
-            const unsigned long long m = peers(e, nbits);
-            if (e >= 0 && !(m & below)) wcnt[wave][e] += __popcll(m);
-        }
+        for (int j = 0; j < GROUP_AHEAD; ++j)
+            if (ev[j] >= 0 && ev[j] < E) atomicAdd(&cnt[ev[j]], 1);
     }
     __syncthreads();
     for (int e = tid; e < E; e += GROUP_THREADS) {
         int run = 0;
         for (int w = 0; w < GROUP_WAVES; ++w) {
-            const int c = wcnt[w][e];
-            wcnt[w][e] = run;
+            const int c = wcnt[w * E + e];
+            wcnt[w * E + e] = run;
             run += c;
         }
         eoff[e] = run;
@@ -118,13 +113,16 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __r
         }
 #pragma unroll
         for (int j = 0; j < GROUP_AHEAD; ++j) {
-            if (b0 + 64 * j >= a1) break;
-            const int64_t a = b0 + 64 * j + lane;
-            const int e = ev[j] < E ? ev[j] : -1;
-            const unsigned long long m = peers(e, nbits);
-            if (e >= 0) {
-                perm[eoff[e] + wcnt[wave][e] + __popcll(m & below)] = (int32_t)a;
-                if (!(m & below)) wcnt[wave][e] += __popcll(m);  // after every lane of the group read it
+            const int e = ev[j];
+            if (e >= 0 && e < E) {
+                atomicOr(&msk[e], 1ull << lane);
+                const unsigned long long m = msk[e];  // after every lane's OR: this batch's lanes of e
+                const int at = eoff[e] + cnt[e] + __popcll(m & below);
+                perm[at] = (int32_t)(b0 + 64 * j + lane);
+                if (!(m & below)) {  // after every lane of the group read the mask and the count
+                    msk[e] = 0ull;
+                    cnt[e] += __popcll(m);
+                }
             }
         }
     }
@@ -143,7 +141,10 @@ __global__ void __launch_bounds__(256) map_slots_kernel(const int32_t* __restric
 
 int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                         hipStream_t stream) {
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, stream, idx, n, E, counts, offsets, perm);
+    const int lds = group_lds_bytes(E);
+    const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&group_kernel), lds);
+    TSA_REQUIRE(e == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", lds, hipGetErrorString(e));
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), lds, stream, idx, n, E, counts, offsets, perm);
     TSA_LAUNCH_CHECK();
     return TSA_OK;
 }
