@@ -102,6 +102,29 @@ __device__ __forceinline__ int wave_min_u(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Inclusive sum of v over the workgroup's threads in thread order (up to 16 waves): a
+// shuffle scan per wave, then each wave adds the totals of the waves before it (wsum: 16
+// ints of LDS). total = the sum over all threads. Every thread must call it; two barriers,
+// the second so that wsum may be reused.
+__device__ __forceinline__ int block_incl_sum(int v, int* wsum, int& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(v, d, 64);
+        if (lane >= d) v += t;
+    }
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int i = 0; i < nw; ++i) {
+        const int s = wsum[i];
+        off += i < w ? s : 0;
+        tot += s;
+    }
+    total = tot;
+    __syncthreads();
+    return v + off;
+}
+
 // Slot tables live in LDS, so the compiler treats values read from them as per-lane;
 // a buffer resource built from such a value is wrapped in a waterfall loop per load.
 // Every lane reads the same entry, so lane 0's value is the wave's.

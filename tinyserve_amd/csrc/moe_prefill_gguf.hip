@@ -605,29 +605,23 @@ __global__ void __launch_bounds__(1024) gf_table_kernel(const int32_t* __restric
                                                         const int32_t* __restrict__ expert_slot, int E,
                                                         int64_t n_slots, int* __restrict__ n_entries,
                                                         GfEntry* __restrict__ table) {
-    __shared__ int pre[1024];
+    __shared__ int wsum[16];
     const int e = threadIdx.x;
-    int slot = -1, c = 0;
-    if (e < E) {
+    int slot = -1, c = 0, o = 0;
+    if (e < E) {  // the three loads go out together
         slot = expert_slot[e];
         c = counts[e];
+        o = offsets[e];
         if (slot < 0 || slot >= n_slots) c = 0;
     }
     const int nt = (c + GF_BM - 1) / GF_BM;
-    pre[e] = nt;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan
-        const int v = e >= d ? pre[e - d] : 0;
-        __syncthreads();
-        pre[e] += v;
-        __syncthreads();
-    }
-    const int first = pre[e] - nt;
+    int total;
+    const int first = block_incl_sum(nt, wsum, total) - nt;
     for (int i = 0; i < nt; ++i) {
         const int r = c - GF_BM * i;
-        table[first + i] = GfEntry{slot, offsets[e] + GF_BM * i, r < GF_BM ? r : GF_BM, 0};
+        table[first + i] = GfEntry{slot, o + GF_BM * i, r < GF_BM ? r : GF_BM, 0};
     }
-    if (e == 1023) n_entries[0] = pre[1023];
+    if (e == 0) n_entries[0] = total;
 }
 
 template <int TY, bool GU, bool SD>

@@ -531,7 +531,7 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
                                                         const int32_t* __restrict__ expert_slot, int E,
                                                         int64_t n_slots, int* __restrict__ n_entries,
                                                         PfEntry* __restrict__ table, int* __restrict__ ctr) {
-    __shared__ int pre[1024];
+    __shared__ int wsum[16];
     __shared__ int hist[PF_BM];    // partial entries with r rows
     __shared__ int pos[PF_BM];     // rank (offset by the full entries) of the next partial entry with r rows
     __shared__ int prow[1024];     // partial entries by rank: rows
@@ -540,35 +540,34 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
     const int e = threadIdx.x;
     if (e < PF_CTR_INTS) ctr[e] = 0;
     if (e < PF_BM) hist[e] = 0;
-    int slot = -1, c = 0, nt = 0, r = 0;
-    if (e < E) {
+    int slot = -1, c = 0, nt = 0, r = 0, o = 0;
+    if (e < E) {  // the three loads go out together
         slot = expert_slot[e];
         c = counts[e];
+        o = offsets[e];
         if (slot >= 0 && slot < n_slots) {
             nt = c / PF_BM;
             r = c % PF_BM;
         }
     }
-    pre[e] = nt;
-    __syncthreads();
+    __syncthreads();  // hist cleared
     if (r > 0) atomicAdd(&hist[r], 1);
-    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan of the full entries
-        const int v = e >= d ? pre[e - d] : 0;
-        __syncthreads();
-        pre[e] += v;
-        __syncthreads();
+    int F;
+    const int pre = block_incl_sum(nt, wsum, F);  // inclusive scan of the full entries (its barriers order hist)
+    // pos[b] = F + partial entries with more than b rows: F + all of hist - its inclusive
+    // prefix sum to b, by wave 0 (lane l: b = 2l, 2l + 1)
+    static_assert(PF_BM == 128, "two hist entries per lane of one wave");
+    if (e < 64) {
+        const int h0 = hist[2 * e], h1 = hist[2 * e + 1];
+        int s = h0 + h1;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int t = __shfl_up(s, d, 64);
+            if (e >= d) s += t;
+        }
+        const int all = __shfl(s, 63, 64);
+        pos[2 * e] = F + all - (s - h1);
+        pos[2 * e + 1] = F + all - s;
     }
-    const int F = pre[1023];
-    // pos[b] = F + partial entries with more than b rows (an exclusive suffix scan of hist)
-    if (e < PF_BM) pos[e] = e + 1 < PF_BM ? hist[e + 1] : 0;
-    __syncthreads();
-    for (int d = 1; d < PF_BM; d <<= 1) {
-        const int v = e < PF_BM && e + d < PF_BM ? pos[e + d] : 0;
-        __syncthreads();
-        if (e < PF_BM) pos[e] += v;
-        __syncthreads();
-    }
-    if (e < PF_BM) pos[e] += F;
     __syncthreads();
     const int P = pos[0] - F;
     __syncthreads();  // pos[0] is read before the partial entries take ranks (r > 0 never touches it)
@@ -613,15 +612,15 @@ __global__ void __launch_bounds__(1024) pf_table_kernel(const int32_t* __restric
     }
     __syncthreads();
     for (int j = 0; j < nt; ++j) {
-        const int f = pre[e] - nt + j;  // full entry f: run x with F x / 8 <= f < F (x + 1) / 8
+        const int f = pre - nt + j;  // full entry f: run x with F x / 8 <= f < F (x + 1) / 8
         int x = 0;
 #pragma unroll
         for (int y = 1; y < 8; ++y) x += F * y / 8 <= f ? 1 : 0;
-        table[gstart[x] + f - F * x / 8] = PfEntry{slot, offsets[e] + PF_BM * j, PF_BM, e};
+        table[gstart[x] + f - F * x / 8] = PfEntry{slot, o + PF_BM * j, PF_BM, e};
     }
     if (q >= 0) {
         const int x = pgrp[q];
-        table[gstart[x] + gfull[x] + pidx[q]] = PfEntry{slot, offsets[e] + PF_BM * nt, r, e};
+        table[gstart[x] + gfull[x] + pidx[q]] = PfEntry{slot, o + PF_BM * nt, r, e};
     }
 }
 
