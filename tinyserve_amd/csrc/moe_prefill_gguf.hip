@@ -205,8 +205,15 @@ __device__ __forceinline__ void gf_decode_a(const uint8_t* sb, int u, int g, uin
         const uint32_t* wb = reinterpret_cast<const uint32_t*>(sb - ob);
         auto ld4 = [&](int off, uint32_t (&w)[4]) {  // dwords 2g, 2g + 1, 2g + 4, 2g + 5 of the 32 bytes at sb + off
             const int b0 = (off >> 2) + 2 * g;
-            const uint32_t t0 = wb[b0], t1 = wb[b0 + 1], t2 = wb[b0 + 2];
-            const uint32_t t4 = wb[b0 + 4], t5 = wb[b0 + 5], t6 = wb[b0 + 6];  // at most the ninth: inside the block or half window
+            uint32_t t0, t1, t2, t4, t5, t6;  // at most the ninth: inside the block or half window
+            if constexpr (HALF) {  // a half window starts at the dword of its block (wb), 16-byte aligned: 8-byte reads
+                const uint2* w2 = reinterpret_cast<const uint2*>(wb + b0);
+                const uint2 p0 = w2[0], p1 = w2[1], p2 = w2[2], p3 = w2[3];
+                t0 = p0.x, t1 = p0.y, t2 = p1.x, t4 = p2.x, t5 = p2.y, t6 = p3.x;
+            } else {
+                t0 = wb[b0], t1 = wb[b0 + 1], t2 = wb[b0 + 2];
+                t4 = wb[b0 + 4], t5 = wb[b0 + 5], t6 = wb[b0 + 6];
+            }
             w[0] = __builtin_amdgcn_alignbyte(t1, t0, ob);
             w[1] = __builtin_amdgcn_alignbyte(t2, t1, ob);
             w[2] = __builtin_amdgcn_alignbyte(t5, t4, ob);
@@ -448,8 +455,11 @@ constexpr int GF_SROFF = 2 * GF_SXB;     // then two raw areas
 
 // 16-byte chunks of a row's half window (odd, as gf_nch): Q4_K header + 4 of codes; Q5_K
 // header, high bits + 4 of codes; Q6_K 5 of low codes, 3 of high codes, 2 of scales and d
-// (+1 unused), each run from the boundary at or below it (a Q6_K block sits 0..14 bytes past
-// one).
+// (+1 unused). A Q6_K window's chunks are counted from the dword at or below its block (0
+// or 2 bytes before it: the copies read 16 bytes at dword-aligned offsets), so the block
+// sits 0 or 2 bytes into a 16-byte-aligned window and its decode reads aligned 8-byte pairs
+// (on distinct banks for the 16 rows of a read, where single dwords 44 apart pair up rows r
+// and r + 16).
 template <int TY> constexpr int gf_half_nch() { return TY == 12 ? 5 : TY == 13 ? 7 : 11; }
 template <int TY> constexpr int gf_half_raw() { return GF_BN * gf_half_nch<TY>() * 16; }
 template <int TY> constexpr int gf_step_lds() {
@@ -458,8 +468,8 @@ template <int TY> constexpr int gf_step_lds() {
 static_assert(gf_step_lds<12>() <= 80 * 1024 && gf_step_lds<13>() <= 80 * 1024 && gf_step_lds<14>() <= 80 * 1024,
               "two workgroups per CU");
 
-// Source chunk of half window slot c in half h, counted from the boundary at or below the
-// super-block (Q4_K 9 chunks, Q5_K 11; a Q6_K block covers chunks 0 .. 13).
+// Source chunk of half window slot c in half h, counted from the window's base (Q4_K 9
+// chunks, Q5_K 11; a Q6_K block covers chunks 0 .. 13).
 template <int TY> __device__ __forceinline__ int gf_half_chunk(int c, int h) {
     if constexpr (TY == 12) return c == 0 ? 0 : c + 4 * h;
     else if constexpr (TY == 13) return c < 3 ? c : c + 4 * h;
@@ -497,6 +507,7 @@ __global__ void __launch_bounds__(GF_THREADS, 2) gf_step_kernel(GfGemm p) {
                 rs1 = gf_desc(mat1 - mis1, (p.w_bytes + mis1 + 15) & ~15ll);
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     constexpr int RAW = gf_half_raw<TY>(), NCH = gf_half_nch<TY>(), PB = GfType<TY>::PB;
+    constexpr uint32_t WA = TY == 14 ? 3u : 15u;  // a window's base: the dword (Q6_K) or 16 bytes at or below the block
     // a step's raw copies: 128 NCH chunks = 2 NCH wave instructions (ii = wave, wave + 8, ..)
     constexpr int RI = (2 * NCH + 7) / 8;
 
@@ -539,7 +550,7 @@ __global__ void __launch_bounds__(GF_THREADS, 2) gf_step_kernel(GfGemm p) {
         for (int i = 0; i < RI; ++i) {
             const int ii = wave + 8 * i;
             if (ii < 2 * NCH) {  // wave-uniform
-                const uint32_t voff = ((rg[i] + (uint32_t)pc * PB) & ~15u) + (h ? rc1[i] : rc0[i]);
+                const uint32_t voff = ((rg[i] + (uint32_t)pc * PB) & ~WA) + (h ? rc1[i] : rc0[i]);
                 gf_dma(GU && ii >= NCH ? rs1 : rs0, voff, ra + 1024u * (uint32_t)ii);
             }
         }
@@ -585,7 +596,7 @@ __global__ void __launch_bounds__(GF_THREADS, 2) gf_step_kernel(GfGemm p) {
     // read in step s - 1, is free for step s + 1's copies.
     issue(0);
     for (int pc = 0; pc < P; ++pc) {
-        const uint8_t* sbp = win + ((dg + (uint32_t)pc * PB) & 15u);  // the block's place in its window
+        const uint8_t* sbp = win + ((dg + (uint32_t)pc * PB) & WA);  // the block's place in its window
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
