@@ -271,7 +271,8 @@ __device__ __forceinline__ void gf_store_tile(const GfGemm& p, const GfEntry& en
                 make_float4(acc[t][4 * u], acc[t][4 * u + 1], acc[t][4 * u + 2], acc[t][4 * u + 3]);
     __syncthreads();
     if constexpr (GU) {
-        // h = act(gate, up) rounded once to bf16, 8 columns per thread
+        // h = act(gate, up) rounded once to bf16, 8 columns per thread (the sigmoid from
+        // v_exp_f32 and v_rcp_f32: 64 values per thread and tile, far below the bf16 rounding)
         const int hr = tid >> 3, hc = 8 * (tid & 7);
         if (hr < en.rows && n0 + hc < N) {
             const float* s0 = stage + hr * GF_SS + hc;
@@ -280,7 +281,7 @@ __device__ __forceinline__ void gf_store_tile(const GfGemm& p, const GfEntry& en
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float gv = s0[i] + s1[i], uv = s0[64 + i] + s1[64 + i];
-                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai(p.L, gv, uv) : gv * sigmoidf_(gv) * uv;
+                h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai_fast(p.L, gv, uv) : silu_mul_fast(gv, uv);
             }
             *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
                 make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
