@@ -1,6 +1,6 @@
 // Prefill side of the MoE path: expert-major grouping of (token, j) assignments and the
 // batched expert FFN over many tokens.
-#include "tsa_common.h"
+#include "fused_common.h"
 
 namespace tsa {
 int validate_layout(const tsa_expert_layout* L);
@@ -22,6 +22,17 @@ constexpr int GROUP_WAVES = GROUP_THREADS / 64;
 constexpr int MAX_GROUP_E = 1024;
 constexpr int GROUP_AHEAD = 8;  // id batches loaded ahead per wave
 
+// Optional tile table written by group_kernel (the grouped GGUF GEMMs' work list): per
+// resident expert in id order, entries of up to `rows` sorted rows {slot, first sorted row,
+// rows, 0}; n_entries[0] = their count.
+struct GroupTiles {
+    const int32_t* expert_slot;
+    int64_t n_slots;
+    int rows;
+    int* n_entries;
+    int4* table;
+};
+
 // LDS of group_kernel for E experts: per (wave, expert) counters, the experts' offsets, and
 // per (wave, expert) 64-bit lane masks (8-byte aligned).
 __host__ __device__ constexpr int group_lds_bytes(int E) { return ((GROUP_WAVES + 1) * E * 4 + 7) / 8 * 8 + GROUP_WAVES * E * 8; }
@@ -36,17 +47,32 @@ __host__ __device__ constexpr int group_lds_bytes(int E) { return ((GROUP_WAVES 
 // same expert: every lane ORs its bit into its wave's mask of the expert and reads the mask
 // back (LDS runs one wave's instructions in order), the lowest lane of each group then
 // clears the mask and advances the running rank. Every expert's run keeps assignment order
-// (token-major), as the reference's grouping does.
+// (token-major), as the reference's grouping does. With tiles.table set it also writes the
+// tile table between the passes (each thread two experts; the slots are loaded first).
 __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __restrict__ idx, int64_t n, int E,
                                                               int32_t* __restrict__ counts,
                                                               int32_t* __restrict__ offsets,
-                                                              int32_t* __restrict__ perm) {
+                                                              int32_t* __restrict__ perm, GroupTiles tiles) {
     extern __shared__ __align__(16) unsigned char gsm[];
     int* wcnt = reinterpret_cast<int*>(gsm);  // [wave][expert]
     int* eoff = wcnt + GROUP_WAVES * E;
     unsigned long long* wmask = reinterpret_cast<unsigned long long*>(gsm + ((GROUP_WAVES + 1) * E * 4 + 7) / 8 * 8);
+    __shared__ int wsum[16];
+    __shared__ int n_all;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const unsigned long long below = (1ull << lane) - 1ull;
+    static_assert(2 * GROUP_THREADS >= MAX_GROUP_E, "two experts per thread for the tile table");
+    int es[2] = {-1, -1};  // the tile table's experts 2 tid, 2 tid + 1: their slots, loaded early
+    if (tiles.table) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 2 * tid + i;
+            if (e < E) {
+                es[i] = tiles.expert_slot[e];
+                if (es[i] >= tiles.n_slots) es[i] = -1;
+            }
+        }
+    }
     for (int i = tid; i < GROUP_WAVES * E; i += GROUP_THREADS) {
         wcnt[i] = 0;
         wmask[i] = 0ull;
@@ -101,9 +127,32 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int32_t* __r
                 run += c;
             }
         }
-        if (lane == 63) offsets[E] = inc;
+        if (lane == 63) {
+            offsets[E] = inc;
+            n_all = inc;
+        }
     }
     __syncthreads();
+    if (tiles.table) {  // eoff holds the offsets; a count is the next offset minus its own
+        int c[2], nt[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 2 * tid + i;
+            c[i] = e < E && es[i] >= 0 ? (e + 1 < E ? eoff[e + 1] : n_all) - eoff[e] : 0;
+            nt[i] = (c[i] + tiles.rows - 1) / tiles.rows;
+        }
+        int total;
+        int first = block_incl_sum(nt[0] + nt[1], wsum, total) - nt[0] - nt[1];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 2 * tid + i;
+            for (int j = 0; j < nt[i]; ++j) {
+                const int r = c[i] - tiles.rows * j;
+                tiles.table[first++] = make_int4(es[i], eoff[e] + tiles.rows * j, r < tiles.rows ? r : tiles.rows, 0);
+            }
+        }
+        if (tid == 0) tiles.n_entries[0] = total;
+    }
     for (int64_t b0 = a0; b0 < a1; b0 += 64 * GROUP_AHEAD) {
         int ev[GROUP_AHEAD];
 #pragma unroll
@@ -139,12 +188,16 @@ __global__ void __launch_bounds__(256) map_slots_kernel(const int32_t* __restric
 
 }  // namespace
 
+// tile_rows > 0: also the tile table of the resident experts (table: int4 entries).
 int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
-                        hipStream_t stream) {
+                        hipStream_t stream, const int32_t* expert_slot, int64_t n_slots, int tile_rows,
+                        int* n_entries, void* table) {
     const int lds = group_lds_bytes(E);
     const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&group_kernel), lds);
     TSA_REQUIRE(e == hipSuccess, TSA_ERR_HIP, "hipFuncSetAttribute(LDS %d): %s", lds, hipGetErrorString(e));
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), lds, stream, idx, n, E, counts, offsets, perm);
+    const GroupTiles tiles{expert_slot, n_slots, tile_rows, n_entries, tile_rows > 0 ? static_cast<int4*>(table) : nullptr};
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), lds, stream, idx, n, E, counts, offsets, perm,
+                       tiles);
     TSA_LAUNCH_CHECK();
     return TSA_OK;
 }
@@ -161,7 +214,8 @@ extern "C" int tsa_group_by_expert(const int32_t* idx, int64_t T, int k, int64_t
                 MAX_GROUP_E);
     TSA_REQUIRE(T * k < (int64_t)1 << 31, TSA_ERR_SHAPE, "too many assignments");
     TSA_REQUIRE(idx && counts && offsets && (perm || T == 0), TSA_ERR_INVALID_ARG, "null pointer");
-    return launch_group_kernel(idx, T * k, (int)E, counts, offsets, perm, as_stream(stream));
+    return launch_group_kernel(idx, T * k, (int)E, counts, offsets, perm, as_stream(stream), nullptr, 0, 0, nullptr,
+                               nullptr);
 }
 
 // Workspace of the token-chunked decode path: the assignments' slots, then a decode workspace.

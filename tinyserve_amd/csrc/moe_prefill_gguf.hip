@@ -8,7 +8,7 @@
 // and never reach HBM.
 //
 // After group_kernel has sorted the (token, j) assignments expert-major, each resident
-// expert's run of sorted rows is cut into tiles of up to 64 rows (gf_table_kernel). Two
+// expert's run of sorted rows is cut into tiles of up to 64 rows (by group_kernel too). Two
 // launches then cover every (row tile, weight tile) pair, and a combine pass sums:
 //   gate_up: h[i, n] = act(x[token(i)] . W_g[n], x[token(i)] . W_u[n]), bf16, sorted order;
 //   down:    yk[a, n] = h[i] . W_d[n], bf16, by assignment a = perm[i];
@@ -46,7 +46,8 @@
 namespace tsa {
 
 int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
-                        hipStream_t stream);
+                        hipStream_t stream, const int32_t* expert_slot = nullptr, int64_t n_slots = 0,
+                        int tile_rows = 0, int* n_entries = nullptr, void* table = nullptr);
 int pf_combine(const uint16_t* yk, const int32_t* idx, const float* w, const int32_t* expert_slot, int64_t E,
                int64_t n_slots, int64_t T, int k, int H, void* y, int y_dtype, hipStream_t stream);
 
@@ -610,32 +611,6 @@ __global__ void __launch_bounds__(GF_THREADS, 2) gf_step_kernel(GfGemm p) {
     gf_store_tile<GU>(p, en, n0, acc, smem);
 }
 
-// Tiles of up to GF_BM sorted rows per resident expert: entry = (slot, first sorted row,
-// rows), experts in id order; n_entries[0] = the count. One workgroup, E <= 1024.
-__global__ void __launch_bounds__(1024) gf_table_kernel(const int32_t* __restrict__ counts,
-                                                        const int32_t* __restrict__ offsets,
-                                                        const int32_t* __restrict__ expert_slot, int E,
-                                                        int64_t n_slots, int* __restrict__ n_entries,
-                                                        GfEntry* __restrict__ table) {
-    __shared__ int wsum[16];
-    const int e = threadIdx.x;
-    int slot = -1, c = 0, o = 0;
-    if (e < E) {  // the three loads go out together
-        slot = expert_slot[e];
-        c = counts[e];
-        o = offsets[e];
-        if (slot < 0 || slot >= n_slots) c = 0;
-    }
-    const int nt = (c + GF_BM - 1) / GF_BM;
-    int total;
-    const int first = block_incl_sum(nt, wsum, total) - nt;
-    for (int i = 0; i < nt; ++i) {
-        const int r = c - GF_BM * i;
-        table[first + i] = GfEntry{slot, o + GF_BM * i, r < GF_BM ? r : GF_BM, 0};
-    }
-    if (e == 0) n_entries[0] = total;
-}
-
 template <int TY, bool GU, bool SD>
 const void* gf_fn() { return reinterpret_cast<const void*>(&gf_gemm_kernel<TY, GU, SD>); }
 
@@ -730,11 +705,9 @@ int gf_prefill(const tsa_expert_layout& L, const uint8_t* pool, int64_t n_slots,
     const int H = (int)L.hidden, I = (int)L.inter;
     const int64_t n = T * k;
 
-    int rc = launch_group_kernel(idx, n, (int)E, counts, offsets, perm, stream);
+    static_assert(sizeof(GfEntry) == 16, "the grouping kernel writes the tile table as int4 entries");
+    int rc = launch_group_kernel(idx, n, (int)E, counts, offsets, perm, stream, expert_slot, n_slots, GF_BM, nent, table);
     if (rc) return rc;
-    hipLaunchKernelGGL(gf_table_kernel, dim3(1), dim3(1024), 0, stream, counts, offsets, expert_slot, (int)E, n_slots,
-                       nent, table);
-    TSA_LAUNCH_CHECK();
 
     // a K-quant matrix whose K is a multiple of 256 takes gf_step_kernel; one whose K is not,
     // the straddling variant of gf_gemm_kernel; Q8_0 its plain variant

@@ -765,7 +765,8 @@ int64_t pf_mxt_workspace_bytes(const tsa_expert_layout& L, int64_t T, int k, int
 }
 
 int launch_group_kernel(const int32_t* idx, int64_t n, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
-                        hipStream_t stream);
+                        hipStream_t stream, const int32_t* expert_slot = nullptr, int64_t n_slots = 0,
+                        int tile_rows = 0, int* n_entries = nullptr, void* table = nullptr);
 
 // y[t] = sum_j w[t, j] yk[t k + j] over the live assignments, j in order (H % 8 == 0).
 int pf_combine(const uint16_t* yk, const int32_t* idx, const float* w, const int32_t* expert_slot, int64_t E,
