@@ -276,12 +276,21 @@ __device__ __forceinline__ void gf_store_tile(const GfGemm& p, const GfEntry& en
         // v_exp_f32 and v_rcp_f32: 64 values per thread and tile, far below the bf16 rounding)
         const int hr = tid >> 3, hc = 8 * (tid & 7);
         if (hr < en.rows && n0 + hc < N) {
-            const float* s0 = stage + hr * GF_SS + hc;
-            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
+            // 16-byte reads: the 16 lanes of a read (two rows 132 floats apart, eight column
+            // groups) then cover the 64 banks once; single floats put four lanes on a bank
+            const float4* s0 = reinterpret_cast<const float4*>(stage + hr * GF_SS + hc);
+            const float4* s1 = reinterpret_cast<const float4*>(stage + (GF_BM + hr) * GF_SS + hc);
+            float g8[8], u8[8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float4 a = s0[i], b = s1[i], c = s0[16 + i], d = s1[16 + i];  // +16 float4: the up rows
+                g8[4 * i] = a.x + b.x, g8[4 * i + 1] = a.y + b.y, g8[4 * i + 2] = a.z + b.z, g8[4 * i + 3] = a.w + b.w;
+                u8[4 * i] = c.x + d.x, u8[4 * i + 1] = c.y + d.y, u8[4 * i + 2] = c.z + d.z, u8[4 * i + 3] = c.w + d.w;
+            }
             float h[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float gv = s0[i] + s1[i], uv = s0[64 + i] + s1[64 + i];
+                const float gv = g8[i], uv = u8[i];
                 h[i] = p.L.act == TSA_ACT_SWIGLU_OAI ? swiglu_oai_fast(p.L, gv, uv) : silu_mul_fast(gv, uv);
             }
             *reinterpret_cast<uint4*>(p.out + (int64_t)(en.row0 + hr) * N + n0 + hc) =
@@ -293,11 +302,15 @@ __device__ __forceinline__ void gf_store_tile(const GfGemm& p, const GfEntry& en
         const int hr = tid >> 3, hc = 16 * (tid & 7);
         if (hr < en.rows && n0 + hc < N) {  // N % 16 == 0
             const int64_t a = p.perm[en.row0 + hr];
-            const float* s0 = stage + hr * GF_SS + hc;
-            const float* s1 = stage + (GF_BM + hr) * GF_SS + hc;
+            const float4* s0 = reinterpret_cast<const float4*>(stage + hr * GF_SS + hc);  // 16-byte reads, as above
+            const float4* s1 = reinterpret_cast<const float4*>(stage + (GF_BM + hr) * GF_SS + hc);
             uint32_t o[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = pack_bf16x2(s0[2 * i] + s1[2 * i], s0[2 * i + 1] + s1[2 * i + 1]);
+            for (int i = 0; i < 4; ++i) {
+                const float4 x = s0[i], y = s1[i];
+                o[2 * i] = pack_bf16x2(x.x + y.x, x.y + y.y);
+                o[2 * i + 1] = pack_bf16x2(x.z + y.z, x.w + y.w);
+            }
             uint4* dst = reinterpret_cast<uint4*>(p.out + a * N + n0 + hc);
             dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
             dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
