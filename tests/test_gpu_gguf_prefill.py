@@ -149,6 +149,22 @@ def test_gguf_grouped_prefill_missing_and_repeated_experts():
     assert_close_bf16(y, ref, "GGUF grouped prefill, missing / repeated experts")
 
 
+def test_gguf_grouped_prefill_many_expert_ids():
+    """640 expert ids (the grouping kernel's tile table takes two experts per thread past
+    512) over 32 resident slots, with every ninth id not resident: ids past 512 own tiles."""
+    rng = np.random.default_rng(13)
+    H, I, E, k, T = 256, 256, 640, 8, 96
+    L, experts, pool = _pool(rng, H, I, (13, 13, 14), 32)
+    es = np.array([-1 if e % 9 == 4 else e % 32 for e in range(E)], dtype=np.int32)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    idx[: T // 2, 0] = 600 + (np.arange(T // 2) % 40)  # ids past 512 in many rows
+    for t in range(T // 2):  # keep each token's ids distinct
+        if (idx[t, 1:] == idx[t, 0]).any():
+            idx[t, 1:][idx[t, 1:] == idx[t, 0]] = (idx[t, 0] + 1) % 512
+    y, ref = _run(L, experts, pool, rng, T, k, E, expert_slot=es, idx=idx, grouped=True)
+    assert_close_bf16(y, ref, "GGUF grouped prefill, 640 expert ids")
+
+
 def test_gguf_grouped_prefill_workload4_shapes_long_prompt():
     """Workload-4 expert shapes (Q5_K gate/up 2048 -> 768, Q6_K down), 128 experts, top-8 of
     256 tokens: 2048 assignments over the grouped tiles."""
